@@ -1,0 +1,110 @@
+"""ctypes binding of libkomp_hip.so (the C ABI declared in include/komp_abi.h).
+
+torch is imported first on purpose: it loads its own HIP runtime (soname libamdhip64.so.7), and the dynamic linker
+then binds this library to that same runtime, so torch's streams and device pointers are valid here.
+
+There is no fallback: if the library is missing or fails to load, every call raises KompError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (see the module docstring)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkomp_hip.so")
+
+KOMP_OK, KOMP_EINVAL, KOMP_EHIP = 0, 1, 2
+TIMING_KINDS = ("quant_q8_0", "quant_q8_K", "q4_0_gemv", "tq2_0_gemv", "probe")
+
+
+class KompError(RuntimeError):
+    """A call into the HIP library failed (or the library is not available)."""
+
+
+class KompArgumentError(KompError, ValueError):
+    """The HIP library rejected an argument (shape, stride, alignment, knob or mode)."""
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+
+# name -> (restype, argtypes); exactly the functions include/komp_abi.h declares
+SIGNATURES = {
+    "komp_abi_version": (_INT, []),
+    "komp_last_error": (ctypes.c_char_p, []),
+    "komp_quant_q8_0": (_INT, [_P, _P, _P, _I64, _I64, _INT, _P]),
+    "komp_quant_q8_K": (_INT, [_P, _P, _P, _P, _I64, _I64, _P]),
+    "komp_q4_0_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_tq2_0_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_gemv_auto_config": (_INT, [_INT, _I64, _I64, _I64, _P, _P, _P]),
+    "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
+    "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),
+    "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
+    "komp_timing_begin": (_INT, [_I64]),
+    "komp_timing_end": (_INT, [_P, _P]),
+}
+ABI_VERSION = 1
+
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded once).  Raises KompError if it is missing or incompatible."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise KompError(f"{LIB_PATH} is not built: run `python -m comp_amd.build` (hipcc, gfx950)")
+    try:
+        handle = ctypes.CDLL(LIB_PATH)
+    except OSError as e:
+        raise KompError(f"cannot load {LIB_PATH}: {e}") from e
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    v = handle.komp_abi_version()
+    if v != ABI_VERSION:
+        raise KompError(f"{LIB_PATH}: ABI version {v}, expected {ABI_VERSION}; rebuild it")
+    _lib = handle
+    return _lib
+
+
+def last_error():
+    return lib().komp_last_error().decode(errors="replace")
+
+
+def check(status, what):
+    if status == KOMP_OK:
+        return
+    msg = last_error() or f"{what}: status {status}"
+    if status == KOMP_EINVAL:
+        raise KompArgumentError(msg)
+    raise KompError(msg)
+
+
+def call(name, *args):
+    """Call an ABI function and raise on a nonzero status."""
+    check(getattr(lib(), name)(*args), name)
+
+
+def auto_config(fmt_id, m, n, k):
+    bn, nb, nw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    call("komp_gemv_auto_config", fmt_id, m, n, k, ctypes.byref(bn), ctypes.byref(nb), ctypes.byref(nw))
+    return bn.value, nb.value, nw.value
+
+
+def timing_begin(max_dispatches=1 << 16):
+    call("komp_timing_begin", max_dispatches)
+
+
+def timing_end():
+    """-> {kind: (total_ms, dispatches)} for the dispatches since timing_begin()."""
+    ms = (ctypes.c_double * len(TIMING_KINDS))()
+    cnt = (ctypes.c_int64 * len(TIMING_KINDS))()
+    call("komp_timing_end", ms, cnt)
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(TIMING_KINDS)}

@@ -1,0 +1,292 @@
+// extern "C" entry points of libkomp_hip.so (declared in include/komp_abi.h): argument validation, the mapping of
+// the reference's tune knobs to a launch plan, column chunking, and the dispatch timing of the tuning harness.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/komp_abi.h"
+#include "komp_internal.h"
+
+namespace komp {
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return KOMP_OK;
+  return fail(KOMP_EHIP, "%s: HIP error %d (%s)", what, static_cast<int>(e), hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+bool in_set(int v, const int* set, int n) {
+  for (int i = 0; i < n; ++i)
+    if (set[i] == v) return true;
+  return false;
+}
+
+const int kBlockN[] = {8, 16, 32, 64, 128};
+const int kNb[] = {1, 2, 4, 8, 16};
+const int kWarps[] = {1, 2, 4, 8};
+constexpr size_t kLdsMax = 160 * 1024;
+
+// ---- dispatch timing ------------------------------------------------------------------------------------------------
+struct TimingState {
+  std::mutex mu;
+  std::atomic<bool> on{false};
+  int64_t max = 0;
+  int64_t used = 0;
+  std::vector<hipEvent_t> events;  // pairs (start, stop)
+  std::vector<int> kinds;
+};
+TimingState g_timing;
+
+// ---- auto plan ------------------------------------------------------------------------------------------------------
+// Pick (block_n, nb, num_warps) for a shape: cover each row's blocks in as few K steps as possible with little idle
+// slot width, then size workgroups so the grid has enough of them to fill 256 CUs.
+void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warps) {
+  const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
+  double best = -1e30;
+  int best_lpr = 16, best_nb = 8;
+  for (int lpr = 64; lpr >= 4; lpr >>= 1) {
+    for (int cand_nb = 8; cand_nb >= 1; cand_nb >>= 1) {
+      const int64_t slots = (fmt == FMT_Q4_0 ? lpr : lpr / 4) * static_cast<int64_t>(cand_nb);  // blocks per K step
+      const int64_t steps = nblk > 0 ? (nblk + slots - 1) / slots : 1;
+      const double util = nblk > 0 ? static_cast<double>(nblk) / static_cast<double>(steps * slots) : 1.0;
+      const double score = util - 0.02 * static_cast<double>(steps) - (cand_nb < 4 ? 0.05 : 0.0);
+      if (score > best + 1e-9) {
+        best = score;
+        best_lpr = lpr;
+        best_nb = cand_nb;
+      }
+    }
+  }
+  const int rpw = 64 / best_lpr;
+  int w = 8;
+  while (w > 1) {
+    const int64_t bn = static_cast<int64_t>(w) * rpw;
+    const int64_t grid = (n + bn - 1) / bn;
+    if (bn <= 128 && grid >= 512) break;
+    if (bn / 2 < 8) break;  // block_n must stay >= 8
+    w >>= 1;
+  }
+  while (w * rpw > 128) w >>= 1;
+  while (w * rpw < 8) w <<= 1;
+  *block_n = w * rpw;
+  *nb = best_nb;
+  *warps = w;
+}
+
+int gemv_entry(int fmt, const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y,
+               int32_t* S, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+               void* stream) {
+  const char* name = fmt == FMT_Q4_0 ? "komp_q4_0_gemv" : "komp_tq2_0_gemv";
+  const int blk = fmt == FMT_Q4_0 ? 32 : 256;
+  const int64_t row_bytes = fmt == FMT_Q4_0 ? K / 2 : K / 4;
+  if (M < 0 || N < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (M=%lld N=%lld K=%lld)", name,
+                                          (long long)M, (long long)N, (long long)K);
+  if (N > INT32_MAX || K > INT32_MAX) return fail(KOMP_EINVAL, "%s: N and K must be < 2^31", name);
+  if (K % blk) return fail(KOMP_EINVAL, "%s: K=%lld is not a multiple of the %d-value block", name, (long long)K, blk);
+  if (SW < row_bytes || SW % 16)
+    return fail(KOMP_EINVAL, "%s: SW=%lld must be a multiple of 16 and >= %lld (the quant bytes of a row)", name,
+                (long long)SW, (long long)row_bytes);
+  if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A) return fail(KOMP_EINVAL, "%s: mode=%d not in {0,1,2}", name, mode);
+  if (block_n == 0) {
+    auto_config(fmt, N, K, &block_n, &nb, &num_warps);
+  } else {
+    if (!in_set(block_n, kBlockN, 5)) return fail(KOMP_EINVAL, "%s: block_n=%d not in {8,16,32,64,128}", name, block_n);
+    if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
+    if (!in_set(num_warps, kWarps, 4)) return fail(KOMP_EINVAL, "%s: num_warps=%d not in {1,2,4,8}", name, num_warps);
+  }
+  if (M == 0 || N == 0) return KOMP_OK;
+  if (K > 0 && (WQ == nullptr || WS == nullptr || XQ == nullptr || XD == nullptr))
+    return fail(KOMP_EINVAL, "%s: WQ, WS, XQ and XD must not be NULL", name);
+  if (Y == nullptr) return fail(KOMP_EINVAL, "%s: Y must not be NULL", name);
+  if (!aligned(WQ, 16) || !aligned(XQ, 16)) return fail(KOMP_EINVAL, "%s: WQ and XQ must be 16-byte aligned", name);
+  if (!aligned(WS, 2) || !aligned(XD, 4) || !aligned(Y, 4) || !aligned(S, 4))
+    return fail(KOMP_EINVAL, "%s: WS, XD, Y and S must be aligned to their element size", name);
+  int mc = static_cast<int>(M < 3 ? M : 3);
+  while (mc > 1 && gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax) --mc;
+  if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
+    return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
+
+  GemvPlan plan;
+  plan.block_n = block_n;
+  plan.nb = nb;
+  plan.waves = num_warps;
+  const int rpw = block_n / num_warps;
+  const int rpp = rpw < 16 ? rpw : 16;
+  plan.lpr_log2 = 0;
+  while ((64 >> plan.lpr_log2) > rpp) ++plan.lpr_log2;
+  plan.passes = rpw / rpp;
+
+  const int64_t nblk = K / blk;
+  for (int64_t m0 = 0; m0 < M; m0 += mc) {
+    GemvCall c;
+    c.fmt = fmt;
+    c.wq = WQ;
+    c.ws = WS;
+    c.xq = XQ + m0 * K;
+    c.xd = XD + m0 * nblk;
+    c.y = Y + m0 * N;
+    c.s = S != nullptr ? S + m0 * N * nblk : nullptr;
+    c.m = static_cast<int>(M - m0 < mc ? M - m0 : mc);
+    c.n = static_cast<int>(N);
+    c.k = static_cast<int>(K);
+    c.sw = SW;
+    c.n_total = static_cast<int>(N);
+    c.mode = mode;
+    c.nontemporal = 0;
+    const int st = hip_status(launch_gemv(c, plan, static_cast<hipStream_t>(stream)), name);
+    if (st != KOMP_OK) return st;
+  }
+  return KOMP_OK;
+}
+
+}  // namespace
+
+Timing timing_slot(int kind) {
+  Timing t{false, nullptr, nullptr};
+  if (!g_timing.on.load(std::memory_order_relaxed)) return t;
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  if (!g_timing.on || g_timing.used >= g_timing.max) return t;
+  const size_t i = static_cast<size_t>(g_timing.used);
+  while (g_timing.events.size() < 2 * (i + 1)) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return t;
+    g_timing.events.push_back(e);
+  }
+  if (g_timing.kinds.size() <= i) g_timing.kinds.resize(i + 1);
+  g_timing.kinds[i] = kind;
+  g_timing.used++;
+  t.on = true;
+  t.start = g_timing.events[2 * i];
+  t.stop = g_timing.events[2 * i + 1];
+  return t;
+}
+
+}  // namespace komp
+
+using namespace komp;
+
+extern "C" {
+
+int komp_abi_version(void) { return KOMP_ABI_VERSION; }
+
+const char* komp_last_error(void) { return g_error.c_str(); }
+
+int komp_quant_q8_0(const float* X, int8_t* XQ, float* XD, int64_t M, int64_t K, int bb, void* stream) {
+  if (M < 0 || K < 0) return fail(KOMP_EINVAL, "komp_quant_q8_0: negative size");
+  if (K % 32) return fail(KOMP_EINVAL, "komp_quant_q8_0: K=%lld is not a multiple of 32", (long long)K);
+  if (bb < 1) return fail(KOMP_EINVAL, "komp_quant_q8_0: bb=%d must be >= 1", bb);
+  const int64_t nblocks = M * (K / 32);
+  if (nblocks == 0) return KOMP_OK;
+  if (X == nullptr || XQ == nullptr || XD == nullptr) return fail(KOMP_EINVAL, "komp_quant_q8_0: NULL pointer");
+  if (!aligned(X, 16) || !aligned(XQ, 4) || !aligned(XD, 4))
+    return fail(KOMP_EINVAL, "komp_quant_q8_0: X must be 16-byte aligned, XQ and XD 4-byte aligned");
+  return hip_status(launch_quant_q8_0(X, XQ, XD, nblocks, static_cast<hipStream_t>(stream)), "komp_quant_q8_0");
+}
+
+int komp_quant_q8_K(const float* X, int8_t* XQ, float* XD, int16_t* XB, int64_t M, int64_t K, void* stream) {
+  if (M < 0 || K < 0) return fail(KOMP_EINVAL, "komp_quant_q8_K: negative size");
+  if (K % 256) return fail(KOMP_EINVAL, "komp_quant_q8_K: K=%lld is not a multiple of 256", (long long)K);
+  const int64_t nblocks = M * (K / 256);
+  if (nblocks == 0) return KOMP_OK;
+  if (X == nullptr || XQ == nullptr || XD == nullptr) return fail(KOMP_EINVAL, "komp_quant_q8_K: NULL pointer");
+  if (!aligned(X, 16) || !aligned(XQ, 4) || !aligned(XD, 4) || !aligned(XB, 2))
+    return fail(KOMP_EINVAL, "komp_quant_q8_K: X must be 16-byte aligned, XQ and XD 4-byte, XB 2-byte aligned");
+  return hip_status(launch_quant_q8_K(X, XQ, XD, XB, nblocks, static_cast<hipStream_t>(stream)), "komp_quant_q8_K");
+}
+
+int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                   void* stream) {
+  return gemv_entry(FMT_Q4_0, WQ, WS, XQ, XD, Y, S, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                    void* stream) {
+  return gemv_entry(FMT_TQ2_0, WQ, WS, XQ, XD, Y, S, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_gemv_auto_config(int fmt, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps) {
+  (void)M;
+  if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
+  if (N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)
+    return fail(KOMP_EINVAL, "komp_gemv_auto_config: bad argument");
+  auto_config(fmt, N, K, block_n, nb, num_warps);
+  return KOMP_OK;
+}
+
+int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,
+                    void* stream) {
+  if (n < 0) return fail(KOMP_EINVAL, "komp_dp4a_probe: negative n");
+  if (mode != KOMP_MODE_DP4A && mode != KOMP_MODE_DP4A_EMU)
+    return fail(KOMP_EINVAL, "komp_dp4a_probe: mode=%d must be 1 (emulated) or 2 (v_dot4c_i32_i8)", mode);
+  if (n == 0) return KOMP_OK;
+  if (!A || !B || !C || !OUT) return fail(KOMP_EINVAL, "komp_dp4a_probe: NULL pointer");
+  return hip_status(launch_dp4a_probe(A, B, C, OUT, n, mode, static_cast<hipStream_t>(stream)), "komp_dp4a_probe");
+}
+
+int komp_q4_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t R, void* stream) {
+  if (R < 0) return fail(KOMP_EINVAL, "komp_q4_0_decode: negative R");
+  if (R == 0) return KOMP_OK;
+  if (!WQ || !OUT || !aligned(WQ, 16)) return fail(KOMP_EINVAL, "komp_q4_0_decode: WQ must be 16-byte aligned");
+  return hip_status(launch_q4_0_decode(WQ, OUT, R, static_cast<hipStream_t>(stream)), "komp_q4_0_decode");
+}
+
+int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* stream) {
+  if (nblk < 0) return fail(KOMP_EINVAL, "komp_tq2_0_decode: negative nblk");
+  if (nblk == 0) return KOMP_OK;
+  if (!WQ || !OUT || !aligned(WQ, 16)) return fail(KOMP_EINVAL, "komp_tq2_0_decode: WQ must be 16-byte aligned");
+  return hip_status(launch_tq2_0_decode(WQ, OUT, nblk, static_cast<hipStream_t>(stream)), "komp_tq2_0_decode");
+}
+
+int komp_timing_begin(int64_t max_dispatches) {
+  if (max_dispatches < 0) return fail(KOMP_EINVAL, "komp_timing_begin: negative max_dispatches");
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  g_timing.max = max_dispatches;
+  g_timing.used = 0;
+  g_timing.on = true;
+  return KOMP_OK;
+}
+
+int komp_timing_end(double* ms, int64_t* count) {
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  g_timing.on = false;
+  for (int i = 0; i < KOMP_TIMING_KINDS; ++i) {
+    if (ms) ms[i] = 0.0;
+    if (count) count[i] = 0;
+  }
+  for (int64_t i = 0; i < g_timing.used; ++i) {
+    hipEvent_t e0 = g_timing.events[2 * i], e1 = g_timing.events[2 * i + 1];
+    hipError_t e = hipEventSynchronize(e1);
+    if (e != hipSuccess) return hip_status(e, "komp_timing_end");
+    float t = 0.0f;
+    e = hipEventElapsedTime(&t, e0, e1);
+    if (e != hipSuccess) return hip_status(e, "komp_timing_end");
+    const int kd = g_timing.kinds[i];
+    if (ms) ms[kd] += t;
+    if (count) count[kd] += 1;
+  }
+  g_timing.used = 0;
+  return KOMP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Internal (C++) interface between the C-ABI layer (komp_abi.cpp) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace komp {
+
+enum Fmt { FMT_Q4_0 = 0, FMT_TQ2_0 = 1 };
+
+// Kernel kinds, for the per-dispatch timing of the tuning harness.
+enum Kind { KIND_QUANT_Q8_0 = 0, KIND_QUANT_Q8_K = 1, KIND_Q4_0_GEMV = 2, KIND_TQ2_0_GEMV = 3, KIND_PROBE = 4, KIND_COUNT = 5 };
+
+// Work decomposition of one GEMV launch (see gemv.hip for the mapping of block_n / nb / num_warps).
+struct GemvPlan {
+  int block_n;    // rows per workgroup
+  int nb;         // 16-byte weight chunks each lane loads per row per K step
+  int waves;      // wavefronts per workgroup
+  int lpr_log2;   // log2(lanes per row group)
+  int passes;     // row groups each wave walks in sequence
+};
+
+struct GemvCall {
+  int fmt;
+  const uint8_t* wq;
+  const int16_t* ws;
+  const int8_t* xq;
+  const float* xd;
+  float* y;
+  int32_t* s;
+  int m;          // activation columns in this launch (1..3)
+  int n;
+  int k;
+  int64_t sw;     // WQ row stride in bytes
+  int n_total;    // rows of the full Y / S planes (S offsets use it)
+  int mode;
+  int nontemporal;
+};
+
+// Dispatch hook: every launch goes through it so the tuning harness can time dispatches with hipExtLaunchKernel events.
+struct Timing {
+  bool on;
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+Timing timing_slot(int kind);   // defined in komp_abi.cpp
+
+size_t gemv_lds_bytes(int fmt, int m, int k);
+hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
+hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
+hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,
+                             hipStream_t stream);
+hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream);
+hipError_t launch_tq2_0_decode(const uint8_t* wq, int32_t* out, int64_t nblk, hipStream_t stream);
+
+}  // namespace komp

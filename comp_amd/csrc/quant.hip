@@ -1,0 +1,173 @@
+// Activation quantizers (q8_0, q8_K) and the probe kernels, for gfx950.
+//
+// Replaces src/komp/kernels.py:22-45 (quant_q8_0, quant_q8_K) and :145-170 (dp4a_probe, q4_0_decode, tq2_0_decode).
+// The arithmetic is ggml's reference quantizers as restated in patches/0001-language-extra-kurn.patch:104-131, with
+// correctly rounded f32 division (v_div_scale/fmas/fixup, never a bare v_rcp_f32), f32 denormals preserved, and
+// round-to-nearest-even f32 -> f16 conversion; so the bytes equal the reference's bytes exactly.
+#include <hip/hip_ext.h>
+
+#include "komp_device.h"
+#include "komp_internal.h"
+
+namespace komp {
+namespace {
+
+constexpr int QUANT_THREADS = 256;
+
+// q8_0: 8 lanes per block of 32 (4 values each, one 16-byte load), 32 blocks per 256-lane workgroup.
+__global__ void __launch_bounds__(QUANT_THREADS)
+quant_q8_0_kernel(const float* __restrict__ X, int8_t* __restrict__ XQ, float* __restrict__ XD, int64_t nblocks) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * QUANT_THREADS + threadIdx.x;
+  const int64_t blk = gid >> 3;
+  const bool valid = blk < nblocks;
+  f32x4 v = valid ? reinterpret_cast<const f32x4*>(X)[gid] : f32x4{0.f, 0.f, 0.f, 0.f};
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
+  const float d = a / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  unsigned packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int qv = static_cast<int>(round_half_away(v[e] * id));
+    packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
+  }
+  if (valid) {
+    reinterpret_cast<unsigned*>(XQ)[gid] = packed;
+    if ((gid & 7) == 0) XD[blk] = __half2float(__float2half_rn(d));
+  }
+}
+
+// q8_K: one wavefront per block of 256 (4 values per lane), 4 blocks per workgroup.  bsums (XB) are optional.
+__global__ void __launch_bounds__(QUANT_THREADS)
+quant_q8_K_kernel(const float* __restrict__ X, int8_t* __restrict__ XQ, float* __restrict__ XD,
+                  int16_t* __restrict__ XB, int64_t nblocks) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * QUANT_THREADS + threadIdx.x;
+  const int64_t blk = gid >> 6;
+  if (blk >= nblocks) return;  // whole wavefronts leave together: a wavefront is one block
+  const int lane = threadIdx.x & 63;
+  const f32x4 v = reinterpret_cast<const f32x4*>(X)[gid];
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_MIRROR>(a));
+  a = fmaxf(a, __shfl_xor(a, 16, 64));
+  const float amax = fmaxf(a, __shfl_xor(a, 32, 64));
+  // first index whose |x| equals amax (patch:124)
+  int first = 256;
+#pragma unroll
+  for (int e = 3; e >= 0; --e) first = fabsf(v[e]) == amax ? lane * 4 + e : first;
+  first = min(first, __shfl_xor(first, 1, 64));
+  first = min(first, __shfl_xor(first, 2, 64));
+  first = min(first, __shfl_xor(first, 4, 64));
+  first = min(first, __shfl_xor(first, 8, 64));
+  first = min(first, __shfl_xor(first, 16, 64));
+  first = min(first, __shfl_xor(first, 32, 64));
+  const int fe = first & 3;
+  const float mine = fe == 0 ? v[0] : fe == 1 ? v[1] : fe == 2 ? v[2] : v[3];
+  const float mx = __shfl(mine, (first >> 2) & 63, 64);
+  const bool nz = amax != 0.0f;
+  const float iscale = -127.0f / (nz ? mx : 1.0f);
+  unsigned packed = 0;
+  int bsum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int qv = nz ? static_cast<int>(fminf(rintf(iscale * v[e]), 127.0f)) : 0;
+    bsum += qv;
+    packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
+  }
+  reinterpret_cast<unsigned*>(XQ)[gid] = packed;
+  bsum = group_sum(bsum, 4);
+  if (XB != nullptr && (lane & 3) == 0) XB[blk * 16 + (lane >> 2)] = static_cast<int16_t>(bsum);
+  if (lane == 0) XD[blk] = nz ? 1.0f / iscale : 0.0f;
+}
+
+__global__ void dp4a_probe_kernel(const int32_t* __restrict__ A, const int32_t* __restrict__ B,
+                                  const int32_t* __restrict__ C, int32_t* __restrict__ OUT, int64_t n, int mode) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const unsigned a = static_cast<unsigned>(A[i]);
+  const unsigned b = static_cast<unsigned>(B[i]);
+  OUT[i] = mode == MODE_DP4A ? dot4<MODE_DP4A>(a, b, C[i]) : dot4<MODE_DP4A_EMU>(a, b, C[i]);
+}
+
+// [R][16] q4_0 quant bytes -> [R][32] int32 values, through the GEMV's packed-word nibble split.
+__global__ void q4_0_decode_kernel(const uint8_t* __restrict__ WQ, int32_t* __restrict__ OUT, int64_t rows) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const u32x4 w = reinterpret_cast<const u32x4*>(WQ)[r];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const unsigned lo = w[d] & 0x0F0F0F0Fu;
+    const unsigned hi = (w[d] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      OUT[r * 32 + 4 * d + e] = static_cast<int>((lo >> (8 * e)) & 0xFFu) - 8;
+      OUT[r * 32 + 16 + 4 * d + e] = static_cast<int>((hi >> (8 * e)) & 0xFFu) - 8;
+    }
+  }
+}
+
+// [NBLK][64] tq2_0 quant bytes -> [NBLK][256] int32 values, through the GEMV's packed-word crumb split.
+__global__ void tq2_0_decode_kernel(const uint8_t* __restrict__ WQ, int32_t* __restrict__ OUT, int64_t nblk) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // one 16-byte chunk per lane
+  if (gid >= nblk * 4) return;
+  const int64_t b = gid >> 2;
+  const int q = static_cast<int>(gid & 3);
+  const u32x4 w = reinterpret_cast<const u32x4*>(WQ)[gid];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const unsigned c = (w[d] >> (2 * j)) & 0x03030303u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // chunk q: h = q / 2, i = 16 * (q % 2) + 4d + e; value h*128 + j*32 + i
+        const int v = (q >> 1) * 128 + j * 32 + 16 * (q & 1) + 4 * d + e;
+        OUT[b * 256 + v] = static_cast<int>((c >> (8 * e)) & 0xFFu) - 1;
+      }
+    }
+  }
+}
+
+template <typename F, typename... Args>
+hipError_t launch(int kind, F kern, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+  const Timing tm = timing_slot(kind);
+  if (tm.on) {
+    hipExtLaunchKernelGGL(kern, grid, block, 0, stream, tm.start, tm.stop, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, 0, stream, args...);
+  }
+  return hipGetLastError();
+}
+
+unsigned blocks_for(int64_t threads, int per) { return static_cast<unsigned>((threads + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream) {
+  return launch(KIND_QUANT_Q8_0, quant_q8_0_kernel, dim3(blocks_for(nblocks * 8, QUANT_THREADS)), dim3(QUANT_THREADS),
+                stream, x, xq, xd, nblocks);
+}
+
+hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream) {
+  return launch(KIND_QUANT_Q8_K, quant_q8_K_kernel, dim3(blocks_for(nblocks * 64, QUANT_THREADS)),
+                dim3(QUANT_THREADS), stream, x, xq, xd, xb, nblocks);
+}
+
+hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,
+                             hipStream_t stream) {
+  return launch(KIND_PROBE, dp4a_probe_kernel, dim3(blocks_for(n, 256)), dim3(256), stream, a, b, c, out, n, mode);
+}
+
+hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream) {
+  return launch(KIND_PROBE, q4_0_decode_kernel, dim3(blocks_for(rows, 64)), dim3(64), stream, wq, out, rows);
+}
+
+hipError_t launch_tq2_0_decode(const uint8_t* wq, int32_t* out, int64_t nblk, hipStream_t stream) {
+  return launch(KIND_PROBE, tq2_0_decode_kernel, dim3(blocks_for(nblk * 4, 64)), dim3(64), stream, wq, out, nblk);
+}
+
+}  // namespace komp

@@ -1,0 +1,214 @@
+"""Host side of the decode path: KURN split layouts from ggml blocks, and the quantizer / GEMV launches.
+
+Same surface as the reference's operator boundary src/komp/host.py:1-85 (FORMATS, MODES, split, split_q4_0,
+tq2_0_qplane, q8_0_blocks, q8_K_blocks, act_blocks, device, quantize, gemv), with the same argument meaning.  The
+launches go to hand-written gfx950 HIP kernels through the C ABI (comp_amd._abi), on the current torch stream, with
+no synchronisation inside.
+
+Differences a caller can observe:
+  * quantize / gemv need tensors on a HIP device (like any compiled Triton kernel); there is no CPU path, and the
+    call raises if the HIP library is not built.
+  * mode 1 runs the packed-word dot products emulated with shifts and multiplies and mode 2 on v_dot4c_i32_i8 (the
+    reference's mode 1 is its pure-Triton fallback, mode 2 inline PTX); all modes give identical int32 dots.
+  * quantize(..., bsums=True) also returns the q8_K bsums, computed by the kernel.
+  * gemv(..., block_n=None) lets the library choose block_n / nb / num_warps for the shape.
+  * arguments the kernels cannot take (K not a multiple of the block, misaligned or strided planes, unknown knobs)
+    raise KompArgumentError (a ValueError) instead of reading out of bounds.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _abi
+
+FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale offset, activation format
+    "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
+    "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
+}
+MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
+FMT_ID = {"q4_0": 0, "tq2_0": 1}
+
+
+def split(fmt, W, n, k):
+    """ggml blocks (bytes, n rows) -> (WQ uint8 [n][quant bytes per row], WS int16 [n][blocks]): KURN's split planes.
+
+    src/komp/host.py:16-22."""
+    f = FORMATS[fmt]
+    nb = k // f["block"]
+    blocks = np.frombuffer(W, dtype=np.uint8).reshape(n, nb, f["nbytes"])
+    wq = blocks[:, :, f["qoff"] : f["qoff"] + f["qbytes"]].reshape(n, nb * f["qbytes"]).copy()
+    ws = blocks[:, :, f["soff"] : f["soff"] + 2].copy().view(np.int16).reshape(n, nb)
+    return wq, ws
+
+
+def split_q4_0(W, n, k):
+    return split("q4_0", W, n, k)
+
+
+def tq2_0_qplane(W, nblk):
+    """ggml tq2_0 blocks -> the quant plane [nblk][64] (the f16 d goes to the scale plane).  src/komp/host.py:29-31."""
+    return np.frombuffer(W, dtype=np.uint8).reshape(nblk, 66)[:, :64].copy()
+
+
+def _np(a):
+    return a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+
+
+def q8_0_blocks(xq, xd):
+    """q8_0 split planes -> ggml q8_0 blocks (bytes): f16 d then 32 int8 per block.  src/komp/host.py:34-40."""
+    xq, xd = _np(xq), _np(xd)
+    m, k = xq.shape
+    nb = k // 32
+    out = np.empty((m, nb, 34), dtype=np.uint8)
+    out[:, :, 0:2] = np.asarray(xd, np.float32).astype(np.float16).view(np.uint8).reshape(m, nb, 2)
+    out[:, :, 2:34] = np.asarray(xq, np.int8).view(np.uint8).reshape(m, nb, 32)
+    return out.tobytes()
+
+
+def q8_K_blocks(xq, xd, xb=None):
+    """q8_K split planes (numpy) -> ggml q8_K blocks (bytes): f32 d, 256 int8, 16 int16 bsums.
+
+    src/komp/host.py:43-52; the bsums come from `xb` (the kernel's) when given, else from xq."""
+    xq, xd = _np(xq), _np(xd)
+    xb = None if xb is None else _np(xb)
+    m, k = xq.shape
+    nb = k // 256
+    out = np.empty((m, nb, 292), dtype=np.uint8)
+    out[:, :, 0:4] = np.asarray(xd, np.float32).view(np.uint8).reshape(m, nb, 4)
+    out[:, :, 4:260] = np.asarray(xq, np.int8).view(np.uint8).reshape(m, nb, 256)
+    if xb is None:
+        xb = np.asarray(xq, np.int8).astype(np.int32).reshape(m, nb, 16, 16).sum(axis=3).astype(np.int16)
+    out[:, :, 260:292] = np.asarray(xb, np.int16).view(np.uint8).reshape(m, nb, 32)
+    return out.tobytes()
+
+
+def act_blocks(fmt, xq, xd, xb=None):
+    if FORMATS[fmt]["act"] == "q8_0":
+        return q8_0_blocks(xq, xd)
+    return q8_K_blocks(xq, xd, xb)
+
+
+def device():
+    return "cuda" if torch.cuda.is_available() else "cpu"
+
+
+def _stream(t):
+    return ctypes_stream(t.device)
+
+
+def ctypes_stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _need(t, name, dtype, ndim=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise _abi.KompArgumentError(f"{name} is on {t.device}: the decode path runs on a HIP device only")
+    if t.dtype != dtype:
+        raise _abi.KompArgumentError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise _abi.KompArgumentError(f"{name} must have {ndim} dimensions, got shape {tuple(t.shape)}")
+
+
+def quantize(fmt, x, bb=4, bsums=False):
+    """f32 [M][K] tensor -> (XQ int8 [M][K], XD f32 [M][K/block]) with the q8_0 / q8_K quantizer kernel.
+
+    src/komp/host.py:63-73.  With bsums=True (q8_K only) also returns XB int16 [M][K/16]."""
+    act = FORMATS[fmt]["act"]
+    _need(x, "x", torch.float32, 2)
+    x = x.contiguous()
+    m, k = x.shape
+    blk = 32 if act == "q8_0" else 256
+    if k % blk:
+        raise _abi.KompArgumentError(f"quantize {fmt}: K={k} is not a multiple of {blk}")
+    xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    xd = torch.empty((m, k // blk), dtype=torch.float32, device=x.device)
+    s = _stream(x)
+    with torch.cuda.device(x.device):
+        if act == "q8_0":
+            if bsums:
+                raise _abi.KompArgumentError("bsums are a q8_K field; q8_0 has none")
+            _abi.call("komp_quant_q8_0", x.data_ptr(), xq.data_ptr(), xd.data_ptr(), m, k, bb, s)
+            return xq, xd
+        xb = torch.empty((m, k // 16), dtype=torch.int16, device=x.device) if bsums else None
+        _abi.call("komp_quant_q8_K", x.data_ptr(), xq.data_ptr(), xd.data_ptr(), xb.data_ptr() if bsums else None, m,
+                  k, s)  # fmt: skip
+    return (xq, xd, xb) if bsums else (xq, xd)
+
+
+def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store_s=False):
+    """-> (Y f32 [M][N], S int32 [M][N][blocks] or None).  mode: 0 bytes, 1 dp4a emulated, 2 dp4a (v_dot4c_i32_i8).
+
+    src/komp/host.py:76-85.  block_n=None lets the library choose block_n, nb and num_warps for the shape."""
+    f = FORMATS[fmt]
+    _need(wq, "wq", torch.uint8, 2)
+    _need(ws, "ws", torch.int16, 2)
+    _need(xq, "xq", torch.int8, 2)
+    _need(xd, "xd", torch.float32, 2)
+    if wq.stride(1) != 1:
+        raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
+    nblk = k // f["block"]
+    if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{nblk}] plane, got {tuple(ws.shape)}")
+    if wq.shape[0] != n or wq.shape[1] < nblk * f["qbytes"]:
+        raise _abi.KompArgumentError(f"wq must be [{n}][>= {nblk * f['qbytes']}], got {tuple(wq.shape)}")
+    m = xq.shape[0]
+    if tuple(xq.shape) != (m, k) or not xq.is_contiguous():
+        raise _abi.KompArgumentError(f"xq must be a contiguous [M][{k}] plane, got {tuple(xq.shape)}")
+    if tuple(xd.shape) != (m, nblk) or not xd.is_contiguous():
+        raise _abi.KompArgumentError(f"xd must be a contiguous [{m}][{nblk}] plane, got {tuple(xd.shape)}")
+    dev = xq.device
+    for t, name in ((wq, "wq"), (ws, "ws"), (xd, "xd")):
+        if t.device != dev:
+            raise _abi.KompArgumentError(f"{name} is on {t.device}, xq on {dev}")
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=dev) if store_s else None
+    if block_n is None:
+        block_n, nb, num_warps = 0, 0, 0
+    fn = "komp_q4_0_gemv" if fmt == "q4_0" else "komp_tq2_0_gemv"
+    with torch.cuda.device(dev):
+        _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
+                  s.data_ptr() if store_s else None, m, n, k, wq.stride(0), block_n, nb, mode, num_warps, _stream(xq))  # fmt: skip
+    return y, s
+
+
+def auto_config(fmt, m, n, k):
+    """(block_n, nb, num_warps) that gemv(..., block_n=None) uses for this shape."""
+    return _abi.auto_config(FMT_ID[fmt], m, n, k)
+
+
+def dp4a_probe(a, b, c, mode=2):
+    """OUT[i] = dp4a(a[i], b[i], c[i]) on the device (kernels.dp4a_probe, src/komp/kernels.py:145-149)."""
+    for t, name in ((a, "a"), (b, "b"), (c, "c")):
+        _need(t, name, torch.int32, 1)
+    a, b, c = a.contiguous(), b.contiguous(), c.contiguous()
+    out = torch.empty_like(a)
+    with torch.cuda.device(a.device):
+        _abi.call("komp_dp4a_probe", a.data_ptr(), b.data_ptr(), c.data_ptr(), out.data_ptr(), a.numel(), mode,
+                  _stream(a))  # fmt: skip
+    return out
+
+
+def q4_0_decode(wq):
+    """[R][16] q4_0 quant bytes -> [R][32] int32 values (kernels.q4_0_decode, src/komp/kernels.py:152-157)."""
+    _need(wq, "wq", torch.uint8, 2)
+    wq = wq.contiguous()
+    r = wq.shape[0]
+    out = torch.empty((r, 32), dtype=torch.int32, device=wq.device)
+    with torch.cuda.device(wq.device):
+        _abi.call("komp_q4_0_decode", wq.data_ptr(), out.data_ptr(), r, _stream(wq))
+    return out
+
+
+def tq2_0_decode(wq):
+    """[NBLK][64] tq2_0 quant bytes -> [NBLK][256] int32 values (kernels.tq2_0_decode, src/komp/kernels.py:160-170)."""
+    _need(wq, "wq", torch.uint8, 2)
+    wq = wq.contiguous()
+    nblk = wq.shape[0]
+    out = torch.empty((nblk, 256), dtype=torch.int32, device=wq.device)
+    with torch.cuda.device(wq.device):
+        _abi.call("komp_tq2_0_decode", wq.data_ptr(), out.data_ptr(), nblk, _stream(wq))
+    return out

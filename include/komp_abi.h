@@ -1,0 +1,99 @@
+/* C ABI of the MI355X (gfx950) decode path of COMP: activation quantizers and Q4_0 / TQ2_0 decode GEMVs.
+ *
+ * Plain C: pointers are device pointers (HIP), sizes are int64_t, `stream` is a hipStream_t passed as void*
+ * (NULL = the default stream).  Every call is asynchronous on `stream` and allocates nothing.  Each entry validates
+ * shapes, strides and alignment first and returns a nonzero status without touching the GPU when they are wrong;
+ * komp_last_error() then describes the problem.  Nothing aborts.  The library keeps no state between calls except
+ * the optional dispatch timing of the tuning harness (komp_timing_*).
+ *
+ * Layouts are the reference's split planes (src/komp/kernels.py:3-7, src/komp/host.py:16-31):
+ *   Q4_0 weights   WQ uint8 [N][SW] (row r at WQ + r*SW; 16 quant bytes per block of 32, ggml order),
+ *                  WS int16 [N][K/32] (f16 bit patterns, dense)
+ *   TQ2_0 weights  WQ uint8 [N][SW] (64 quant bytes per block of 256), WS int16 [N][K/256]
+ *   q8_0 acts      XQ int8 [M][K], XD f32 [M][K/32] (holding f32(f16(d)))
+ *   q8_K acts      XQ int8 [M][K], XD f32 [M][K/256], XB int16 [M][K/16] bsums (optional)
+ *   outputs        Y f32 [M][N]; S int32 [M][N][K/block] exact block dots (optional, verification)
+ */
+#ifndef KOMP_ABI_H
+#define KOMP_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KOMP_ABI_VERSION 1
+
+/* status codes */
+#define KOMP_OK 0
+#define KOMP_EINVAL 1 /* bad argument: shape, stride, alignment, knob or mode */
+#define KOMP_EHIP 2   /* the HIP runtime reported an error (launch or event) */
+
+/* GEMV modes (src/komp/host.py:13, src/komp/kernels.py:9-11) */
+#define KOMP_MODE_BYTES 0     /* every value unpacked to int32 first */
+#define KOMP_MODE_DP4A_EMU 1  /* packed-word dot products emulated with shifts and multiplies */
+#define KOMP_MODE_DP4A 2      /* packed-word dot products on v_dot4c_i32_i8 */
+
+/* Version of this ABI (KOMP_ABI_VERSION).  No reference counterpart. */
+int komp_abi_version(void);
+
+/* Message for the last nonzero status returned on the calling thread ("" if none). */
+const char* komp_last_error(void);
+
+/* f32 X [M][K] -> q8_0 planes XQ, XD.  K % 32 == 0; X 16-byte aligned, XQ 4-byte aligned.  `bb` (blocks per
+ * program in the reference) must be >= 1; every bb gives the same launch and the same bytes.
+ * Replaces: host.quantize q8_0 branch (src/komp/host.py:63-69) launching kernels.quant_q8_0 (src/komp/kernels.py:22-33). */
+int komp_quant_q8_0(const float* X, int8_t* XQ, float* XD, int64_t M, int64_t K, int bb, void* stream);
+
+/* f32 X [M][K] -> q8_K planes XQ, XD and, when XB is not NULL, the bsums XB [M][K/16].  K % 256 == 0.
+ * Replaces: host.quantize q8_K branch (src/komp/host.py:70-72) launching kernels.quant_q8_K (src/komp/kernels.py:36-45);
+ * the bsums, which the reference computes on the host (src/komp/host.py:50), come from the kernel. */
+int komp_quant_q8_K(const float* X, int8_t* XQ, float* XD, int16_t* XB, int64_t M, int64_t K, void* stream);
+
+/* Y [M][N] (and S when not NULL) for Q4_0 weights x q8_0 activations.
+ * K % 32 == 0; SW % 16 == 0 and SW >= K/2; WQ and XQ 16-byte aligned.
+ * block_n in {8,16,32,64,128}, nb in {1,2,4,8,16}, num_warps in {1,2,4,8}; block_n == 0 picks all three for the shape.
+ * mode: KOMP_MODE_*.
+ * Replaces: host.gemv (src/komp/host.py:76-85) launching kernels.q4_0_gemv (src/komp/kernels.py:48-94), whose
+ * argument list is (WQ, WS, XQ, XD, Y, S, N, K, SW; BLOCK_N, NB, MODE, STORE_S) (src/komp/compile.py:20-27). */
+int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                   void* stream);
+
+/* The same for TQ2_0 weights x q8_K activations.  K % 256 == 0; SW % 16 == 0 and SW >= K/4.
+ * Replaces: host.gemv (src/komp/host.py:76-85) launching kernels.tq2_0_gemv (src/komp/kernels.py:97-142). */
+int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                    void* stream);
+
+/* The (block_n, nb, num_warps) that block_n == 0 selects for a GEMV shape; fmt 0 = q4_0, 1 = tq2_0.
+ * No reference counterpart: the reference always takes the knobs from its caller. */
+int komp_gemv_auto_config(int fmt, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps);
+
+/* OUT[i] = dp4a(A[i], B[i], C[i]) for i < n; mode KOMP_MODE_DP4A (hardware) or KOMP_MODE_DP4A_EMU.
+ * Replaces: kernels.dp4a_probe (src/komp/kernels.py:145-149). */
+int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,
+                    void* stream);
+
+/* [R][16] Q4_0 quant bytes -> [R][32] int32 values.  Replaces: kernels.q4_0_decode (src/komp/kernels.py:152-157). */
+int komp_q4_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t R, void* stream);
+
+/* [NBLK][64] TQ2_0 quant bytes -> [NBLK][256] int32 values.  Replaces: kernels.tq2_0_decode (src/komp/kernels.py:160-170). */
+int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* stream);
+
+/* Dispatch timing for the tuning harness (no reference counterpart; the reference was never timed).
+ * Between komp_timing_begin() and komp_timing_end(), every launch made by this library on the calling process is
+ * issued with hipExtLaunchKernel start/stop events, which the runtime stamps with the dispatch's own begin and end.
+ * komp_timing_end() waits for those events and returns, per kernel kind, the summed dispatch time in milliseconds and
+ * the dispatch count.  Kinds: 0 quant_q8_0, 1 quant_q8_K, 2 q4_0_gemv, 3 tq2_0_gemv, 4 probes (arrays of length 5).
+ * max_dispatches bounds the events created. */
+#define KOMP_TIMING_KINDS 5
+int komp_timing_begin(int64_t max_dispatches);
+int komp_timing_end(double* ms, int64_t* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KOMP_ABI_H */

@@ -1,0 +1,407 @@
+"""CPU oracle for COMP's decode path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the thing measured or shipped: only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` may import it.  The product path (`comp_amd`) never imports anything under `oracle/`
+and fails loudly when its HIP library is missing.
+
+It restates, in numpy, the arithmetic of the reference decode path (COMP, package `komp`):
+
+  * the format helpers of `triton.language.extra.kurn`   patches/0001-language-extra-kurn.patch:33-131
+  * the split layouts and ggml block packing               src/komp/host.py:9-56
+  * the exact integer block dots and the f64 rebuild       src/komp/verify.py:37-41, 57-67, 94-120
+  * the GEMV arithmetic (int32 block dot, then f32 scale)  src/komp/kernels.py:48-142
+  * the synthetic problem generators of the workload list (seeded numpy; the reference's own generators live in the
+    absent `kurn.gpu.ref`, so the random streams are this repository's own)
+
+How each function is pinned (tests/test_oracle_pins.py):
+
+  f16_bits_to_f32        all 65536 bit patterns vs IEEE binary16 decoded from its fields with exact rationals
+  q4_0_values            all 256 byte values vs the per-value formula; ggml q4_0 quantize->decode round trip
+  tq2_0_values           all 256 byte values at every crumb position vs a per-value loop over the layout text
+  dp4a                   the reference's 11 edge words + random words vs an independent struct-based byte dot
+  round_half_*           vs Python's round()/Fraction on ties, negatives, huge and subnormal values
+  quant_q8_0 / q8_K      vs an exact-rational (fractions.Fraction) implementation with explicit IEEE f32 rounding,
+                         plus known answers (amax 127 -> d 1, ties, zero blocks, first-index ties, spikes)
+  block_dots             vs brute-force Python integer loops on tiny shapes, plus bilinearity
+  reference_dot          each term is exact in f64 (proved in the docstring) so tests compare the sum against
+                         math.fsum-free sequential Fraction sums rounded per step
+  relerr                 parity unpinned: KURN's `relerr` formula is in the absent `kurn` package
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------------------------------------------------
+# formats (src/komp/host.py:9-13)
+
+FORMATS = {
+    "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
+    "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
+}
+ACT_BLOCK = {"q8_0": 32, "q8_K": 256}
+
+
+def f16_bits_to_f32(bits):
+    """int16/uint16 fp16 bit patterns -> f32, exact (patch:33-36)."""
+    return np.asarray(bits).astype(np.uint16).view(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# weight decode (patch:16-19, 39-63; src/komp/verify.py:57-67)
+
+
+def q4_0_values(qs):
+    """[..., 16] q4_0 quant bytes -> [..., 32] int32: value i = (byte i & 15) - 8, value i+16 = (byte i >> 4) - 8."""
+    qs = np.asarray(qs, dtype=np.uint8)
+    lo = (qs & 15).astype(np.int32) - 8
+    hi = (qs >> 4).astype(np.int32) - 8
+    return np.concatenate([lo, hi], axis=-1)
+
+
+def tq2_0_values(qs):
+    """[..., 64] tq2_0 quant bytes -> [..., 256] int32.
+
+    Byte h*32+i holds value h*128 + j*32 + i at bits 2j..2j+1; value = crumb - 1 (crumb 3 decodes to +2)."""
+    qs = np.asarray(qs, dtype=np.uint8)
+    q = qs.reshape(*qs.shape[:-1], 2, 1, 32).astype(np.int32)  # [.., h, 1, i]
+    sh = (2 * np.arange(4, dtype=np.int32)).reshape(1, 4, 1)  # [1, j, 1]
+    v = ((q >> sh) & 3) - 1  # [.., h, j, i] -> value h*128 + j*32 + i
+    return v.reshape(*qs.shape[:-1], 256)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# dp4a (patch:66-81; src/komp/verify.py:37-41)
+
+
+def dp4a(a, b, c):
+    """c + sum of the four signed-byte products of int32 words a and b, with int32 wraparound (dp4a.s32.s32)."""
+    a = np.asarray(a, dtype=np.int64) & 0xFFFFFFFF
+    b = np.asarray(b, dtype=np.int64) & 0xFFFFFFFF
+    r = np.asarray(c, dtype=np.int64).copy()
+    for i in range(4):
+        sa = (a >> (8 * i)) & 0xFF
+        sb = (b >> (8 * i)) & 0xFF
+        sa = np.where(sa >= 128, sa - 256, sa)
+        sb = np.where(sb >= 128, sb - 256, sb)
+        r = r + sa * sb
+    return (((r + 2**31) % 2**32) - 2**31).astype(np.int32)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# exact rounding (patch:84-101), in f32
+
+
+def round_half_away(x):
+    """roundf(): nearest integer, halfway cases away from zero, exact for every f32 (patch:84-90)."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x)
+    f = np.floor(a)
+    r = np.where(a - f >= np.float32(0.5), f + np.float32(1.0), f)
+    return np.where(x < 0, -r, r).astype(np.float32)
+
+
+def round_half_even(x):
+    """nearbyint() in round-to-nearest-even mode, exact for every f32 (patch:93-101)."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x)
+    f = np.floor(a)
+    d = a - f
+    odd = (f - np.float32(2.0) * np.floor(f * np.float32(0.5))) != 0
+    r = np.where((d > np.float32(0.5)) | ((d == np.float32(0.5)) & odd), f + np.float32(1.0), f)
+    return np.where(x < 0, -r, r).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# activation quantizers (patch:104-131; src/komp/kernels.py:22-45; src/komp/host.py:43-52)
+
+
+def quant_q8_0(x):
+    """f32 [M][K] -> (XQ int8 [M][K], XD f32 [M][K/32]) as ggml quantize_row_q8_0_ref.
+
+    Per block of 32: amax = max|x|; d = amax / 127 (f32, round to nearest); id = 1/d (0 when d == 0);
+    q = roundf(x * id) computed with the unrounded d; XD stores f32(f16(d)) (patch:104-114, kernels.py:33)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    assert k % 32 == 0
+    xb = x.reshape(m, k // 32, 32)
+    amax = np.max(np.abs(xb), axis=2)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    nz = d != 0
+    idv = np.where(nz, np.float32(1.0) / np.where(nz, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    q = round_half_away((xb * idv[:, :, None]).astype(np.float32))
+    xq = q.astype(np.int32).astype(np.int8).reshape(m, k)
+    with np.errstate(over="ignore"):
+        xd = d.astype(np.float16).astype(np.float32)
+    return xq, xd
+
+
+def quant_q8_K(x):
+    """f32 [M][K] -> (XQ int8 [M][K], XD f32 [M][K/256], XB int16 [M][K/16]) as ggml quantize_row_q8_K_ref.
+
+    Per block of 256: amax = max|x|, mx = x at the FIRST index where |x| == amax; all-zero block -> q = 0, d = 0;
+    else iscale = -127 / mx, q = min(127, nearest-even(iscale * x)), d = 1 / iscale (patch:117-131).
+    XB are the bsums, the sums of each 16 consecutive q (src/komp/host.py:50)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    assert k % 256 == 0
+    xb = x.reshape(m, k // 256, 256)
+    ax = np.abs(xb)
+    amax = ax.max(axis=2)
+    first = np.argmax(ax == amax[:, :, None], axis=2)  # argmax returns the first True
+    mx = np.take_along_axis(xb, first[:, :, None], axis=2)[:, :, 0]
+    nz = amax != 0
+    iscale = (np.float32(-127.0) / np.where(nz, mx, np.float32(1.0))).astype(np.float32)
+    q = np.minimum(round_half_even((iscale[:, :, None] * xb).astype(np.float32)), np.float32(127.0))
+    q = np.where(nz[:, :, None], q, np.float32(0.0)).astype(np.int32)
+    d = np.where(nz, (np.float32(1.0) / iscale).astype(np.float32), np.float32(0.0)).astype(np.float32)
+    xq = q.astype(np.int8).reshape(m, k)
+    xbs = q.reshape(m, k // 16, 16).sum(axis=2).astype(np.int16)
+    return xq, d, xbs
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# split planes and ggml blocks (src/komp/host.py:16-56)
+
+
+def split(fmt, W, n, k):
+    """ggml weight blocks (bytes, n rows) -> (WQ uint8 [n][quant bytes per row], WS int16 [n][blocks])."""
+    f = FORMATS[fmt]
+    nb = k // f["block"]
+    blocks = np.frombuffer(bytes(W), dtype=np.uint8).reshape(n, nb, f["nbytes"])
+    wq = np.ascontiguousarray(blocks[:, :, f["qoff"] : f["qoff"] + f["qbytes"]]).reshape(n, nb * f["qbytes"])
+    ws = np.ascontiguousarray(blocks[:, :, f["soff"] : f["soff"] + 2]).view(np.int16).reshape(n, nb)
+    return wq, ws
+
+
+def join(fmt, wq, ws):
+    """Inverse of split: split planes -> ggml block bytes."""
+    f = FORMATS[fmt]
+    n, nb = ws.shape
+    out = np.zeros((n, nb, f["nbytes"]), dtype=np.uint8)
+    out[:, :, f["qoff"] : f["qoff"] + f["qbytes"]] = np.asarray(wq, np.uint8).reshape(n, nb, f["qbytes"])
+    out[:, :, f["soff"] : f["soff"] + 2] = np.ascontiguousarray(ws, dtype=np.int16).view(np.uint8).reshape(n, nb, 2)
+    return out.tobytes()
+
+
+def q8_0_blocks(xq, xd):
+    """q8_0 split planes -> ggml q8_0 blocks: f16 d then 32 int8 per block (34 bytes)."""
+    xq = np.asarray(xq, np.int8)
+    m, k = xq.shape
+    out = np.empty((m, k // 32, 34), dtype=np.uint8)
+    out[:, :, :2] = np.asarray(xd, np.float32).astype(np.float16).view(np.uint8).reshape(m, k // 32, 2)
+    out[:, :, 2:] = xq.view(np.uint8).reshape(m, k // 32, 32)
+    return out.tobytes()
+
+
+def q8_K_blocks(xq, xd, xb=None):
+    """q8_K split planes -> ggml q8_K blocks: f32 d, 256 int8, 16 int16 bsums (292 bytes)."""
+    xq = np.asarray(xq, np.int8)
+    m, k = xq.shape
+    nb = k // 256
+    out = np.empty((m, nb, 292), dtype=np.uint8)
+    out[:, :, :4] = np.asarray(xd, np.float32).view(np.uint8).reshape(m, nb, 4)
+    out[:, :, 4:260] = xq.view(np.uint8).reshape(m, nb, 256)
+    if xb is None:
+        xb = xq.astype(np.int32).reshape(m, nb, 16, 16).sum(-1).astype(np.int16)
+    out[:, :, 260:] = np.ascontiguousarray(xb, dtype=np.int16).view(np.uint8).reshape(m, nb, 32)
+    return out.tobytes()
+
+
+def act_blocks(fmt, xq, xd, xb=None):
+    if FORMATS[fmt]["act"] == "q8_0":
+        return q8_0_blocks(xq, xd)
+    return q8_K_blocks(xq, xd, xb)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# GEMV references (src/komp/verify.py:94-120; src/komp/kernels.py:48-142)
+
+
+def weight_values(fmt, wq, n, k):
+    """Split quant plane -> int32 weight values [n][k]."""
+    wq = np.asarray(wq, np.uint8).reshape(n, -1)
+    if fmt == "q4_0":
+        return q4_0_values(wq[:, : k // 2].reshape(n, k // 32, 16)).reshape(n, k)
+    return tq2_0_values(wq[:, : k // 4].reshape(n, k // 256, 64)).reshape(n, k)
+
+
+def block_dots(fmt, wq, xq, n, k):
+    """Exact int64 block dots S[m][n][b] = sum_i w(n, b*blk + i) * q(m, b*blk + i) (verify.py:94-100)."""
+    blk = FORMATS[fmt]["block"]
+    v = weight_values(fmt, wq, n, k).reshape(n, k // blk, blk).astype(np.int64)
+    q = np.asarray(xq, np.int8).reshape(-1, k // blk, blk).astype(np.int64)
+    return np.einsum("nbi,mbi->mnb", v, q)
+
+
+def reference_dot(fmt, ws, xd, s):
+    """f64 reference outputs [M][N], summed block by block in order (verify.py:103-120).
+
+    q4_0 adds f16(dw) * f16(dx) * s, tq2_0 adds f32(dx) * f16(dw) * s, left to right, in Python-float (f64)
+    arithmetic.  Both products are exact in f64 (11+11+22 and 24+11+16 significant bits), so only the running
+    sum rounds, and the result depends on the block order alone."""
+    dw = f16_bits_to_f32(ws).astype(np.float64)  # [N][nb]
+    dx = np.asarray(xd, np.float32).astype(np.float64)  # [M][nb]
+    s = np.asarray(s, dtype=np.int64)
+    m, n, nb = s.shape
+    total = np.zeros((m, n), dtype=np.float64)
+    for b in range(nb):
+        if fmt == "q4_0":
+            term = (dw[None, :, b] * dx[:, None, b]) * s[:, :, b]
+        else:
+            term = (dx[:, None, b] * dw[None, :, b]) * s[:, :, b]
+        total = total + term
+    return total
+
+
+def gemv(fmt, wq, ws, xq, xd, n, k):
+    """(Y f64 reference [M][N], S int64 [M][N][blocks]) for split planes and q8 activations."""
+    s = block_dots(fmt, wq, xq, n, k)
+    return reference_dot(fmt, ws, xd, s), s
+
+
+def relerr(y, r):
+    """Norm-wise relative error max|y - r| / max|r| (0 when both are all zero).
+
+    KURN's own `kurn.gpu.ref.relerr` is in the absent `kurn` package: its formula is parity unpinned.  The norm-wise
+    form stays meaningful for outputs that cancel to near zero, where an element-wise ratio would not."""
+    y = np.asarray(y, dtype=np.float64).reshape(-1)
+    r = np.asarray(r, dtype=np.float64).reshape(-1)
+    if y.size == 0:
+        return 0.0
+    den = float(np.max(np.abs(r)))
+    num = float(np.max(np.abs(y - r)))
+    if den == 0.0:
+        return 0.0 if num == 0.0 else float("inf")
+    return num / den
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# weight builders used by the synthetic problems
+
+
+def quantize_q4_0_weights(w):
+    """f32 [n][k] -> ggml q4_0 blocks (bytes), ggml quantize_row_q4_0_ref.
+
+    Per block of 32: max = the signed value of largest |x| (first on ties); d = max / -8; id = 1/d (0 if d == 0);
+    q = min(15, trunc(x * id + 8.5)); byte j = q[j] | q[j+16] << 4; f16 d first."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    wb = w.reshape(n, k // 32, 32)
+    ax = np.abs(wb)
+    first = np.argmax(ax == ax.max(axis=2)[:, :, None], axis=2)
+    mx = np.take_along_axis(wb, first[:, :, None], axis=2)[:, :, 0]
+    d = (mx / np.float32(-8.0)).astype(np.float32)
+    nz = d != 0
+    idv = np.where(nz, np.float32(1.0) / np.where(nz, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    v = (wb * idv[:, :, None]).astype(np.float32) + np.float32(8.5)
+    q = np.minimum(np.trunc(v), np.float32(15.0)).astype(np.int32)
+    q = np.clip(q, 0, 15).astype(np.uint8)
+    qs = (q[:, :, :16] | (q[:, :, 16:] << 4)).astype(np.uint8)
+    out = np.empty((n, k // 32, 18), dtype=np.uint8)
+    with np.errstate(over="ignore"):
+        out[:, :, :2] = d.astype(np.float16).view(np.uint8).reshape(n, k // 32, 2)
+    out[:, :, 2:] = qs
+    return out.tobytes()
+
+
+def pack_q4_0(nibbles, d_bits):
+    """nibbles uint8 [n][k] in 0..15 (value = nibble - 8) and f16 bit patterns [n][k/32] -> ggml q4_0 blocks."""
+    nib = np.asarray(nibbles, np.uint8)
+    n, k = nib.shape
+    nb = nib.reshape(n, k // 32, 32)
+    out = np.empty((n, k // 32, 18), dtype=np.uint8)
+    out[:, :, :2] = np.ascontiguousarray(d_bits, dtype=np.uint16).view(np.uint8).reshape(n, k // 32, 2)
+    out[:, :, 2:] = (nb[:, :, :16] & 15) | ((nb[:, :, 16:] & 15) << 4)
+    return out.tobytes()
+
+
+def pack_tq2_0(crumbs, d_bits):
+    """crumbs uint8 [n][k] in 0..3 (value = crumb - 1) and f16 bit patterns [n][k/256] -> ggml tq2_0 blocks."""
+    c = np.asarray(crumbs, np.uint8)
+    n, k = c.shape
+    cb = c.reshape(n, k // 256, 2, 4, 32)  # value h*128 + j*32 + i
+    qs = np.zeros((n, k // 256, 2, 32), dtype=np.uint8)
+    for j in range(4):
+        qs |= (cb[:, :, :, j, :] & 3) << (2 * j)
+    out = np.empty((n, k // 256, 66), dtype=np.uint8)
+    out[:, :, :64] = qs.reshape(n, k // 256, 64)
+    out[:, :, 64:] = np.ascontiguousarray(d_bits, dtype=np.uint16).view(np.uint8).reshape(n, k // 256, 2)
+    return out.tobytes()
+
+
+F16_MAX_BITS = 0x7BFF  # 65504
+F16_MIN_SUBNORMAL_BITS = 0x0001  # 2**-24
+
+
+def weights(fmt, rng, n, k, extreme=False):
+    """Seeded ggml weight blocks for an n x k matrix.
+
+    random  q4_0: W ~ N(0, 0.02) quantized by ggml's q4_0 rule; tq2_0: trits from {-1, 0, +1} with p 0.3/0.4/0.3,
+            d ~ U(0.01, 0.05) rounded to f16.
+    extreme per block: f16 d at 65504, at the smallest subnormal 2**-24 or random; values all at the minimum
+            (nibble 0 / crumb 0), all at the maximum (nibble 15 / crumb 2), random, or (tq2_0) crumb 3."""
+    nb = k // FORMATS[fmt]["block"]
+    if fmt == "q4_0" and not extreme:
+        return quantize_q4_0_weights(rng.normal(0.0, 0.02, size=(n, k)).astype(np.float32))
+    if fmt == "q4_0":
+        nib = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+        kind = rng.integers(0, 3, size=(n, nb))
+        nibb = nib.reshape(n, nb, 32)
+        nibb[kind == 1] = 0
+        nibb[kind == 2] = 15
+        d = np.asarray(rng.uniform(-0.05, 0.05, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+        sk = rng.integers(0, 4, size=(n, nb))
+        d = np.where(sk == 1, F16_MAX_BITS, np.where(sk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
+        return pack_q4_0(nibb.reshape(n, k), d)
+    crumbs = (rng.choice(3, size=(n, k), p=[0.3, 0.4, 0.3])).astype(np.uint8)  # crumb = trit + 1
+    d = np.asarray(rng.uniform(0.01, 0.05, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+    if extreme:
+        cb = crumbs.reshape(n, nb, 256)
+        kind = rng.integers(0, 4, size=(n, nb))
+        cb[kind == 1] = 0
+        cb[kind == 2] = 2
+        three = (kind == 3)[:, :, None] & (rng.random(size=(n, nb, 256)) < 0.05)
+        cb[three] = 3
+        crumbs = cb.reshape(n, k)
+        sk = rng.integers(0, 4, size=(n, nb))
+        d = np.where(sk == 1, F16_MAX_BITS, np.where(sk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
+    return pack_tq2_0(crumbs, d)
+
+
+def activations(rng, k, m, block=32, extreme=False, outliers=0.0):
+    """Seeded f32 activations [m][k] ~ N(0, 1).
+
+    outliers: that fraction of entries scaled x20.  extreme per block: all zero, one +-1e4 spike in N(0, 1) noise,
+    or random."""
+    x = rng.normal(0.0, 1.0, size=(m, k)).astype(np.float32)
+    if outliers:
+        sel = rng.random(size=(m, k)) < outliers
+        x[sel] *= np.float32(20.0)
+    if extreme:
+        nb = k // block
+        xb = x.reshape(m, nb, block)
+        kind = rng.integers(0, 3, size=(m, nb))
+        xb[kind == 1] = 0.0
+        pos = rng.integers(0, block, size=(m, nb))
+        sign = np.where(rng.random(size=(m, nb)) < 0.5, -1.0, 1.0).astype(np.float32)
+        mi, bi = np.nonzero(kind == 2)
+        xb[mi, bi, pos[mi, bi]] = sign[mi, bi] * np.float32(1e4)
+        x = xb.reshape(m, k)
+    return x
+
+
+def problem(fmt, n, k, m, seed, extreme=False):
+    """(W ggml block bytes, x f32 [m][k]) for one GEMV problem, seeded."""
+    rng = np.random.default_rng(seed)
+    W = weights(fmt, rng, n, k, extreme)
+    x = activations(rng, k, m, block=ACT_BLOCK[FORMATS[fmt]["act"]], extreme=extreme)
+    return W, x
+
+
+def quantize(fmt, x):
+    """The activation quantizer for a weight format: q4_0 -> (xq, xd, None); tq2_0 -> (xq, xd, bsums)."""
+    if FORMATS[fmt]["act"] == "q8_0":
+        xq, xd = quant_q8_0(x)
+        return xq, xd, None
+    return quant_q8_K(x)

@@ -1,0 +1,146 @@
+"""HIP kernels vs the oracle on the same seeded inputs: quantizer bytes exact, int32 block dots exact, f32 outputs within
+1e-5 (norm-wise) of the f64 reference_dot.  Everything goes through the C ABI (comp_amd.host -> libkomp_hip.so)."""
+
+import numpy as np
+import pytest
+import torch
+
+from comp_amd import host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+# src/komp/verify.py:141-142
+PROBLEMS = {"q4_0": ((64, 512, 1), (37, 416, 3), (5, 96, 2)), "tq2_0": ((64, 1024, 1), (37, 768, 3), (5, 1280, 2))}
+CONFIGS = {"q4_0": ((32, 4, 4), (16, 2, 2), (64, 8, 4)), "tq2_0": ((32, 2, 4), (16, 1, 2), (64, 4, 4))}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_quant(fmt, x):
+    xq, xd, *xb = host.quantize(fmt, dev(x), bsums=(fmt == "tq2_0"))
+    torch.cuda.synchronize()
+    return xq.cpu().numpy(), xd.cpu().numpy(), (xb[0].cpu().numpy() if xb else None)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("extreme", [False, True])
+@pytest.mark.parametrize("m,k", [(1, 256), (3, 2560), (2, 4096 + 256)])
+def test_quantizer_bytes_exact(fmt, extreme, m, k):
+    rng = np.random.default_rng(100 + m + k + extreme)
+    x = O.activations(rng, k, m, block=32 if fmt == "q4_0" else 256, extreme=extreme, outliers=0.01)
+    xq, xd, xb = run_quant(fmt, x)
+    rq, rd, rb = O.quantize(fmt, x)
+    assert np.array_equal(xq, rq)
+    assert np.array_equal(xd.view(np.uint32), rd.view(np.uint32))
+    if fmt == "tq2_0":
+        assert np.array_equal(xb, rb)
+    assert host.act_blocks(fmt, xq, xd, xb) == O.act_blocks(fmt, rq, rd)
+
+
+def test_q8_0_f16_scale_edges():
+    # d = amax / 127 rounds to f16 subnormals, to f16 overflow (inf) and exactly to 1
+    k = 32 * 6
+    x = np.zeros((1, k), np.float32)
+    x[0, 0:32] = np.linspace(-127, 127, 32, dtype=np.float32)  # amax 127 -> d 1, q == x
+    x[0, 32:64] = 3e-6  # d in the f16 subnormal range
+    x[0, 64:96] = np.float32(1e38)  # f16(d) overflows to inf
+    x[0, 96:100] = np.float32(1e-36)  # d = amax / 127 is an f32 subnormal with a finite 1 / d
+    x[0, 100] = np.float32(-1e-40)  # subnormal input in the same block
+    x[0, 128:160] = np.arange(32, dtype=np.float32) - np.float32(15.5)  # ties at k + 0.5 (d = 16.5 / 127)
+    x[0, 160:192] = 0.0
+    xq, xd, _ = run_quant("q4_0", x)
+    rq, rd = O.quant_q8_0(x)
+    assert np.array_equal(xq, rq)
+    assert np.array_equal(xd.view(np.uint32), rd.view(np.uint32))
+    assert np.isinf(xd[0, 2]) and xd[0, 5] == 0.0
+
+
+def test_q8_K_first_index_and_ties():
+    k = 256 * 3
+    x = np.random.default_rng(5).normal(size=(1, k)).astype(np.float32)
+    x[0, 10] = 7.0
+    x[0, 20] = -7.0  # |x| tie: the first index (positive) decides the sign of iscale
+    x[0, 256 + 3] = -5.0
+    x[0, 256 + 200] = 5.0
+    x[0, 512:] = 0.0
+    xq, xd, xb = run_quant("tq2_0", x)
+    rq, rd, rb = O.quant_q8_K(x)
+    assert np.array_equal(xq, rq) and np.array_equal(xd.view(np.uint32), rd.view(np.uint32)) and np.array_equal(xb, rb)
+    assert xq[0, 10] == -127 and xq[0, 20] == 127 and xd[0, 2] == 0.0
+
+
+def run_gemv(fmt, n, k, m, seed, extreme, block_n, nb, mode, num_warps):
+    W, x = O.problem(fmt, n, k, m, seed, extreme)
+    wq, ws = host.split(fmt, W, n, k)
+    xq, xd, *_ = host.quantize(fmt, dev(x))
+    y, s = host.gemv(fmt, dev(wq), dev(ws), xq, xd, n, k, block_n, nb, mode, num_warps, store_s=True)
+    torch.cuda.synchronize()
+    rq, rd, _ = O.quantize(fmt, x)
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    return y.cpu().numpy(), s.cpu().numpy(), r, rs, xq.cpu().numpy(), rq
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("prob", [0, 1, 2])
+@pytest.mark.parametrize("extreme", [False, True])
+def test_gemv_verify_problems(fmt, mode, cfg, prob, extreme):
+    n, k, m = PROBLEMS[fmt][prob]
+    block_n, nb, nw = CONFIGS[fmt][cfg]
+    y, s, r, rs, xq, rq = run_gemv(fmt, n, k, m, 1 + extreme, extreme, block_n, nb, mode, nw)
+    assert np.array_equal(xq, rq)
+    assert np.array_equal(s.astype(np.int64), rs)
+    assert O.relerr(y, r) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("block_n", [8, 16, 32, 64, 128])
+@pytest.mark.parametrize("nb", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("nw", [1, 2, 4, 8])
+def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
+    n, k, m = (77, 96 * 32, 3) if fmt == "q4_0" else (77, 13 * 256, 3)
+    y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
+    assert np.array_equal(s.astype(np.int64), rs)
+    assert O.relerr(y, r) <= TOL
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_0", 4096, 4096), ("q4_0", 4097, 4192), ("q4_0", 127, 4192),
+                                     ("tq2_0", 6912, 2560), ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_gemv_auto_config_shapes(fmt, n, k, m):
+    y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 21, False, None, None, 2, None)
+    assert np.array_equal(s.astype(np.int64), rs)
+    assert O.relerr(y, r) <= TOL
+
+
+def test_dp4a_probe_both_modes():
+    rng = np.random.default_rng(3)
+    edge = np.array([0, -1, 0x7F7F7F7F, -0x7F7F7F80, 0x01010101, 0x0F0F0F0F, 0x03030303, 2**31 - 1, -(2**31),
+                     0x80000000 - 2**32], dtype=np.int64)  # fmt: skip  (src/komp/verify.py:47)
+    n = 1024
+    def vals():
+        v = rng.integers(-(2**31), 2**31, size=n)
+        pick = rng.random(n) < 0.3
+        v[pick] = rng.choice(edge, size=int(pick.sum()))
+        return v.astype(np.int32)
+    a, b = vals(), vals()
+    c = rng.integers(-(2**20), 2**20, size=n).astype(np.int32)
+    want = O.dp4a(a, b, c)
+    for mode in (1, 2):
+        got = host.dp4a_probe(dev(a), dev(b), dev(c), mode).cpu().numpy()
+        assert np.array_equal(got, want), mode
+
+
+def test_decode_probes():
+    rng = np.random.default_rng(7)
+    wq = rng.integers(0, 256, size=(37, 16), dtype=np.uint8)
+    got = host.q4_0_decode(dev(wq)).cpu().numpy()
+    assert np.array_equal(got, O.q4_0_values(wq))
+    tq = rng.integers(0, 256, size=(5, 64), dtype=np.uint8)
+    got = host.tq2_0_decode(dev(tq)).cpu().numpy()
+    assert np.array_equal(got, O.tq2_0_values(tq))
