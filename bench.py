@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Decode-path benchmark on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--mode 2] [--no-detail] [--no-cpu]
+
+Workload (the headline): TQ2_0 (ternary, BitNet b1.58) decode steps at BitNet-2B FFN shapes.  One step quantizes an
+activation column block with quant_q8_K and runs tq2_0_gemv, for W[6912 x 2560] and then for W[2560 x 6912].  Weights
+are synthetic ternary ({-1, 0, +1} with p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), activations N(0, 1), all resident in
+HBM before the timed region.  Each step reads a different copy of both matrices (>= 1 GiB of copies), so no call is
+served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-graph replays, so the host launch rate
+does not bound them.
+
+Printed: one JSON line.  value = algorithmic bytes of the K steps / their wall time (GB/s); roofline = the tq2_0_gemv
+dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
+(the clock rocprofv3 --kernel-trace reads); cpu_baseline = the numpy oracle on a bounded sample of the same steps on
+this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold, library-chosen knobs).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "GEMV µs/call + achieved HBM GB/s (% of peak), Q4_0 & TQ2_0 decode shapes"
+PEAK_GBS = 8000.0  # MI355X HBM3E, published
+COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infinity Cache)
+
+
+def gemv_bytes(fmt, n, k, m):
+    """Algorithmic HBM bytes of one GEMV call: weights (quant + scale planes), q8 activations, f32 outputs."""
+    if fmt == "q4_0":
+        return n * k * 18 // 32 + m * (k + 4 * k // 32) + 4 * m * n
+    return n * k * 66 // 256 + m * (k + 4 * k // 256) + 4 * m * n
+
+
+def quant_bytes(fmt, k, m):
+    """Algorithmic bytes of one quantizer call: f32 read, int8 + f32 scale written (no bsums)."""
+    blk = 32 if fmt == "q4_0" else 256
+    return 4 * m * k + m * k + 4 * m * (k // blk)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# synthetic weights, generated on the device
+
+
+def tq2_0_weights(n, k, gen, torch):
+    """Split planes of ternary TQ2_0 weights: crumb c = trit + 1 from {0, 1, 2} with p 0.3/0.4/0.3; f16 d ~ U(.01,.05).
+    Byte h*32 + i of a block holds value h*128 + j*32 + i at bits 2j."""
+    nb = k // 256
+    u = torch.rand((n, nb, 2, 4, 32), generator=gen, device="cuda")
+    c = (u > 0.3).to(torch.uint8) + (u > 0.7).to(torch.uint8)
+    qs = c[:, :, :, 0] | (c[:, :, :, 1] << 2) | (c[:, :, :, 2] << 4) | (c[:, :, :, 3] << 6)
+    wq = qs.reshape(n, nb * 64).contiguous()
+    d = torch.rand((n, nb), generator=gen, device="cuda") * 0.04 + 0.01
+    ws = d.half().view(torch.int16).contiguous()
+    return wq, ws
+
+
+def q4_0_weights(n, k, gen, torch):
+    """Split planes of Q4_0 weights: W ~ N(0, 0.02) quantized by ggml's q4_0 rule (d = max / -8 with max the signed
+    value of largest |w|, q = min(15, trunc(w / d + 8.5)))."""
+    nb = k // 32
+    w = torch.randn((n, nb, 32), generator=gen, device="cuda") * 0.02
+    idx = w.abs().argmax(dim=2, keepdim=True)
+    mx = torch.gather(w, 2, idx)
+    d = mx / -8.0
+    idv = torch.where(d != 0, 1.0 / torch.where(d != 0, d, torch.ones_like(d)), torch.zeros_like(d))
+    q = torch.clamp(torch.trunc(w * idv + 8.5), 0, 15).to(torch.uint8)
+    wq = (q[:, :, :16] | (q[:, :, 16:] << 4)).reshape(n, nb * 16).contiguous()
+    ws = d[:, :, 0].half().view(torch.int16).contiguous()
+    return wq, ws
+
+
+def weight_copies(fmt, n, k, gen, torch, total=COLD_BYTES):
+    make = q4_0_weights if fmt == "q4_0" else tq2_0_weights
+    wq, ws = make(n, k, gen, torch)
+    per = wq.numel() + 2 * ws.numel()
+    copies = max(2, math.ceil(total / per))
+    return [(wq.clone(), ws.clone()) for _ in range(copies)]
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+
+
+def run_graph(torch, fn, count, replays):
+    """Capture fn(0..count-1) in one HIP graph; return (graph, replay function)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(count, 2)):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(count):
+            fn(i)
+    return g
+
+
+def timed_steps(torch, step, ncopies, steps, warmup):
+    """Run `warmup` then exactly `steps` steps as graph replays; returns elapsed ms of the timed steps."""
+    g_full = run_graph(torch, step, ncopies, 1)
+    rem = steps % ncopies
+    g_rem = run_graph(torch, step, rem, 1) if rem else None
+    for _ in range(max(1, math.ceil(warmup / ncopies))):
+        g_full.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps // ncopies):
+        g_full.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return e0.elapsed_time(e1), wall
+
+
+def dispatch_times(abi, torch, step, count):
+    """Run `count` eager steps with per-dispatch timing; -> {kind: (total_ms, dispatches)}."""
+    torch.cuda.synchronize()
+    abi.timing_begin(count * 8 + 16)
+    for i in range(count):
+        step(i)
+    torch.cuda.synchronize()
+    return abi.timing_end()
+
+
+def headline(torch, host, abi, args):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    m = args.m
+    shapes = ((6912, 2560), (2560, 6912))
+    mats = []
+    for n, k in shapes:
+        copies = weight_copies("tq2_0", n, k, gen, torch, COLD_BYTES // len(shapes))
+        x = torch.randn((m, k), generator=gen, device="cuda")
+        xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+        xd = torch.empty((m, k // 256), dtype=torch.float32, device="cuda")
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        mats.append(dict(n=n, k=k, copies=copies, x=x, xq=xq, xd=xd, y=y))
+    ncopies = min(len(mt["copies"]) for mt in mats)
+    knobs = [host.auto_config("tq2_0", m, mt["n"], mt["k"]) if args.block_n is None else
+             (args.block_n, args.nb, args.num_warps) for mt in mats]  # fmt: skip
+
+    def step(i):
+        for mt, (bn, nb, nw) in zip(mats, knobs):
+            wq, ws = mt["copies"][i % ncopies]
+            host.quantize_into("tq2_0", mt["x"], mt["xq"], mt["xd"])
+            host.gemv_into("tq2_0", wq, ws, mt["xq"], mt["xd"], mt["y"], mt["n"], mt["k"], bn, nb, args.mode, nw)
+
+    ms, wall_ms = timed_steps(torch, step, ncopies, args.steps, args.warmup)
+    # the graph must reproduce the eager result of the same (last) step bit for bit
+    last = (args.steps - 1) % ncopies
+    got = [mt["y"].clone() for mt in mats]
+    step(last)
+    torch.cuda.synchronize()
+    for mt, gy in zip(mats, got):
+        if not torch.equal(mt["y"], gy):
+            raise RuntimeError("graph replay and eager outputs differ")
+
+    step_bytes = sum(gemv_bytes("tq2_0", mt["n"], mt["k"], m) + quant_bytes("tq2_0", mt["k"], m) for mt in mats)
+    ms_per_step = ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    disp = dispatch_times(abi, torch, step, min(args.steps, 4 * ncopies))
+    g_ms, g_n = disp["tq2_0_gemv"]
+    q_ms, q_n = disp["quant_q8_K"]
+    gemv_b = sum(gemv_bytes("tq2_0", mt["n"], mt["k"], m) for mt in mats) / len(mats)
+    g_us = g_ms * 1e3 / g_n
+    achieved = gemv_b / (g_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "tq2_0_gemv",
+                "dispatch_us": round(g_us, 3), "bytes_per_launch": int(gemv_b)}  # fmt: skip
+    config = {"workload": "tq2_0 decode step at BitNet-2B FFN shapes: quant_q8_K + tq2_0_gemv on W[6912x2560], "
+                          "then on W[2560x6912]",  # fmt: skip
+              "shapes_nk": [list(s) for s in shapes], "m": m, "mode": {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}[args.mode],
+              "knobs_block_n_nb_warps": [list(kn) for kn in knobs], "cold_copies": ncopies, "seed": args.seed,
+              "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3),
+              "gemv_us_per_call_dispatch": round(g_us, 3), "quant_us_per_call_dispatch": round(q_ms * 1e3 / q_n, 3),
+              "us_per_step_graph": round(ms_per_step * 1e3, 3)}  # fmt: skip
+    return value, ms_per_step, roofline, config, step_bytes
+
+
+def cpu_baseline(args, step_bytes_m, seconds=10.0):
+    """numpy oracle (this repository's restatement of the reference path) on whole steps of the same workload."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(args.seed)
+    m = args.m
+    mats = []
+    for n, k in ((6912, 2560), (2560, 6912)):
+        nb = k // 256
+        crumbs = rng.choice(3, size=(n, k), p=[0.3, 0.4, 0.3]).astype(np.uint8)
+        d = rng.uniform(0.01, 0.05, size=(n, nb)).astype(np.float32).astype(np.float16).view(np.uint16)
+        wq, ws = O.split("tq2_0", O.pack_tq2_0(crumbs, d), n, k)
+        mats.append((n, k, wq, ws, rng.normal(size=(m, k)).astype(np.float32)))
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for n, k, wq, ws, x in mats:
+            xq, xd, _ = O.quant_q8_K(x)
+            O.gemv("tq2_0", wq, ws, xq, xd, n, k)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    value = step_bytes_m * steps / el / 1e9
+    return {"value": round(value, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} whole steps of the same workload (both matrices, m={m}) through the numpy oracle "
+                      f"(quant_q8_K, exact int64 block dots, f64 reference_dot) in {el:.1f} s, 1 thread; host has "
+                      f"{len(os.sched_getaffinity(0))} cores"}  # fmt: skip
+
+
+DETAIL_SHAPES = (  # (fmt, n, k, m)
+    ("q4_0", 4096, 4096, 1), ("q4_0", 6144, 4096, 1), ("q4_0", 28672, 4096, 1), ("q4_0", 4096, 14336, 1),
+    ("q4_0", 4096, 14336, 3), ("q4_0", 128256, 4096, 1), ("q4_0", 28672, 8192, 1), ("tq2_0", 6912, 2560, 1),
+    ("tq2_0", 2560, 6912, 1), ("tq2_0", 6912, 2560, 3), ("tq2_0", 32768, 8192, 1), ("q4_0", 4097, 4192, 1),
+    ("tq2_0", 6913, 2816, 1),
+)  # fmt: skip
+
+
+def detail(torch, host, abi, args):
+    """Per-shape GEMV us/call (graph replay) and dispatch duration, cold, library-chosen knobs, dp4a."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 1)
+    for fmt, n, k, m in DETAIL_SHAPES:
+        copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
+        x = torch.randn((m, k), generator=gen, device="cuda")
+        xq, xd = host.quantize(fmt, x)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        nc = len(copies)
+
+        def call(i, copies=copies, xq=xq, xd=xd, y=y, fmt=fmt, n=n, k=k):
+            wq, ws = copies[i % nc]
+            host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, 2, 0)
+
+        reps = max(64, nc)
+        reps -= reps % nc
+        ms, _ = timed_steps(torch, call, nc, reps, nc)
+        disp = dispatch_times(abi, torch, call, min(reps, 256))
+        kind = "q4_0_gemv" if fmt == "q4_0" else "tq2_0_gemv"
+        d_us = disp[kind][0] * 1e3 / disp[kind][1]
+        b = gemv_bytes(fmt, n, k, m)
+        us = ms * 1e3 / reps
+        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "knobs": list(host.auto_config(fmt, m, n, k)),
+                     "bytes": b, "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                     "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "dispatch_us": round(d_us, 3),
+                     "gbs_dispatch": round(b / d_us / 1e3, 1), "copies": nc})  # fmt: skip
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--m", type=int, default=1, help="activation columns (1..3 in the workload list)")
+    ap.add_argument("--mode", type=int, default=2, choices=(0, 1, 2))
+    ap.add_argument("--block-n", type=int, default=None)
+    ap.add_argument("--nb", type=int, default=4)
+    ap.add_argument("--num-warps", type=int, default=4)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU: the decode path is single-device, and --gpus {args.gpus} is not supported "
+              f"(value is the one GPU's throughput)", file=sys.stderr)  # fmt: skip
+        return 2
+    if args.steps < 1:
+        print("--steps must be >= 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from comp_amd import _abi, host
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    _abi.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    value, ms_per_step, roofline, config, step_bytes = headline(torch, host, _abi, args)
+    out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8", "data": "synthetic", "config": config, "roofline": roofline,
+           "pct_peak": round(value / PEAK_GBS * 100, 2)}  # fmt: skip
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args, step_bytes, args.cpu_seconds)
+    if not args.no_detail:
+        out["detail"] = detail(torch, host, _abi, args)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -57,38 +57,41 @@ struct TimingState {
 TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
-// Pick (block_n, nb, num_warps) for a shape: cover each row's blocks in as few K steps as possible with little idle
-// slot width, then size workgroups so the grid has enough of them to fill 256 CUs.
+// Pick (block_n, nb, num_warps) for a shape.
+//   Latency regime (weights <= 64 MB, so every wave of the grid is resident at once): a wave must cover its rows in
+//   ONE K step, since each extra step adds a full HBM round trip to the wave's critical path.  Lanes per row ~ half
+//   the row's 16-byte chunks (2 chunks per lane), nb just large enough for one step, 8 waves per workgroup.
+//   Bandwidth regime (larger weights): 16 lanes per row (a short row-group reduction, many rows per wave), a few K
+//   steps, bigger workgroups so the LDS staging of the activations is amortised over more rows.
+int pow2_ceil(int64_t v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
 void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warps) {
+  const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
   const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
-  double best = -1e30;
-  int best_lpr = 16, best_nb = 8;
-  for (int lpr = 64; lpr >= 4; lpr >>= 1) {
-    for (int cand_nb = 8; cand_nb >= 1; cand_nb >>= 1) {
-      const int64_t slots = (fmt == FMT_Q4_0 ? lpr : lpr / 4) * static_cast<int64_t>(cand_nb);  // blocks per K step
-      const int64_t steps = nblk > 0 ? (nblk + slots - 1) / slots : 1;
-      const double util = nblk > 0 ? static_cast<double>(nblk) / static_cast<double>(steps * slots) : 1.0;
-      const double score = util - 0.02 * static_cast<double>(steps) - (cand_nb < 4 ? 0.05 : 0.0);
-      if (score > best + 1e-9) {
-        best = score;
-        best_lpr = lpr;
-        best_nb = cand_nb;
-      }
-    }
+  const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
+  const int64_t wbytes = n * nblk * (fmt == FMT_Q4_0 ? 18 : 66);
+  int lpr, cand_nb, w;
+  if (wbytes <= (int64_t)64 << 20) {
+    lpr = pow2_ceil((chunks + 1) / 2);
+    lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
+    const int64_t blocks_per_slot = lpr / bpb;
+    cand_nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
+    cand_nb = cand_nb < 1 ? 1 : (cand_nb > 16 ? 16 : cand_nb);
+    w = 8;
+  } else {
+    lpr = 16;
+    cand_nb = fmt == FMT_Q4_0 ? 4 : 2;
+    w = fmt == FMT_Q4_0 ? 4 : 8;
   }
-  const int rpw = 64 / best_lpr;
-  int w = 8;
-  while (w > 1) {
-    const int64_t bn = static_cast<int64_t>(w) * rpw;
-    const int64_t grid = (n + bn - 1) / bn;
-    if (bn <= 128 && grid >= 512) break;
-    if (bn / 2 < 8) break;  // block_n must stay >= 8
-    w >>= 1;
-  }
+  const int rpw = 64 / lpr;
   while (w * rpw > 128) w >>= 1;
   while (w * rpw < 8) w <<= 1;
   *block_n = w * rpw;
-  *nb = best_nb;
+  *nb = cand_nb;
   *warps = w;
 }
 

@@ -139,10 +139,8 @@ def quantize(fmt, x, bb=4, bsums=False):
     return (xq, xd, xb) if bsums else (xq, xd)
 
 
-def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store_s=False):
-    """-> (Y f32 [M][N], S int32 [M][N][blocks] or None).  mode: 0 bytes, 1 dp4a emulated, 2 dp4a (v_dot4c_i32_i8).
-
-    src/komp/host.py:76-85.  block_n=None lets the library choose block_n, nb and num_warps for the shape."""
+def _check_gemv(fmt, wq, ws, xq, xd, n, k):
+    """Validate the planes a GEMV reads (the C ABI sees raw pointers and cannot check buffer sizes)."""
     f = FORMATS[fmt]
     _need(wq, "wq", torch.uint8, 2)
     _need(ws, "ws", torch.int16, 2)
@@ -160,19 +158,72 @@ def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store
         raise _abi.KompArgumentError(f"xq must be a contiguous [M][{k}] plane, got {tuple(xq.shape)}")
     if tuple(xd.shape) != (m, nblk) or not xd.is_contiguous():
         raise _abi.KompArgumentError(f"xd must be a contiguous [{m}][{nblk}] plane, got {tuple(xd.shape)}")
-    dev = xq.device
     for t, name in ((wq, "wq"), (ws, "ws"), (xd, "xd")):
-        if t.device != dev:
-            raise _abi.KompArgumentError(f"{name} is on {t.device}, xq on {dev}")
-    y = torch.empty((m, n), dtype=torch.float32, device=dev)
-    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=dev) if store_s else None
+        if t.device != xq.device:
+            raise _abi.KompArgumentError(f"{name} is on {t.device}, xq on {xq.device}")
+    return m, nblk
+
+
+def _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps):
     if block_n is None:
         block_n, nb, num_warps = 0, 0, 0
     fn = "komp_q4_0_gemv" if fmt == "q4_0" else "komp_tq2_0_gemv"
-    with torch.cuda.device(dev):
+    with torch.cuda.device(xq.device):
         _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
-                  s.data_ptr() if store_s else None, m, n, k, wq.stride(0), block_n, nb, mode, num_warps, _stream(xq))  # fmt: skip
+                  None if s is None else s.data_ptr(), xq.shape[0], n, k, wq.stride(0), block_n, nb, mode, num_warps,
+                  _stream(xq))  # fmt: skip
+
+
+def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store_s=False):
+    """-> (Y f32 [M][N], S int32 [M][N][blocks] or None).  mode: 0 bytes, 1 dp4a emulated, 2 dp4a (v_dot4c_i32_i8).
+
+    src/komp/host.py:76-85.  block_n=None lets the library choose block_n, nb and num_warps for the shape."""
+    m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
+    y = torch.empty((m, n), dtype=torch.float32, device=xq.device)
+    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
+    _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
     return y, s
+
+
+def quantize_into(fmt, x, xq, xd, xb=None, bb=4):
+    """Allocation-free quantize: writes the q8 planes into preallocated xq / xd (and the q8_K bsums into xb).
+
+    For callers that capture HIP graphs or cannot allocate; arguments as quantize()."""
+    act = FORMATS[fmt]["act"]
+    _need(x, "x", torch.float32, 2)
+    _need(xq, "xq", torch.int8, 2)
+    _need(xd, "xd", torch.float32, 2)
+    if not (x.is_contiguous() and xq.is_contiguous() and xd.is_contiguous()):
+        raise _abi.KompArgumentError("quantize_into: x, xq and xd must be contiguous")
+    m, k = x.shape
+    blk = 32 if act == "q8_0" else 256
+    if tuple(xq.shape) != (m, k) or tuple(xd.shape) != (m, k // blk):
+        raise _abi.KompArgumentError(f"quantize_into: xq must be [{m}][{k}] and xd [{m}][{k // blk}]")
+    with torch.cuda.device(x.device):
+        if act == "q8_0":
+            _abi.call("komp_quant_q8_0", x.data_ptr(), xq.data_ptr(), xd.data_ptr(), m, k, bb, _stream(x))
+        else:
+            if xb is not None:
+                _need(xb, "xb", torch.int16, 2)
+                if tuple(xb.shape) != (m, k // 16) or not xb.is_contiguous():
+                    raise _abi.KompArgumentError(f"quantize_into: xb must be a contiguous [{m}][{k // 16}] plane")
+            _abi.call("komp_quant_q8_K", x.data_ptr(), xq.data_ptr(), xd.data_ptr(),
+                      None if xb is None else xb.data_ptr(), m, k, _stream(x))  # fmt: skip
+
+
+def gemv_into(fmt, wq, ws, xq, xd, y, n, k, block_n=None, nb=4, mode=2, num_warps=4, s=None):
+    """Allocation-free GEMV into preallocated y f32 [M][N] (and s int32 [M][N][blocks] when given).
+
+    For callers that capture HIP graphs or cannot allocate; block_n=None lets the library choose the knobs."""
+    m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
+    _need(y, "y", torch.float32, 2)
+    if tuple(y.shape) != (m, n) or not y.is_contiguous():
+        raise _abi.KompArgumentError(f"gemv_into: y must be a contiguous [{m}][{n}] tensor")
+    if s is not None:
+        _need(s, "s", torch.int32, 3)
+        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"gemv_into: s must be a contiguous [{m}][{n}][{nblk}] tensor")
+    _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
 
 
 def auto_config(fmt, m, n, k):

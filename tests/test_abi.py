@@ -1,0 +1,90 @@
+"""The C-ABI library without a GPU: it loads, exports exactly what include/komp_abi.h declares, and rejects bad
+arguments before touching the device."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from comp_amd import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "komp_abi.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|const char\*)\s+(komp_\w+)\(", text, re.M))
+
+
+def test_header_and_binding_agree():
+    assert declared() == set(_abi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (komp_\w+)", out))
+    assert exported == declared()
+
+
+def test_abi_version():
+    assert _abi.lib().komp_abi_version() == 1
+
+
+def _gemv(name="komp_q4_0_gemv", M=1, N=4, K=64, SW=32, bn=32, nb=4, mode=2, nw=4, ptr=16):
+    p = ctypes.c_void_p(ptr)
+    return getattr(_abi.lib(), name)(p, p, p, p, p, None, M, N, K, SW, bn, nb, mode, nw, None)
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(K=33), "multiple of the 32"), (dict(SW=24), "SW"), (dict(SW=16), "SW"), (dict(mode=3), "mode"),
+    (dict(bn=33), "block_n"), (dict(nb=3), "nb"), (dict(nw=16), "num_warps"), (dict(M=-1), "negative"),
+    (dict(ptr=8), "16-byte aligned"), (dict(name="komp_tq2_0_gemv", K=128, SW=32), "multiple of the 256"),
+    (dict(K=2 ** 31 + 32, SW=2 ** 30 + 16), "2^31"), (dict(K=64 * 3000, SW=96000), "LDS"),
+])  # fmt: skip
+def test_gemv_rejects_bad_arguments(kw, needle):
+    st = _gemv(**kw)
+    assert st == _abi.KOMP_EINVAL
+    assert needle in _abi.last_error()
+
+
+def test_empty_shapes_are_no_ops():
+    assert _gemv(M=0) == 0 and _gemv(N=0) == 0
+    lib = _abi.lib()
+    assert lib.komp_quant_q8_0(None, None, None, 0, 64, 4, None) == 0
+    assert lib.komp_quant_q8_K(None, None, None, None, 3, 0, None) == 0
+    assert lib.komp_dp4a_probe(None, None, None, None, 0, 2, None) == 0
+
+
+def test_quantizers_reject_bad_arguments():
+    lib = _abi.lib()
+    p = ctypes.c_void_p(16)
+    assert lib.komp_quant_q8_0(p, p, p, 1, 48, 4, None) == _abi.KOMP_EINVAL and "multiple of 32" in _abi.last_error()
+    assert lib.komp_quant_q8_0(p, p, p, 1, 64, 0, None) == _abi.KOMP_EINVAL and "bb" in _abi.last_error()
+    assert lib.komp_quant_q8_K(p, p, p, None, 1, 300, None) == _abi.KOMP_EINVAL
+    assert lib.komp_quant_q8_K(ctypes.c_void_p(8), p, p, None, 1, 256, None) == _abi.KOMP_EINVAL
+    assert lib.komp_dp4a_probe(p, p, p, p, 4, 0, None) == _abi.KOMP_EINVAL
+
+
+def test_python_errors_carry_the_message():
+    with pytest.raises(_abi.KompArgumentError, match="mode=7"):
+        _abi.check(_gemv(mode=7), "komp_q4_0_gemv")
+
+
+@pytest.mark.parametrize("fmt,n,k", [(0, 4096, 4096), (0, 128256, 4096), (0, 4097, 4192), (1, 6912, 2560),
+                                     (1, 2560, 6912), (1, 32768, 8192), (0, 1, 32), (1, 3, 256)])  # fmt: skip
+def test_auto_config_is_a_legal_knob_set(fmt, n, k):
+    bn, nb, nw = _abi.auto_config(fmt, 1, n, k)
+    assert bn in (8, 16, 32, 64, 128) and nb in (1, 2, 4, 8, 16) and nw in (1, 2, 4, 8) and bn % nw == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_abi, "_lib", None)
+    monkeypatch.setattr(_abi, "LIB_PATH", str(tmp_path / "libkomp_hip.so"))
+    with pytest.raises(_abi.KompError, match="not built"):
+        _abi.lib()
