@@ -3,14 +3,16 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--mode 2] [--no-detail] [--no-cpu]
 
-Workload (the headline): TQ2_0 (ternary, BitNet b1.58) decode steps at BitNet-2B FFN shapes.  One step quantizes an
-activation column block with quant_q8_K and runs tq2_0_gemv, for W[6912 x 2560] and then for W[2560 x 6912].  Weights
-are synthetic ternary ({-1, 0, +1} with p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), activations N(0, 1), all resident in
-HBM before the timed region.  Each step reads a different copy of both matrices (>= 1 GiB of copies), so no call is
+Workload (the headline): TQ2_0 (ternary, BitNet b1.58) decode steps at BitNet-2B FFN shapes.  One step runs the chain
+x[m][2560] -> W1[6912 x 2560] -> W2[2560 x 6912]: each GEMV quantizes its f32 input to q8_K inside the same launch
+(tq2_0_gemv_f32), so a step is two dependent dispatches.  The reference-shaped path (quant_q8_K then tq2_0_gemv, four
+dispatches) is timed beside it and must agree bit for bit.  Weights are synthetic ternary ({-1, 0, +1} with
+p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), the input N(0, 1), all resident in HBM before the timed region.  Each step reads a different copy of both matrices (>= 1 GiB of copies), so no call is
 served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-graph replays, so the host launch rate
 does not bound them.
 
-Printed: one JSON line.  value = algorithmic bytes of the K steps / their wall time (GB/s); roofline = the tq2_0_gemv
+Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in + f32 outputs)
+/ their wall time (GB/s); roofline = the tq2_0_gemv
 dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
 (the clock rocprofv3 --kernel-trace reads); cpu_baseline = the numpy oracle on a bounded sample of the same steps on
 this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold, library-chosen knobs).
@@ -137,64 +139,82 @@ def dispatch_times(abi, torch, step, count):
     return abi.timing_end()
 
 
+def step_bytes_fused(fmt, n, k, m):
+    """Algorithmic bytes of one quantize-and-GEMV: weights, f32 activations in, f32 outputs."""
+    wb = n * k * 18 // 32 if fmt == "q4_0" else n * k * 66 // 256
+    return wb + 4 * m * k + 4 * m * n
+
+
 def headline(torch, host, abi, args):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed)
     m = args.m
-    shapes = ((6912, 2560), (2560, 6912))
-    mats = []
-    for n, k in shapes:
-        copies = weight_copies("tq2_0", n, k, gen, torch, COLD_BYTES // len(shapes))
-        x = torch.randn((m, k), generator=gen, device="cuda")
-        xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
-        xd = torch.empty((m, k // 256), dtype=torch.float32, device="cuda")
-        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-        mats.append(dict(n=n, k=k, copies=copies, x=x, xq=xq, xd=xd, y=y))
-    ncopies = min(len(mt["copies"]) for mt in mats)
-    knobs = [host.auto_config("tq2_0", m, mt["n"], mt["k"]) if args.block_n is None else
-             (args.block_n, args.nb, args.num_warps) for mt in mats]  # fmt: skip
+    shapes = ((6912, 2560), (2560, 6912))  # W1 then W2; W2 reads W1's output
+    copies = [weight_copies("tq2_0", n, k, gen, torch, COLD_BYTES // len(shapes)) for n, k in shapes]
+    ncopies = min(len(c) for c in copies)
+    x = torch.randn((m, shapes[0][1]), generator=gen, device="cuda")
+    y1 = torch.empty((m, shapes[0][0]), dtype=torch.float32, device="cuda")
+    y2 = torch.empty((m, shapes[1][0]), dtype=torch.float32, device="cuda")
+    knobs = [host.auto_config("tq2_0", m, n, k) if args.block_n is None else (args.block_n, args.nb, args.num_warps)
+             for n, k in shapes]  # fmt: skip
+    (n1, k1), (n2, k2) = shapes
 
-    def step(i):
-        for mt, (bn, nb, nw) in zip(mats, knobs):
-            wq, ws = mt["copies"][i % ncopies]
-            host.quantize_into("tq2_0", mt["x"], mt["xq"], mt["xd"])
-            host.gemv_into("tq2_0", wq, ws, mt["xq"], mt["xd"], mt["y"], mt["n"], mt["k"], bn, nb, args.mode, nw)
+    def step(i):  # fused: 2 dispatches
+        w1, s1 = copies[0][i % ncopies]
+        w2, s2 = copies[1][i % ncopies]
+        host.gemv_f32_into("tq2_0", w1, s1, x, y1, n1, k1, *knobs[0][:2], args.mode, knobs[0][2])
+        host.gemv_f32_into("tq2_0", w2, s2, y1, y2, n2, k2, *knobs[1][:2], args.mode, knobs[1][2])
+
+    q1 = (torch.empty((m, k1), dtype=torch.int8, device="cuda"), torch.empty((m, k1 // 256), device="cuda"))
+    q2 = (torch.empty((m, k2), dtype=torch.int8, device="cuda"), torch.empty((m, k2 // 256), device="cuda"))
+    u1, u2 = torch.empty_like(y1), torch.empty_like(y2)
+
+    def step_two_launch(i):  # the reference's shape: quantizer then GEMV, 4 dispatches
+        w1, s1 = copies[0][i % ncopies]
+        w2, s2 = copies[1][i % ncopies]
+        host.quantize_into("tq2_0", x, *q1)
+        host.gemv_into("tq2_0", w1, s1, *q1, u1, n1, k1, *knobs[0][:2], args.mode, knobs[0][2])
+        host.quantize_into("tq2_0", u1, *q2)
+        host.gemv_into("tq2_0", w2, s2, *q2, u2, n2, k2, *knobs[1][:2], args.mode, knobs[1][2])
 
     ms, wall_ms = timed_steps(torch, step, ncopies, args.steps, args.warmup)
-    # the graph must reproduce the eager result of the same (last) step bit for bit
+    # the graph must reproduce the eager result of the same (last) step bit for bit, and the fused and two-launch
+    # paths must agree bit for bit
     last = (args.steps - 1) % ncopies
-    got = [mt["y"].clone() for mt in mats]
+    got = (y1.clone(), y2.clone())
     step(last)
+    step_two_launch(last)
     torch.cuda.synchronize()
-    for mt, gy in zip(mats, got):
-        if not torch.equal(mt["y"], gy):
-            raise RuntimeError("graph replay and eager outputs differ")
+    if not (torch.equal(y1, got[0]) and torch.equal(y2, got[1])):
+        raise RuntimeError("graph replay and eager outputs differ")
+    if not (torch.equal(y1, u1) and torch.equal(y2, u2)):
+        raise RuntimeError("fused and two-launch outputs differ")
+    ms2, _ = timed_steps(torch, step_two_launch, ncopies, args.steps, args.warmup)
 
-    step_bytes = sum(gemv_bytes("tq2_0", mt["n"], mt["k"], m) + quant_bytes("tq2_0", mt["k"], m) for mt in mats)
+    step_bytes = sum(step_bytes_fused("tq2_0", n, k, m) for n, k in shapes)
     ms_per_step = ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     disp = dispatch_times(abi, torch, step, min(args.steps, 4 * ncopies))
     g_ms, g_n = disp["tq2_0_gemv"]
-    q_ms, q_n = disp["quant_q8_K"]
-    gemv_b = sum(gemv_bytes("tq2_0", mt["n"], mt["k"], m) for mt in mats) / len(mats)
+    launch_b = step_bytes / len(shapes)
     g_us = g_ms * 1e3 / g_n
-    achieved = gemv_b / (g_us * 1e-6) / 1e9
+    achieved = launch_b / (g_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "tq2_0_gemv",
-                "dispatch_us": round(g_us, 3), "bytes_per_launch": int(gemv_b)}  # fmt: skip
-    config = {"workload": "tq2_0 decode step at BitNet-2B FFN shapes: quant_q8_K + tq2_0_gemv on W[6912x2560], "
-                          "then on W[2560x6912]",  # fmt: skip
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "tq2_0_gemv (fused quantize)",
+                "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b)}  # fmt: skip
+    config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
+                          "activations quantized to q8_K inside each launch",  # fmt: skip
               "shapes_nk": [list(s) for s in shapes], "m": m, "mode": {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}[args.mode],
               "knobs_block_n_nb_warps": [list(kn) for kn in knobs], "cold_copies": ncopies, "seed": args.seed,
-              "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3),
-              "gemv_us_per_call_dispatch": round(g_us, 3), "quant_us_per_call_dispatch": round(q_ms * 1e3 / q_n, 3),
-              "us_per_step_graph": round(ms_per_step * 1e3, 3)}  # fmt: skip
+              "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3), "us_per_step_graph": round(ms_per_step * 1e3, 3),
+              "gemv_us_per_call_dispatch": round(g_us, 3),
+              "two_launch_us_per_step_graph": round(ms2 / args.steps * 1e3, 3)}  # fmt: skip
     return value, ms_per_step, roofline, config, step_bytes
 
 
 def cpu_baseline(args, step_bytes_m, seconds=10.0):
-    """numpy oracle (this repository's restatement of the reference path) on whole steps of the same workload."""
+    """numpy oracle (this repository's restatement of the reference path) on whole steps of the same chain."""
     import numpy as np
 
     from oracle import oracle as O
@@ -207,21 +227,24 @@ def cpu_baseline(args, step_bytes_m, seconds=10.0):
         crumbs = rng.choice(3, size=(n, k), p=[0.3, 0.4, 0.3]).astype(np.uint8)
         d = rng.uniform(0.01, 0.05, size=(n, nb)).astype(np.float32).astype(np.float16).view(np.uint16)
         wq, ws = O.split("tq2_0", O.pack_tq2_0(crumbs, d), n, k)
-        mats.append((n, k, wq, ws, rng.normal(size=(m, k)).astype(np.float32)))
+        mats.append((n, k, wq, ws))
+    x0 = rng.normal(size=(m, 2560)).astype(np.float32)
     steps = 0
     t0 = time.perf_counter()
     while True:
-        for n, k, wq, ws, x in mats:
+        x = x0
+        for n, k, wq, ws in mats:
             xq, xd, _ = O.quant_q8_K(x)
-            O.gemv("tq2_0", wq, ws, xq, xd, n, k)
+            y, _ = O.gemv("tq2_0", wq, ws, xq, xd, n, k)
+            x = y.astype(np.float32)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     value = step_bytes_m * steps / el / 1e9
     return {"value": round(value, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} whole steps of the same workload (both matrices, m={m}) through the numpy oracle "
-                      f"(quant_q8_K, exact int64 block dots, f64 reference_dot) in {el:.1f} s, 1 thread; host has "
+            "sample": f"{steps} whole steps of the same chain (m={m}) through the numpy oracle (quant_q8_K, exact "
+                      f"int64 block dots, f64 reference_dot) in {el:.1f} s, 1 thread; host has "
                       f"{len(os.sched_getaffinity(0))} cores"}  # fmt: skip
 
 
@@ -245,7 +268,7 @@ def detail(torch, host, abi, args):
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         nc = len(copies)
 
-        def call(i, copies=copies, xq=xq, xd=xd, y=y, fmt=fmt, n=n, k=k):
+        def call(i, copies=copies, xq=xq, xd=xd, y=y, fmt=fmt, n=n, k=k):  # the GEMV alone, q8 activations in
             wq, ws = copies[i % nc]
             host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, 2, 0)
 

@@ -95,10 +95,23 @@ void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warp
   *warps = w;
 }
 
-int gemv_entry(int fmt, const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y,
-               int32_t* S, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
-               void* stream) {
-  const char* name = fmt == FMT_Q4_0 ? "komp_q4_0_gemv" : "komp_tq2_0_gemv";
+struct GemvArgs {
+  const uint8_t* wq;
+  const int16_t* ws;
+  const int8_t* xq;   // unfused
+  const float* xd;
+  const float* x;     // fused
+  int8_t* xq_out;
+  float* xd_out;
+  int16_t* xb_out;
+  float* y;
+  int32_t* s;
+};
+
+int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+               int mode, int num_warps, void* stream) {
+  const char* name = fused ? (fmt == FMT_Q4_0 ? "komp_q4_0_gemv_f32" : "komp_tq2_0_gemv_f32")
+                           : (fmt == FMT_Q4_0 ? "komp_q4_0_gemv" : "komp_tq2_0_gemv");
   const int blk = fmt == FMT_Q4_0 ? 32 : 256;
   const int64_t row_bytes = fmt == FMT_Q4_0 ? K / 2 : K / 4;
   if (M < 0 || N < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (M=%lld N=%lld K=%lld)", name,
@@ -116,13 +129,24 @@ int gemv_entry(int fmt, const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, 
     if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
     if (!in_set(num_warps, kWarps, 4)) return fail(KOMP_EINVAL, "%s: num_warps=%d not in {1,2,4,8}", name, num_warps);
   }
+  if (fused && fmt == FMT_Q4_0 && a.xb_out != nullptr)
+    return fail(KOMP_EINVAL, "%s: XB (bsums) is a q8_K plane; pass NULL for q4_0", name);
+  if (fused && a.xq_out == nullptr && (a.xd_out != nullptr || a.xb_out != nullptr))
+    return fail(KOMP_EINVAL, "%s: XD / XB outputs need XQ as well", name);
+  if (fused && a.xq_out != nullptr && a.xd_out == nullptr)
+    return fail(KOMP_EINVAL, "%s: the XQ output needs XD as well", name);
   if (M == 0 || N == 0) return KOMP_OK;
-  if (K > 0 && (WQ == nullptr || WS == nullptr || XQ == nullptr || XD == nullptr))
-    return fail(KOMP_EINVAL, "%s: WQ, WS, XQ and XD must not be NULL", name);
-  if (Y == nullptr) return fail(KOMP_EINVAL, "%s: Y must not be NULL", name);
-  if (!aligned(WQ, 16) || !aligned(XQ, 16)) return fail(KOMP_EINVAL, "%s: WQ and XQ must be 16-byte aligned", name);
-  if (!aligned(WS, 2) || !aligned(XD, 4) || !aligned(Y, 4) || !aligned(S, 4))
-    return fail(KOMP_EINVAL, "%s: WS, XD, Y and S must be aligned to their element size", name);
+  if (K > 0 && (a.wq == nullptr || a.ws == nullptr))
+    return fail(KOMP_EINVAL, "%s: WQ and WS must not be NULL", name);
+  if (K > 0 && !fused && (a.xq == nullptr || a.xd == nullptr))
+    return fail(KOMP_EINVAL, "%s: XQ and XD must not be NULL", name);
+  if (K > 0 && fused && a.x == nullptr) return fail(KOMP_EINVAL, "%s: X must not be NULL", name);
+  if (a.y == nullptr) return fail(KOMP_EINVAL, "%s: Y must not be NULL", name);
+  if (!aligned(a.wq, 16) || !aligned(a.xq, 16) || !aligned(a.x, 16))
+    return fail(KOMP_EINVAL, "%s: WQ, XQ and X must be 16-byte aligned", name);
+  if (!aligned(a.ws, 2) || !aligned(a.xd, 4) || !aligned(a.y, 4) || !aligned(a.s, 4) || !aligned(a.xq_out, 4) ||
+      !aligned(a.xd_out, 4) || !aligned(a.xb_out, 2))
+    return fail(KOMP_EINVAL, "%s: WS, XD, Y, S and the q8 outputs must be aligned to their element size", name);
   int mc = static_cast<int>(M < 3 ? M : 3);
   while (mc > 1 && gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax) --mc;
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
@@ -142,19 +166,21 @@ int gemv_entry(int fmt, const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, 
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
     GemvCall c;
     c.fmt = fmt;
-    c.wq = WQ;
-    c.ws = WS;
-    c.xq = XQ + m0 * K;
-    c.xd = XD + m0 * nblk;
-    c.y = Y + m0 * N;
-    c.s = S != nullptr ? S + m0 * N * nblk : nullptr;
+    c.wq = a.wq;
+    c.ws = a.ws;
+    c.xq = fused ? nullptr : a.xq + m0 * K;
+    c.xd = fused ? nullptr : a.xd + m0 * nblk;
+    c.x = fused ? a.x + m0 * K : nullptr;
+    c.xq_out = a.xq_out != nullptr ? a.xq_out + m0 * K : nullptr;
+    c.xd_out = a.xd_out != nullptr ? a.xd_out + m0 * nblk : nullptr;
+    c.xb_out = a.xb_out != nullptr ? a.xb_out + m0 * (K / 16) : nullptr;
+    c.y = a.y + m0 * N;
+    c.s = a.s != nullptr ? a.s + m0 * N * nblk : nullptr;
     c.m = static_cast<int>(M - m0 < mc ? M - m0 : mc);
     c.n = static_cast<int>(N);
     c.k = static_cast<int>(K);
     c.sw = SW;
-    c.n_total = static_cast<int>(N);
     c.mode = mode;
-    c.nontemporal = 0;
     const int st = hip_status(launch_gemv(c, plan, static_cast<hipStream_t>(stream)), name);
     if (st != KOMP_OK) return st;
   }
@@ -211,21 +237,37 @@ int komp_quant_q8_K(const float* X, int8_t* XQ, float* XD, int16_t* XB, int64_t 
   const int64_t nblocks = M * (K / 256);
   if (nblocks == 0) return KOMP_OK;
   if (X == nullptr || XQ == nullptr || XD == nullptr) return fail(KOMP_EINVAL, "komp_quant_q8_K: NULL pointer");
-  if (!aligned(X, 16) || !aligned(XQ, 4) || !aligned(XD, 4) || !aligned(XB, 2))
-    return fail(KOMP_EINVAL, "komp_quant_q8_K: X must be 16-byte aligned, XQ and XD 4-byte, XB 2-byte aligned");
+  if (!aligned(X, 16) || !aligned(XQ, 16) || !aligned(XD, 4) || !aligned(XB, 2))
+    return fail(KOMP_EINVAL, "komp_quant_q8_K: X and XQ must be 16-byte aligned, XD 4-byte, XB 2-byte aligned");
   return hip_status(launch_quant_q8_K(X, XQ, XD, XB, nblocks, static_cast<hipStream_t>(stream)), "komp_quant_q8_K");
 }
 
 int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                    void* stream) {
-  return gemv_entry(FMT_Q4_0, WQ, WS, XQ, XD, Y, S, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvArgs a{WQ, WS, XQ, XD, nullptr, nullptr, nullptr, nullptr, Y, S};
+  return gemv_entry(FMT_Q4_0, false, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                     int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                     void* stream) {
-  return gemv_entry(FMT_TQ2_0, WQ, WS, XQ, XD, Y, S, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvArgs a{WQ, WS, XQ, XD, nullptr, nullptr, nullptr, nullptr, Y, S};
+  return gemv_entry(FMT_TQ2_0, false, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                       float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                       int mode, int num_warps, void* stream) {
+  const GemvArgs a{WQ, WS, nullptr, nullptr, X, XQ, XD, XB, Y, S};
+  return gemv_entry(FMT_Q4_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                        float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                        int mode, int num_warps, void* stream) {
+  const GemvArgs a{WQ, WS, nullptr, nullptr, X, XQ, XD, XB, Y, S};
+  return gemv_entry(FMT_TQ2_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_gemv_auto_config(int fmt, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps) {

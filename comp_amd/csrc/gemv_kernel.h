@@ -1,0 +1,423 @@
+// Decode GEMVs for Q4_0 x q8_0 and TQ2_0 x q8_K on gfx950 (CDNA4).
+//
+// Replaces the reference's Triton kernels src/komp/kernels.py:48-94 (q4_0_gemv) and :97-142 (tq2_0_gemv).
+//
+// Y[m][n] = sum_b d_w(n, b) * d_x(m, b) * s(m, n, b), where s is the exact int32 dot of weight block b of row n with
+// activation block b of column m.  The weights stream once from HBM for all columns (1..3 per launch), with
+// non-temporal 16-byte loads (they are read once); the activation columns are staged in LDS once per workgroup.
+// The fused variant stages f32 activations instead: every workgroup quantizes them itself (q8_0 / q8_K, with the
+// same device functions as the quantizer kernels, so the bytes are identical) and one workgroup also writes the q8
+// planes out; that removes the separate quantizer dispatch from a decode step.
+//
+// Work decomposition (the reference's tune knobs keep their role; the mapping is this kernel's own):
+//   waves per workgroup   = num_warps
+//   rows per workgroup    = block_n; each wave owns block_n / num_warps rows ("rows per wave")
+//   lanes per row group   = 64 / min(rows per wave, 16); a wave walks its rows in passes of 64 / lanes-per-group rows
+//   nb                    = 16-byte weight chunks each lane loads per row per K step
+// A 16-byte chunk is one Q4_0 block (32 weights) or a quarter of a TQ2_0 block (64 weights).  Q4_0: lane g of a row
+// group takes blocks step*G*nb + u*G + g (u < nb, G = lanes per group), so every load instruction of the group reads
+// G*16 contiguous bytes of its row.  TQ2_0: aligned lane quads own a block; lane q of a quad takes bytes 16q..16q+15,
+// and the quad's partial dots are added with two DPP steps before the block's scale is applied.
+//
+// Integer dots (modes 1 and 2): Q4_0 dots the unsigned nibbles (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F) and starts
+// from -8 * sum(x of the block); TQ2_0 dots the crumbs and starts from -sum(x of the block) (kernels.py:72-88,
+// 122-136).  TQ2_0 masks three crumb fields in place (weights x1, x4, x16 in three accumulators) and shifts only the
+// fourth, which the x16 accumulator also takes; the block dot is (a1 * 16 + a4 * 4 + a16) / 16, exact in int32.
+// Mode 0 unpacks every weight and activation to int32 first (kernels.py:65-71, 115-121).
+#pragma once
+
+#include <hip/hip_ext.h>
+
+#include "komp_device.h"
+#include "komp_internal.h"
+
+namespace komp {
+namespace gemv_impl {
+
+constexpr unsigned NIB = 0x0F0F0F0Fu;
+constexpr unsigned ONES = 0x01010101u;
+
+// Q4_0: exact int32 dot of one block (16 quant bytes) with its 32 activations; xl = values 0..15, xh = 16..31.
+template <int MODE>
+__device__ __forceinline__ int q4_0_block_dot(u32x4 w, u32x4 xl, u32x4 xh, int corr) {
+  if constexpr (MODE == MODE_BYTES) {
+    int s = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int lo = static_cast<int>((w[d] >> (8 * e)) & 15u) - 8;
+        const int hi = static_cast<int>((w[d] >> (8 * e + 4)) & 15u) - 8;
+        s += lo * sbyte(xl[d], e) + hi * sbyte(xh[d], e);
+      }
+    }
+    return s;
+  } else {
+    int s = corr;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      s = dot4<MODE>(w[d] & NIB, xl[d], s);
+      s = dot4<MODE>((w[d] >> 4) & NIB, xh[d], s);
+    }
+    return s;
+  }
+}
+
+// TQ2_0: partial int32 dot of one 16-byte chunk.  Byte t of the chunk holds, at bits 2j, the value whose activation
+// is byte t of x[j].  `init` joins the x1 accumulator.
+template <int MODE>
+__device__ __forceinline__ int tq2_0_chunk_dot(u32x4 w, const u32x4 (&x)[4], int init) {
+  if constexpr (MODE == MODE_BYTES) {
+    int s = init;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned byte = (w[d] >> (8 * e)) & 0xFFu;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += (static_cast<int>((byte >> (2 * j)) & 3u) - 1) * sbyte(x[j][d], e);
+      }
+    }
+    return s;
+  } else {
+    int a1 = init, a4 = 0, a16 = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      a1 = dot4<MODE>(w[d] & 0x03030303u, x[0][d], a1);
+      a4 = dot4<MODE>(w[d] & 0x0C0C0C0Cu, x[1][d], a4);
+      a16 = dot4<MODE>(w[d] & 0x30303030u, x[2][d], a16);
+      a16 = dot4<MODE>((w[d] >> 2) & 0x30303030u, x[3][d], a16);
+    }
+    return ((a1 << 4) + (a4 << 2) + a16) >> 4;
+  }
+}
+
+template <int FMT, int MODE, int MC, int NB, bool FUSED>
+__global__ void __launch_bounds__(512)
+gemv_kernel(const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, const int8_t* __restrict__ XQ,
+            const float* __restrict__ XD, const float* __restrict__ X, int8_t* __restrict__ XQo,
+            float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y, int32_t* __restrict__ S, int N,
+            int K, int64_t SW, int rows_per_wg, int lpr_log2, int passes) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr int BLK = FMT == FMT_Q4_0 ? 32 : 256;
+  constexpr int BB = FMT == FMT_Q4_0 ? 16 : 64;  // quant bytes per block
+  const int nblk = K / BLK;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lpr = 1 << lpr_log2;
+  const int gl = lane & (lpr - 1);
+  const int grp = lane >> lpr_log2;
+  const int rows_per_pass = 64 >> lpr_log2;
+  const int rows_per_wave = rows_per_wg / (nthreads >> 6);
+  const int row_base = blockIdx.x * rows_per_wg + wave * rows_per_wave;  // wave-uniform
+  const int bpg = FMT == FMT_Q4_0 ? lpr : (lpr >> 2);  // blocks a row group covers per chunk slot
+  const int bstep = bpg * NB;                            // blocks a row group covers per K step
+  const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
+  const int q = gl & 3;                                  // TQ2_0: chunk of the block this lane loads
+  const int gblk = FMT == FMT_Q4_0 ? gl : (gl >> 2);     // block offset of this lane within a slot
+  const int tiles = passes * nsteps;
+  // per-lane byte offsets within a row group's tile (row grp of the group, block gblk, chunk q)
+  const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + (FMT == FMT_Q4_0 ? 0 : q * 16);
+  const int64_t lane_s = static_cast<int64_t>(grp) * nblk + gblk;
+
+  u32x4 w[NB];
+  int16_t sc[NB];
+  auto load_tile = [&](int t) {
+    const int p = t / nsteps;
+    const int st = t - p * nsteps;
+    const int rl = p * rows_per_pass + grp;
+    const bool rv = rl < rows_per_wave && row_base + rl < N;
+    const int64_t row0 = static_cast<int64_t>(row_base) + p * rows_per_pass;  // wave-uniform
+    const uint8_t* wt = WQ + row0 * SW + static_cast<int64_t>(st) * bstep * BB + lane_w;
+    const int16_t* stp = WS + row0 * nblk + st * bstep + lane_s;
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int b = st * bstep + u * bpg + gblk;
+      if (rv && b < nblk) {
+        w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + static_cast<int64_t>(u) * bpg * BB));
+        sc[u] = stp[u * bpg];
+      } else {
+        w[u] = u32x4{0u, 0u, 0u, 0u};
+        sc[u] = 0;
+      }
+    }
+  };
+
+  // Issue the first tile's weight loads before staging the activations, so HBM latency overlaps the staging.
+  load_tile(0);
+
+  // ---- stage the activation columns in LDS ----
+  // Q4_0: xlo[m][b] = activations 0..15 of block b, xhi[m][b] = 16..31, meta[m][b] = {d_x bits, -8 * sum(x)}.
+  // TQ2_0: x4[m][j][b][q] = the 16 activations that pair with crumb j of chunk q; meta[m][b] = {d_x bits, -sum(x)}.
+  u32x4* xv = reinterpret_cast<u32x4*>(lds);
+  int2* meta = reinterpret_cast<int2*>(xv + (FMT == FMT_Q4_0 ? 2 : 16) * MC * nblk);
+  // Each loop below issues the global loads of up to SU iterations before using any of them, so a workgroup pays one
+  // memory round trip per SU iterations of staging rather than one per iteration.  The unfused loops finish in one
+  // iteration for every shape that fits LDS with 256+ lanes, and extra staging registers would cut the occupancy of
+  // the weight stream, so they use SU = 1.
+  constexpr int SU = FUSED ? 2 : 1;
+  if constexpr (FMT == FMT_Q4_0 && !FUSED) {
+    const int total = MC * nblk;
+    for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
+      u32x4 a[SU], c[SU];
+      float dxs[SU];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int m = i / nblk;
+          const u32x4* src = reinterpret_cast<const u32x4*>(XQ + static_cast<int64_t>(m) * K + (i - m * nblk) * 32);
+          a[u] = src[0];
+          c[u] = src[1];
+          dxs[u] = XD[i];  // XD [M][nblk] is dense: block (m, b) at m * nblk + b = i
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int m = i / nblk;
+          const int b = i - m * nblk;
+          xv[i] = a[u];
+          xv[MC * nblk + i] = c[u];
+          int sum = 0;
+          if constexpr (MODE != MODE_BYTES) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              sum = dot4<MODE>(a[u][d], ONES, sum);
+              sum = dot4<MODE>(c[u][d], ONES, sum);
+            }
+          }
+          meta[i] = make_int2(__float_as_int(dxs[u]), -8 * sum);
+        }
+      }
+    }
+  } else if constexpr (FMT == FMT_Q4_0) {
+    // 8 consecutive lanes quantize one block (lane e holds values 4e..4e+3); groups of 8 stay aligned and whole.
+    const int total = MC * nblk * 8;
+    for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
+      f32x4 v[SU];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int mb = i >> 3;
+          const int m = mb / nblk;
+          v[u] = *reinterpret_cast<const f32x4*>(X + static_cast<int64_t>(m) * K + (mb - m * nblk) * 32 + (i & 7) * 4);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int e = i & 7;
+          const int mb = i >> 3;
+          const int m = mb / nblk;
+          const int b = mb - m * nblk;
+          float d;
+          int qsum;
+          const unsigned packed = q8_0_group8(v[u], d, qsum);
+          reinterpret_cast<unsigned*>(xv + (e < 4 ? mb : MC * nblk + mb))[e & 3] = packed;
+          if (e == 0) meta[mb] = make_int2(__float_as_int(d), -8 * qsum);
+          if (blockIdx.x == 0 && XQo != nullptr) {
+            reinterpret_cast<unsigned*>(XQo + static_cast<int64_t>(m) * K + b * 32)[e] = packed;
+            if (e == 0) XDo[static_cast<int64_t>(m) * nblk + b] = d;
+          }
+        }
+      }
+    }
+  } else if constexpr (!FUSED) {
+    // 16 consecutive lanes stage one block: piece p = 16 contiguous activation bytes at 16p (h = p >> 3,
+    // j = (p >> 1) & 3, half = p & 1).  nthreads is a multiple of 64, so the 16-lane groups stay aligned and whole.
+    const int total = MC * nblk * 16;
+    for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
+      u32x4 a[SU];
+      float dxs[SU];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int mb = i >> 4;
+          const int m = mb / nblk;
+          a[u] = *reinterpret_cast<const u32x4*>(XQ + static_cast<int64_t>(m) * K + (mb - m * nblk) * 256 + (i & 15) * 16);
+          dxs[u] = XD[mb];  // XD [M][nblk] is dense: block (m, b) at m * nblk + b = mb
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int p = i & 15;
+          const int mb = i >> 4;
+          const int m = mb / nblk;
+          const int b = mb - m * nblk;
+          const int j = (p >> 1) & 3;
+          const int qq = ((p >> 3) << 1) | (p & 1);
+          xv[((m * 4 + j) * nblk + b) * 4 + qq] = a[u];
+          int sum = 0;
+          if constexpr (MODE != MODE_BYTES) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) sum = dot4<MODE>(a[u][d], ONES, sum);
+            sum = group_sum(sum, 16);
+          }
+          if (p == 0) meta[mb] = make_int2(__float_as_int(dxs[u]), -sum);
+        }
+      }
+    }
+  } else {
+    // 16 consecutive lanes quantize one block: lane r holds values 16r..16r+15, which are exactly one bsum group and
+    // exactly the LDS piece (j = (r % 8) / 2, chunk q = 2 (r / 8) + r % 2); rows of 16 stay aligned and whole.
+    const int total = MC * nblk * 16;
+    for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
+      f32x4 v[SU][4];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int mb = i >> 4;
+          const int m = mb / nblk;
+          const f32x4* src = reinterpret_cast<const f32x4*>(X + static_cast<int64_t>(m) * K + (mb - m * nblk) * 256 +
+                                                            (i & 15) * 16);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[u][t] = src[t];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int i = i0 + u * nthreads;
+        if (i < total) {
+          const int r = i & 15;
+          const int mb = i >> 4;
+          const int m = mb / nblk;
+          const int b = mb - m * nblk;
+          u32x4 qv;
+          float d;
+          int qsum;
+          const int bsum = q8_K_row16(v[u], r, qv, d, qsum);
+          const int j = (r & 7) >> 1;
+          const int qq = ((r >> 3) << 1) | (r & 1);
+          xv[((m * 4 + j) * nblk + b) * 4 + qq] = qv;
+          if (r == 0) meta[mb] = make_int2(__float_as_int(d), -qsum);
+          if (blockIdx.x == 0 && XQo != nullptr) {
+            reinterpret_cast<u32x4*>(XQo + static_cast<int64_t>(m) * K + b * 256)[r] = qv;
+            if (r == 0) XDo[static_cast<int64_t>(m) * nblk + b] = d;
+            if (XBo != nullptr) XBo[static_cast<int64_t>(mb) * 16 + r] = static_cast<int16_t>(bsum);
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- stream the weights ----
+  float acc[MC];
+  for (int t = 0; t < tiles; ++t) {
+    if (t > 0) load_tile(t);
+    const int p = t / nsteps;
+    const int st = t - p * nsteps;
+    const int rl = p * rows_per_pass + grp;
+    const int row = row_base + rl;
+    const bool rv = rl < rows_per_wave && row < N;
+    if (st == 0) {
+#pragma unroll
+      for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int b = st * bstep + u * bpg + gblk;
+      if (b < nblk) {
+        const float dw = f16_bits_to_f32(sc[u]);
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+          const int2 mt = meta[m * nblk + b];
+          const float dx = __int_as_float(mt.x);
+          if constexpr (FMT == FMT_Q4_0) {
+            const int s = q4_0_block_dot<MODE>(w[u], xv[m * nblk + b], xv[(MC + m) * nblk + b], mt.y);
+            if (S != nullptr && rv) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
+            acc[m] += static_cast<float>(s) * dw * dx;  // kernels.py:93 order
+          } else {
+            u32x4 xs[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xs[j] = xv[((m * 4 + j) * nblk + b) * 4 + q];
+            const int init = (MODE != MODE_BYTES && q == 0) ? mt.y : 0;
+            const int s = group_sum(tq2_0_chunk_dot<MODE>(w[u], xs, init), 4);
+            if (S != nullptr && rv && q == 0) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
+            const float f = dx * dw * static_cast<float>(s);  // kernels.py:141 order
+            acc[m] += q == 0 ? f : 0.0f;
+          }
+        }
+      }
+    }
+    if (st == nsteps - 1) {
+#pragma unroll
+      for (int m = 0; m < MC; ++m) {
+        const float v = group_sum(acc[m], lpr);
+        if (gl == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+      }
+    }
+  }
+}
+
+template <int FMT, int MODE, int MC, int NB, bool FUSED>
+hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+  auto kern = gemv_kernel<FMT, MODE, MC, NB, FUSED>;
+  const dim3 grid(static_cast<unsigned>((c.n + p.block_n - 1) / p.block_n));
+  const dim3 block(static_cast<unsigned>(64 * p.waves));
+  const unsigned lds = static_cast<unsigned>(gemv_lds_bytes(FMT, MC, c.k));
+  static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
+  if (lds > lds_attr) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    lds_attr = lds;
+  }
+  const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
+  if (tm.on) {
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
+                          c.xd_out, c.xb_out, c.y, c.s, c.n, c.k, c.sw, p.block_n, p.lpr_log2, p.passes);
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y,
+                       c.s, c.n, c.k, c.sw, p.block_n, p.lpr_log2, p.passes);
+  }
+  return hipGetLastError();
+}
+
+template <int FMT, int MODE, int MC, bool FUSED>
+hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (p.nb) {
+    case 1: return launch_t<FMT, MODE, MC, 1, FUSED>(c, p, s);
+    case 2: return launch_t<FMT, MODE, MC, 2, FUSED>(c, p, s);
+    case 4: return launch_t<FMT, MODE, MC, 4, FUSED>(c, p, s);
+    case 8: return launch_t<FMT, MODE, MC, 8, FUSED>(c, p, s);
+    case 16: return launch_t<FMT, MODE, MC, 16, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int FMT, int MODE, bool FUSED>
+hipError_t by_mc(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (c.m) {
+    case 1: return by_nb<FMT, MODE, 1, FUSED>(c, p, s);
+    case 2: return by_nb<FMT, MODE, 2, FUSED>(c, p, s);
+    case 3: return by_nb<FMT, MODE, 3, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int FMT, bool FUSED>
+hipError_t by_mode(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (c.mode) {
+    case MODE_BYTES: return by_mc<FMT, MODE_BYTES, FUSED>(c, p, s);
+    case MODE_DP4A_EMU: return by_mc<FMT, MODE_DP4A_EMU, FUSED>(c, p, s);
+    case MODE_DP4A: return by_mc<FMT, MODE_DP4A, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gemv_impl
+
+size_t gemv_lds_bytes(int fmt, int m, int k);
+
+}  // namespace komp

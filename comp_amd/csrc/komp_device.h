@@ -83,4 +83,89 @@ __device__ __forceinline__ float round_half_away(float x) {
   return copysignf(r, x);
 }
 
+// ---- activation quantizers (patch:104-131), shared by the quantizer kernels and the fused GEMV staging -------------
+
+// ggml q8_0 on one block of 32 values held by 8 aligned lanes (4 consecutive values each).  Returns this lane's 4
+// quantized values packed in a dword (value e in byte e); d_store receives f32(f16(d)) (the stored scale, RTNE), and
+// qsum the block's sum of q (every lane of the group receives it).
+__device__ __forceinline__ unsigned q8_0_group8(f32x4 v, float& d_store, int& qsum) {
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
+  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
+  const float d = a / 127.0f;  // correctly rounded (no fast-math)
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  unsigned packed = 0;
+  int sum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int qv = static_cast<int>(round_half_away(v[e] * id));  // q from the unrounded d
+    sum += qv;
+    packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
+  }
+  sum += dpp_i<KOMP_DPP_XOR1>(sum);
+  sum += dpp_i<KOMP_DPP_XOR2>(sum);
+  sum += dpp_i<KOMP_DPP_HALF_MIRROR>(sum);
+  qsum = sum;
+  d_store = __half2float(__float2half_rn(d));
+  return packed;
+}
+
+// Sum / max / min over each aligned 16-lane DPP row; every lane of the row receives the row's result.
+__device__ __forceinline__ float row16_max_f(float v) {
+  v = fmaxf(v, dpp_f<KOMP_DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f<KOMP_DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f<KOMP_DPP_HALF_MIRROR>(v));
+  return fmaxf(v, dpp_f<KOMP_DPP_MIRROR>(v));
+}
+__device__ __forceinline__ int row16_min_i(int v) {
+  v = min(v, dpp_i<KOMP_DPP_XOR1>(v));
+  v = min(v, dpp_i<KOMP_DPP_XOR2>(v));
+  v = min(v, dpp_i<KOMP_DPP_HALF_MIRROR>(v));
+  return min(v, dpp_i<KOMP_DPP_MIRROR>(v));
+}
+
+// ggml q8_K on one block of 256 values held by an aligned 16-lane row (lane r of the row holds values 16r..16r+15 in
+// v[0..3]); the whole row must be active.  Writes the lane's 16 q into qout (value 4t+e in byte e of qout[t]) and
+// returns the lane's sum of its 16 q, which is exactly bsum r of the block; d_out receives d (0 for an all-zero
+// block) and qsum the block's sum of q.
+__device__ __forceinline__ int q8_K_row16(const f32x4 (&v)[4], int r, u32x4& qout, float& d_out, int& qsum) {
+  float a = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    a = fmaxf(a, fmaxf(fmaxf(fabsf(v[t][0]), fabsf(v[t][1])), fmaxf(fabsf(v[t][2]), fabsf(v[t][3]))));
+  const float amax = row16_max_f(a);
+  // the first index whose |x| equals amax (patch:124), and x at that index
+  int local = 16;
+#pragma unroll
+  for (int t = 3; t >= 0; --t)
+#pragma unroll
+    for (int e = 3; e >= 0; --e) local = fabsf(v[t][e]) == amax ? 4 * t + e : local;
+  const int first = row16_min_i(local < 16 ? 16 * r + local : 256);
+  float mine = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mine = (16 * r + 4 * t + e == first) ? v[t][e] : mine;
+  // exactly one lane of the row owns `first`: adding the owner's bits to zeros broadcasts them exactly
+  const float mx = __int_as_float(group_sum(16 * r + local == first ? __float_as_int(mine) : 0, 16));
+  const bool nz = amax != 0.0f;
+  const float iscale = -127.0f / (nz ? mx : 1.0f);
+  int s16 = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    unsigned packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int qv = nz ? static_cast<int>(fminf(rintf(iscale * v[t][e]), 127.0f)) : 0;
+      s16 += qv;
+      packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
+    }
+    qout[t] = packed;
+  }
+  qsum = group_sum(s16, 16);
+  d_out = nz ? 1.0f / iscale : 0.0f;
+  return s16;
+}
+
 }  // namespace komp

@@ -24,17 +24,19 @@ struct GemvCall {
   int fmt;
   const uint8_t* wq;
   const int16_t* ws;
-  const int8_t* xq;
+  const int8_t* xq;   // q8 activations (unfused) ...
   const float* xd;
+  const float* x;     // ... or f32 activations, quantized by every workgroup into LDS (fused)
+  int8_t* xq_out;     // fused only, optional: the q8 planes as quant_q8_0 / quant_q8_K would write them
+  float* xd_out;
+  int16_t* xb_out;    // q8_K bsums, optional
   float* y;
   int32_t* s;
   int m;          // activation columns in this launch (1..3)
   int n;
   int k;
   int64_t sw;     // WQ row stride in bytes
-  int n_total;    // rows of the full Y / S planes (S offsets use it)
   int mode;
-  int nontemporal;
 };
 
 // Dispatch hook: every launch goes through it so the tuning harness can time dispatches with hipExtLaunchKernel events.
@@ -47,6 +49,7 @@ Timing timing_slot(int kind);   // defined in komp_abi.cpp
 
 size_t gemv_lds_bytes(int fmt, int m, int k);
 hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,

@@ -19,69 +19,36 @@ __global__ void __launch_bounds__(QUANT_THREADS)
 quant_q8_0_kernel(const float* __restrict__ X, int8_t* __restrict__ XQ, float* __restrict__ XD, int64_t nblocks) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * QUANT_THREADS + threadIdx.x;
   const int64_t blk = gid >> 3;
-  const bool valid = blk < nblocks;
-  f32x4 v = valid ? reinterpret_cast<const f32x4*>(X)[gid] : f32x4{0.f, 0.f, 0.f, 0.f};
-  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
-  const float d = a / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  unsigned packed = 0;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int qv = static_cast<int>(round_half_away(v[e] * id));
-    packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
-  }
+  const bool valid = blk < nblocks;  // a group of 8 lanes is wholly valid or not
+  const f32x4 v = valid ? reinterpret_cast<const f32x4*>(X)[gid] : f32x4{0.f, 0.f, 0.f, 0.f};
+  float d;
+  int qsum;
+  const unsigned packed = q8_0_group8(v, d, qsum);
   if (valid) {
     reinterpret_cast<unsigned*>(XQ)[gid] = packed;
-    if ((gid & 7) == 0) XD[blk] = __half2float(__float2half_rn(d));
+    if ((gid & 7) == 0) XD[blk] = d;
   }
 }
 
-// q8_K: one wavefront per block of 256 (4 values per lane), 4 blocks per workgroup.  bsums (XB) are optional.
+// q8_K: 16 lanes per block of 256 (16 consecutive values each, four 16-byte loads), 16 blocks per 256-lane
+// workgroup.  Each lane's 16 values are exactly one bsum group.  bsums (XB) are optional.
 __global__ void __launch_bounds__(QUANT_THREADS)
 quant_q8_K_kernel(const float* __restrict__ X, int8_t* __restrict__ XQ, float* __restrict__ XD,
                   int16_t* __restrict__ XB, int64_t nblocks) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * QUANT_THREADS + threadIdx.x;
-  const int64_t blk = gid >> 6;
-  if (blk >= nblocks) return;  // whole wavefronts leave together: a wavefront is one block
-  const int lane = threadIdx.x & 63;
-  const f32x4 v = reinterpret_cast<const f32x4*>(X)[gid];
-  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_MIRROR>(a));
-  a = fmaxf(a, __shfl_xor(a, 16, 64));
-  const float amax = fmaxf(a, __shfl_xor(a, 32, 64));
-  // first index whose |x| equals amax (patch:124)
-  int first = 256;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * QUANT_THREADS + threadIdx.x;  // one 16-value group per lane
+  const int64_t blk = gid >> 4;
+  if (blk >= nblocks) return;  // rows of 16 lanes leave together: a row is one block
+  const int r = static_cast<int>(gid & 15);
+  f32x4 v[4];
 #pragma unroll
-  for (int e = 3; e >= 0; --e) first = fabsf(v[e]) == amax ? lane * 4 + e : first;
-  first = min(first, __shfl_xor(first, 1, 64));
-  first = min(first, __shfl_xor(first, 2, 64));
-  first = min(first, __shfl_xor(first, 4, 64));
-  first = min(first, __shfl_xor(first, 8, 64));
-  first = min(first, __shfl_xor(first, 16, 64));
-  first = min(first, __shfl_xor(first, 32, 64));
-  const int fe = first & 3;
-  const float mine = fe == 0 ? v[0] : fe == 1 ? v[1] : fe == 2 ? v[2] : v[3];
-  const float mx = __shfl(mine, (first >> 2) & 63, 64);
-  const bool nz = amax != 0.0f;
-  const float iscale = -127.0f / (nz ? mx : 1.0f);
-  unsigned packed = 0;
-  int bsum = 0;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int qv = nz ? static_cast<int>(fminf(rintf(iscale * v[e]), 127.0f)) : 0;
-    bsum += qv;
-    packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
-  }
-  reinterpret_cast<unsigned*>(XQ)[gid] = packed;
-  bsum = group_sum(bsum, 4);
-  if (XB != nullptr && (lane & 3) == 0) XB[blk * 16 + (lane >> 2)] = static_cast<int16_t>(bsum);
-  if (lane == 0) XD[blk] = nz ? 1.0f / iscale : 0.0f;
+  for (int t = 0; t < 4; ++t) v[t] = reinterpret_cast<const f32x4*>(X)[gid * 4 + t];
+  u32x4 q;
+  float d;
+  int qsum;
+  const int bsum = q8_K_row16(v, r, q, d, qsum);
+  reinterpret_cast<u32x4*>(XQ)[gid] = q;
+  if (XB != nullptr) XB[gid] = static_cast<int16_t>(bsum);
+  if (r == 0) XD[blk] = d;
 }
 
 __global__ void dp4a_probe_kernel(const int32_t* __restrict__ A, const int32_t* __restrict__ B,
@@ -153,7 +120,7 @@ hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblo
 }
 
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream) {
-  return launch(KIND_QUANT_Q8_K, quant_q8_K_kernel, dim3(blocks_for(nblocks * 64, QUANT_THREADS)),
+  return launch(KIND_QUANT_Q8_K, quant_q8_K_kernel, dim3(blocks_for(nblocks * 16, QUANT_THREADS)),
                 dim3(QUANT_THREADS), stream, x, xq, xd, xb, nblocks);
 }
 

@@ -226,6 +226,79 @@ def gemv_into(fmt, wq, ws, xq, xd, y, n, k, block_n=None, nb=4, mode=2, num_warp
     _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
 
 
+def _check_weights(fmt, wq, ws, n, k):
+    f = FORMATS[fmt]
+    _need(wq, "wq", torch.uint8, 2)
+    _need(ws, "ws", torch.int16, 2)
+    if wq.stride(1) != 1:
+        raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
+    nblk = k // f["block"]
+    if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{nblk}] plane, got {tuple(ws.shape)}")
+    if wq.shape[0] != n or wq.shape[1] < nblk * f["qbytes"]:
+        raise _abi.KompArgumentError(f"wq must be [{n}][>= {nblk * f['qbytes']}], got {tuple(wq.shape)}")
+    return nblk
+
+
+def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps=4, s=None, xq=None, xd=None,
+                  xb=None):  # fmt: skip
+    """Quantize-and-GEMV in one launch into preallocated outputs: x f32 [M][K] -> y f32 [M][N] (and s, and the q8
+    planes xq / xd / xb when given, as quantize() would return them).  Bit-identical to quantize() then gemv()."""
+    nblk = _check_weights(fmt, wq, ws, n, k)
+    _need(x, "x", torch.float32, 2)
+    if x.shape[1] != k or not x.is_contiguous():
+        raise _abi.KompArgumentError(f"x must be a contiguous [M][{k}] tensor, got {tuple(x.shape)}")
+    m = x.shape[0]
+    _need(y, "y", torch.float32, 2)
+    if tuple(y.shape) != (m, n) or not y.is_contiguous():
+        raise _abi.KompArgumentError(f"y must be a contiguous [{m}][{n}] tensor")
+    if s is not None:
+        _need(s, "s", torch.int32, 3)
+        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"s must be a contiguous [{m}][{n}][{nblk}] tensor")
+    ablk = FORMATS[fmt]["block"]
+    for t, name, dt, shape in ((xq, "xq", torch.int8, (m, k)), (xd, "xd", torch.float32, (m, k // ablk)),
+                               (xb, "xb", torch.int16, (m, k // 16))):  # fmt: skip
+        if t is not None:
+            _need(t, name, dt, 2)
+            if tuple(t.shape) != shape or not t.is_contiguous():
+                raise _abi.KompArgumentError(f"{name} must be a contiguous {list(shape)} tensor")
+    for t, name in ((wq, "wq"), (ws, "ws"), (y, "y")):
+        if t.device != x.device:
+            raise _abi.KompArgumentError(f"{name} is on {t.device}, x on {x.device}")
+    if block_n is None:
+        block_n, nb, num_warps = 0, 0, 0
+    fn = "komp_q4_0_gemv_f32" if fmt == "q4_0" else "komp_tq2_0_gemv_f32"
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    with torch.cuda.device(x.device):
+        _abi.call(fn, wq.data_ptr(), ws.data_ptr(), x.data_ptr(), y.data_ptr(), ptr(s), ptr(xq), ptr(xd), ptr(xb), m, n,
+                  k, wq.stride(0), block_n, nb, mode, num_warps, _stream(x))  # fmt: skip
+
+
+def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, store_s=False, return_q=False):
+    """Quantize-and-GEMV in one launch: x f32 [M][K] -> (Y f32 [M][N], S or None[, (XQ, XD[, XB])]).
+
+    Every workgroup quantizes x (q8_0 for q4_0, q8_K for tq2_0) with the quantizer kernels' arithmetic, so the result
+    equals quantize() followed by gemv() bit for bit, with one dispatch instead of two.  return_q also returns the q8
+    planes (and the q8_K bsums).  No reference counterpart (the reference launches the two kernels separately)."""
+    _need(x, "x", torch.float32, 2)
+    x = x.contiguous()
+    m = x.shape[0]
+    blk = FORMATS[fmt]["block"]
+    if k % blk:
+        raise _abi.KompArgumentError(f"{fmt}: K={k} is not a multiple of {blk}")
+    y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    s = torch.zeros((m, n, k // blk), dtype=torch.int32, device=x.device) if store_s else None
+    q = None
+    if return_q:
+        q = (torch.empty((m, k), dtype=torch.int8, device=x.device),
+             torch.empty((m, k // blk), dtype=torch.float32, device=x.device))  # fmt: skip
+        if fmt == "tq2_0":
+            q = q + (torch.empty((m, k // 16), dtype=torch.int16, device=x.device),)
+    gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n, nb, mode, num_warps, s, *(q or ()))
+    return (y, s, q) if return_q else (y, s)
+
+
 def auto_config(fmt, m, n, k):
     """(block_n, nb, num_warps) that gemv(..., block_n=None) uses for this shape."""
     return _abi.auto_config(FMT_ID[fmt], m, n, k)

@@ -46,7 +46,8 @@ const char* komp_last_error(void);
  * Replaces: host.quantize q8_0 branch (src/komp/host.py:63-69) launching kernels.quant_q8_0 (src/komp/kernels.py:22-33). */
 int komp_quant_q8_0(const float* X, int8_t* XQ, float* XD, int64_t M, int64_t K, int bb, void* stream);
 
-/* f32 X [M][K] -> q8_K planes XQ, XD and, when XB is not NULL, the bsums XB [M][K/16].  K % 256 == 0.
+/* f32 X [M][K] -> q8_K planes XQ, XD and, when XB is not NULL, the bsums XB [M][K/16].  K % 256 == 0; X and XQ
+ * 16-byte aligned.
  * Replaces: host.quantize q8_K branch (src/komp/host.py:70-72) launching kernels.quant_q8_K (src/komp/kernels.py:36-45);
  * the bsums, which the reference computes on the host (src/komp/host.py:50), come from the kernel. */
 int komp_quant_q8_K(const float* X, int8_t* XQ, float* XD, int16_t* XB, int64_t M, int64_t K, void* stream);
@@ -66,6 +67,20 @@ int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const
 int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                     int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                     void* stream);
+
+/* Quantize-and-GEMV in one launch: X is f32 [M][K] (16-byte aligned); every workgroup quantizes it (q8_0 for q4_0,
+ * q8_K for tq2_0) into LDS with the quantizer kernels' arithmetic, then runs the GEMV, so Y and S equal
+ * komp_quant_q8_* followed by komp_*_gemv bit for bit.  When XQ is not NULL, one workgroup also writes the q8 planes
+ * XQ [M][K] and XD (required with XQ), and for tq2_0 the bsums XB [M][K/16] when XB is not NULL (XB must be NULL for
+ * q4_0).  Other arguments as komp_q4_0_gemv / komp_tq2_0_gemv.
+ * No reference counterpart: the reference launches its quantizer and its GEMV separately (src/komp/host.py:63-85);
+ * this removes one dispatch per GEMV from a decode step. */
+int komp_q4_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                       float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                       int mode, int num_warps, void* stream);
+int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                        float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                        int mode, int num_warps, void* stream);
 
 /* The (block_n, nb, num_warps) that block_n == 0 selects for a GEMV shape; fmt 0 = q4_0, 1 = tq2_0.
  * No reference counterpart: the reference always takes the knobs from its caller. */

@@ -1,0 +1,53 @@
+"""The fused quantize-and-GEMV launch equals quantize() followed by gemv() bit for bit (Y, S and the q8 planes),
+for every mode, edge data, tails and 1..4 columns."""
+
+import numpy as np
+import pytest
+import torch
+
+from comp_amd import host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+CASES = [("q4_0", 37, 416, 3), ("q4_0", 4097, 4192, 1), ("q4_0", 64, 512, 4), ("tq2_0", 37, 768, 3),
+         ("tq2_0", 6913, 2816, 2), ("tq2_0", 5, 1280, 1)]  # fmt: skip
+
+
+@pytest.mark.parametrize("fmt,n,k,m", CASES)
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("extreme", [False, True])
+@pytest.mark.parametrize("knobs", [(32, 4, 4), None])
+def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
+    W, x = O.problem(fmt, n, k, m, 40 + extreme, extreme)
+    wq, ws = host.split(fmt, W, n, k)
+    wq, ws, xg = dev(wq), dev(ws), dev(x)
+    bn, nb, nw = knobs if knobs else (None, 0, 0)
+    y1, s1, q = host.gemv_f32(fmt, wq, ws, xg, n, k, bn, nb, mode, nw, store_s=True, return_q=True)
+    qq = host.quantize(fmt, xg, bsums=(fmt == "tq2_0"))
+    y2, s2 = host.gemv(fmt, wq, ws, qq[0], qq[1], n, k, bn, nb, mode, nw, store_s=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s1, s2)
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    for a, b in zip(q, qq):
+        assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int16 else a, b.view(torch.uint8) if b.dtype != torch.int16 else b)
+    rq, rd, rb = O.quantize(fmt, x)
+    assert np.array_equal(q[0].cpu().numpy(), rq)
+    r, rs = O.gemv(fmt, host.split(fmt, W, n, k)[0], host.split(fmt, W, n, k)[1], rq, rd, n, k)
+    assert np.array_equal(s1.cpu().numpy().astype(np.int64), rs)
+    assert O.relerr(y1.cpu().numpy(), r) <= 1e-5
+
+
+def test_fused_without_q_outputs():
+    fmt, n, k, m = "tq2_0", 2560, 6912, 1
+    W, x = O.problem(fmt, n, k, m, 7)
+    wq, ws = host.split(fmt, W, n, k)
+    y, s = host.gemv_f32(fmt, dev(wq), dev(ws), dev(x), n, k)
+    rq, rd, _ = O.quantize(fmt, x)
+    r, _ = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    assert s is None and O.relerr(y.cpu().numpy(), r) <= 1e-5
