@@ -14,8 +14,8 @@ does not bound them.
 Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in + f32 outputs)
 / their wall time (GB/s); roofline = the tq2_0_gemv
 dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
-(the clock rocprofv3 --kernel-trace reads); cpu_baseline = the numpy oracle on a bounded sample of the same steps on
-this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold, library-chosen knobs).
+(the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
+sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold, library-chosen knobs).
 """
 
 from __future__ import annotations
@@ -34,6 +34,10 @@ if ROOT not in sys.path:
 METRIC = "GEMV µs/call + achieved HBM GB/s (% of peak), Q4_0 & TQ2_0 decode shapes"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
 COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infinity Cache)
+# HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
+# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
+# profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
+TRAFFIC_FUSED_BITNET_M1 = 4891431
 
 
 def gemv_bytes(fmt, n, k, m):
@@ -200,8 +204,10 @@ def headline(torch, host, abi, args):
     launch_b = step_bytes / len(shapes)
     g_us = g_ms * 1e3 / g_n
     achieved = launch_b / (g_us * 1e-6) / 1e9
+    default_cfg = m == 1 and args.mode == 2 and args.block_n is None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "tq2_0_gemv (fused quantize)",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": TRAFFIC_FUSED_BITNET_M1 if default_cfg else None,
+                "kernel": "tq2_0_gemv (fused quantize)",
                 "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b)}  # fmt: skip
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
                           "activations quantized to q8_K inside each launch",  # fmt: skip
@@ -214,9 +220,11 @@ def headline(torch, host, abi, args):
 
 
 def cpu_baseline(args, step_bytes_m, seconds=10.0):
-    """numpy oracle (this repository's restatement of the reference path) on whole steps of the same chain."""
+    """The C restatement of the reference path (oracle/oracle.c: ggml's q8_K quantizer, int32 block dots, f32 scale
+    and accumulate in block order), one thread, on whole steps of the same chain."""
     import numpy as np
 
+    from oracle import coracle as C
     from oracle import oracle as O
 
     rng = np.random.default_rng(args.seed)
@@ -229,23 +237,23 @@ def cpu_baseline(args, step_bytes_m, seconds=10.0):
         wq, ws = O.split("tq2_0", O.pack_tq2_0(crumbs, d), n, k)
         mats.append((n, k, wq, ws))
     x0 = rng.normal(size=(m, 2560)).astype(np.float32)
+    C.lib()
     steps = 0
     t0 = time.perf_counter()
     while True:
         x = x0
         for n, k, wq, ws in mats:
-            xq, xd, _ = O.quant_q8_K(x)
-            y, _ = O.gemv("tq2_0", wq, ws, xq, xd, n, k)
-            x = y.astype(np.float32)
+            xq, xd, _ = C.quant_q8_K(x)
+            x = C.gemv_f32("tq2_0", wq, ws, xq, xd, n, k)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     value = step_bytes_m * steps / el / 1e9
     return {"value": round(value, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} whole steps of the same chain (m={m}) through the numpy oracle (quant_q8_K, exact "
-                      f"int64 block dots, f64 reference_dot) in {el:.1f} s, 1 thread; host has "
-                      f"{len(os.sched_getaffinity(0))} cores"}  # fmt: skip
+            "sample": f"{steps} whole steps of the same chain (m={m}, both matrices) through the C oracle "
+                      f"(oracle/oracle.c: quant_q8_K, int32 block dots, f32 block-order accumulation), gcc -O2, "
+                      f"1 thread, {el:.1f} s; host has {len(os.sched_getaffinity(0))} cores"}  # fmt: skip
 
 
 DETAIL_SHAPES = (  # (fmt, n, k, m)
@@ -303,6 +311,9 @@ def main():
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only copy a MIB-MiB device buffer 10 times (the known-size kernel that scales the PMC "
+                         "FETCH_SIZE / WRITE_SIZE readings)")  # fmt: skip
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU: the decode path is single-device, and --gpus {args.gpus} is not supported "
@@ -320,7 +331,15 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
     _abi.lib()
-    torch.backends.cuda.matmul.allow_tf32 = False
+    if args.calibrate_copy:
+        nbytes = args.calibrate_copy << 20
+        src = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 10}), flush=True)
+        return 0
 
     value, ms_per_step, roofline, config, step_bytes = headline(torch, host, _abi, args)
     out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

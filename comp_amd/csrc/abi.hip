@@ -58,11 +58,12 @@ TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
 // Pick (block_n, nb, num_warps) for a shape.
-//   Latency regime (weights <= 64 MB, so every wave of the grid is resident at once): a wave must cover its rows in
-//   ONE K step, since each extra step adds a full HBM round trip to the wave's critical path.  Lanes per row ~ half
-//   the row's 16-byte chunks (2 chunks per lane), nb just large enough for one step, 8 waves per workgroup.
-//   Bandwidth regime (larger weights): 16 lanes per row (a short row-group reduction, many rows per wave), a few K
-//   steps, bigger workgroups so the LDS staging of the activations is amortised over more rows.
+//   Throughput regime (N >= 16384 rows: at 16 lanes per row the grid fields >= 16 wavefronts per CU): 16 lanes per row
+//   (a short row-group reduction, 4 rows per wave), a few K steps, and enough resident waves that one wave's compute
+//   overlaps the others' loads.
+//   Latency regime (fewer rows: every wave of the grid is resident at once): a wave must cover its rows in ONE K step,
+//   since each extra step adds a full HBM round trip to the wave's critical path.  Lanes per row ~ half the row's
+//   16-byte chunks (2 chunks per lane), nb just large enough for one step, 8 waves per workgroup.
 int pow2_ceil(int64_t v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -73,9 +74,8 @@ void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warp
   const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
   const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
   const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
-  const int64_t wbytes = n * nblk * (fmt == FMT_Q4_0 ? 18 : 66);
   int lpr, cand_nb, w;
-  if (wbytes <= (int64_t)64 << 20) {
+  if (n < 16384) {
     lpr = pow2_ceil((chunks + 1) / 2);
     lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
     const int64_t blocks_per_slot = lpr / bpb;
