@@ -41,6 +41,9 @@ def compile_flags():
         "-target-feature",
         "-Xclang",
         "-packed-fp32-ops",
+        # the first 16 kernel-argument dwords arrive in SGPRs at wave launch (gfx950 kernarg preloading)
+        "-mllvm",
+        "-amdgpu-kernarg-preload-count=16",
     ]
 
 

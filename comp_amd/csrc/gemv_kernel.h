@@ -94,14 +94,16 @@ __device__ __forceinline__ int tq2_0_chunk_dot(u32x4 w, const u32x4 (&x)[4], int
 
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 __global__ void __launch_bounds__(512)
-gemv_kernel(const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, const int8_t* __restrict__ XQ,
-            const float* __restrict__ XD, const float* __restrict__ X, int8_t* __restrict__ XQo,
-            float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y, int32_t* __restrict__ S, int N,
-            int K, int64_t SW, int rows_per_wg, int lpr_log2, int passes) {
+gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
+            int nsteps, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
+            const int8_t* __restrict__ XQ, const float* __restrict__ XD, const float* __restrict__ X,
+            int8_t* __restrict__ XQo, float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y,
+            int32_t* __restrict__ S) {
+  // The scalars come first and the host precomputes every quotient (nblk = K / block, rows per wave, K steps), so
+  // with the first 16 argument dwords preloaded into SGPRs the first weight load needs no memory round trip for its
+  // address and the prologue no integer division.
   extern __shared__ __align__(16) unsigned char lds[];
-  constexpr int BLK = FMT == FMT_Q4_0 ? 32 : 256;
   constexpr int BB = FMT == FMT_Q4_0 ? 16 : 64;  // quant bytes per block
-  const int nblk = K / BLK;
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int lane = tid & 63;
@@ -110,11 +112,9 @@ gemv_kernel(const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, cons
   const int gl = lane & (lpr - 1);
   const int grp = lane >> lpr_log2;
   const int rows_per_pass = 64 >> lpr_log2;
-  const int rows_per_wave = rows_per_wg / (nthreads >> 6);
   const int row_base = blockIdx.x * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   const int bpg = FMT == FMT_Q4_0 ? lpr : (lpr >> 2);  // blocks a row group covers per chunk slot
   const int bstep = bpg * NB;                            // blocks a row group covers per K step
-  const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
   const int q = gl & 3;                                  // TQ2_0: chunk of the block this lane loads
   const int gblk = FMT == FMT_Q4_0 ? gl : (gl >> 2);     // block offset of this lane within a slot
   const int tiles = passes * nsteps;
@@ -374,12 +374,17 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     lds_attr = lds;
   }
   const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
+  const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
+  const int bstep = (FMT == FMT_Q4_0 ? (1 << p.lpr_log2) : (1 << p.lpr_log2) / 4) * NB;
+  const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
+  const int rows_per_wave = p.block_n / p.waves;
   if (tm.on) {
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
-                          c.xd_out, c.xb_out, c.y, c.s, c.n, c.k, c.sw, p.block_n, p.lpr_log2, p.passes);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.k, c.sw, nblk, p.block_n,
+                          rows_per_wave, p.lpr_log2, p.passes, nsteps, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
+                          c.xd_out, c.xb_out, c.y, c.s);
   } else {
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y,
-                       c.s, c.n, c.k, c.sw, p.block_n, p.lpr_log2, p.passes);
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, c.k, c.sw, nblk, p.block_n, rows_per_wave, p.lpr_log2,
+                       p.passes, nsteps, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y, c.s);
   }
   return hipGetLastError();
 }
