@@ -89,11 +89,12 @@ __device__ __forceinline__ float round_half_away(float x) {
 // quantized values packed in a dword (value e in byte e); d_store receives f32(f16(d)) (the stored scale, RTNE), and
 // qsum the block's sum of q (every lane of the group receives it).
 __device__ __forceinline__ unsigned q8_0_group8(f32x4 v, float& d_store, int& qsum) {
-  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR1>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_XOR2>(a));
-  a = fmaxf(a, dpp_f<KOMP_DPP_HALF_MIRROR>(a));
-  const float d = a / 127.0f;  // correctly rounded (no fast-math)
+  // |x| >= 0, whose bit patterns order like the floats, so the 8-lane max runs on integers (single DPP instructions)
+  int ab = __float_as_int(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  ab = max(ab, dpp_i<KOMP_DPP_XOR1>(ab));
+  ab = max(ab, dpp_i<KOMP_DPP_XOR2>(ab));
+  ab = max(ab, dpp_i<KOMP_DPP_HALF_MIRROR>(ab));
+  const float d = __int_as_float(ab) / 127.0f;  // correctly rounded (no fast-math)
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   unsigned packed = 0;
   int sum = 0;
@@ -112,12 +113,6 @@ __device__ __forceinline__ unsigned q8_0_group8(f32x4 v, float& d_store, int& qs
 }
 
 // Sum / max / min over each aligned 16-lane DPP row; every lane of the row receives the row's result.
-__device__ __forceinline__ float row16_max_f(float v) {
-  v = fmaxf(v, dpp_f<KOMP_DPP_XOR1>(v));
-  v = fmaxf(v, dpp_f<KOMP_DPP_XOR2>(v));
-  v = fmaxf(v, dpp_f<KOMP_DPP_HALF_MIRROR>(v));
-  return fmaxf(v, dpp_f<KOMP_DPP_MIRROR>(v));
-}
 __device__ __forceinline__ int row16_min_i(int v) {
   v = min(v, dpp_i<KOMP_DPP_XOR1>(v));
   v = min(v, dpp_i<KOMP_DPP_XOR2>(v));
@@ -125,43 +120,70 @@ __device__ __forceinline__ int row16_min_i(int v) {
   return min(v, dpp_i<KOMP_DPP_MIRROR>(v));
 }
 
+__device__ __forceinline__ int row16_max_i(int v) {
+  v = max(v, dpp_i<KOMP_DPP_XOR1>(v));
+  v = max(v, dpp_i<KOMP_DPP_XOR2>(v));
+  v = max(v, dpp_i<KOMP_DPP_HALF_MIRROR>(v));
+  return max(v, dpp_i<KOMP_DPP_MIRROR>(v));
+}
+
+// f32 bits -> int32 whose signed order is the float order (-0 just below +0); the map is its own inverse.  Row
+// reductions of floats run on these keys because integer max/min fold into single DPP instructions, while float ones
+// need NaN-quieting moves around every DPP step.
+__device__ __forceinline__ int f32_order_key(int bits) { return bits ^ ((bits >> 31) & 0x7FFFFFFF); }
+
 // ggml q8_K on one block of 256 values held by an aligned 16-lane row (lane r of the row holds values 16r..16r+15 in
-// v[0..3]); the whole row must be active.  Writes the lane's 16 q into qout (value 4t+e in byte e of qout[t]) and
-// returns the lane's sum of its 16 q, which is exactly bsum r of the block; d_out receives d (0 for an all-zero
-// block) and qsum the block's sum of q.
+// v[0..3]); the whole row must be active and the wave's control flow uniform.  Writes the lane's 16 q into qout (value
+// 4t+e in byte e of qout[t]) and returns the lane's sum of its 16 q, which is exactly bsum r of the block; d_out
+// receives d (0 for an all-zero block) and qsum the block's sum of q.
+//
+// mx, the x of largest |x| with the first index winning ties (patch:121-125), is the block's signed maximum hi or its
+// signed minimum lo: whichever has the larger magnitude.  Only when both +|mx| and -|mx| occur does the index order
+// decide; that rare case takes a wave-uniform branch that finds the sign of the first occurrence.
+//
+// q = round_half_even(iscale * x) (patch:128, 94-101) without the clamp to 127: |x| <= |mx| and iscale = -127 / mx
+// correctly rounded, so |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5 and the rounded value never exceeds 127 in
+// magnitude.  Adding 1.5 * 2^23 to the rounded product rounds it to an integer in the default round-to-nearest-even
+// mode, exactly as round_half_even does, and the low byte of the sum's bits is that integer's two's-complement byte.
 __device__ __forceinline__ int q8_K_row16(const f32x4 (&v)[4], int r, u32x4& qout, float& d_out, int& qsum) {
-  float a = 0.0f;
+#pragma clang fp contract(off)
+  // three-operand chains (v_max3 / v_min3), which take the loaded values as they are
+  float hi = fmaxf(fmaxf(v[0][0], v[0][1]), v[0][2]);
+  float lo = fminf(fminf(v[0][0], v[0][1]), v[0][2]);
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-    a = fmaxf(a, fmaxf(fmaxf(fabsf(v[t][0]), fabsf(v[t][1])), fmaxf(fabsf(v[t][2]), fabsf(v[t][3]))));
-  const float amax = row16_max_f(a);
-  // the first index whose |x| equals amax (patch:124), and x at that index
-  int local = 16;
+  for (int i = 3; i < 15; i += 2) {
+    hi = fmaxf(fmaxf(hi, v[i >> 2][i & 3]), v[(i + 1) >> 2][(i + 1) & 3]);
+    lo = fminf(fminf(lo, v[i >> 2][i & 3]), v[(i + 1) >> 2][(i + 1) & 3]);
+  }
+  hi = fmaxf(hi, v[3][3]);
+  lo = fminf(lo, v[3][3]);
+  hi = __int_as_float(f32_order_key(row16_max_i(f32_order_key(__float_as_int(hi)))));
+  lo = __int_as_float(f32_order_key(row16_min_i(f32_order_key(__float_as_int(lo)))));
+  float mx = hi >= -lo ? hi : lo;
+  const bool tie = hi == -lo && hi != 0.0f;
+  if (__builtin_expect(__ballot(tie) != 0, 0)) {
+    // sign of this lane's first value with |x| == hi (reverse scan), then the lowest lane of the row that has one
+    int neg = 2;
 #pragma unroll
-  for (int t = 3; t >= 0; --t)
+    for (int t = 3; t >= 0; --t)
 #pragma unroll
-    for (int e = 3; e >= 0; --e) local = fabsf(v[t][e]) == amax ? 4 * t + e : local;
-  const int first = row16_min_i(local < 16 ? 16 * r + local : 256);
-  float mine = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) mine = (16 * r + 4 * t + e == first) ? v[t][e] : mine;
-  // exactly one lane of the row owns `first`: adding the owner's bits to zeros broadcasts them exactly
-  const float mx = __int_as_float(group_sum(16 * r + local == first ? __float_as_int(mine) : 0, 16));
-  const bool nz = amax != 0.0f;
-  const float iscale = -127.0f / (nz ? mx : 1.0f);
+      for (int e = 3; e >= 0; --e) neg = fabsf(v[t][e]) == hi ? (v[t][e] < 0.0f ? 1 : 0) : neg;
+    const int first = row16_min_i(neg < 2 ? 2 * r + neg : 64);
+    if (tie) mx = (first & 1) ? lo : hi;
+  }
+  const bool nz = mx != 0.0f;
+  const float iscale = -127.0f / (nz ? mx : 1.0f);  // an all-zero block gives q = 0 through the same arithmetic
+  constexpr float kRound = 12582912.0f;             // 1.5 * 2^23
   int s16 = 0;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    unsigned packed = 0;
+    unsigned b[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int qv = nz ? static_cast<int>(fminf(rintf(iscale * v[t][e]), 127.0f)) : 0;
-      s16 += qv;
-      packed |= (static_cast<unsigned>(qv) & 0xFFu) << (8 * e);
-    }
-    qout[t] = packed;
+    for (int e = 0; e < 4; ++e) b[e] = __float_as_uint(iscale * v[t][e] + kRound);
+    const unsigned p01 = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);  // bytes {b0, b1, 0, 0}
+    const unsigned p23 = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+    qout[t] = p01 | (p23 << 16);
+    s16 = __builtin_amdgcn_sdot4(static_cast<int>(qout[t]), 0x01010101, s16, false);
   }
   qsum = group_sum(s16, 16);
   d_out = nz ? 1.0f / iscale : 0.0f;

@@ -59,18 +59,64 @@ def test_q8_0_f16_scale_edges():
     assert np.isinf(xd[0, 2]) and xd[0, 5] == 0.0
 
 
+def tie_blocks():
+    """q8_K blocks whose largest |x| occurs with both signs: the first index decides mx (and the sign of every q)."""
+    k = 256 * 8
+    x = np.clip(np.random.default_rng(5).normal(size=(1, k)), -4.5, 4.5).astype(np.float32)  # below every planted |x|
+    x[0, 10], x[0, 20] = 7.0, -7.0  # first positive, different lanes of the 16-lane row
+    x[0, 256 + 3], x[0, 256 + 200] = -5.0, 5.0  # first negative, different lanes
+    x[0, 512 + 5], x[0, 512 + 9] = -6.0, 6.0  # first negative, same lane
+    x[0, 768 + 5], x[0, 768 + 9], x[0, 768 + 250] = 6.5, -6.5, -6.5  # first positive, same lane, three occurrences
+    x[0, 1024:1280] = 0.0  # all-zero block
+    x[0, 1280 + 254], x[0, 1280 + 255] = 5.5, -5.5  # tie inside the last lane
+    x[0, 1536:1792] = -0.0  # negative zeros only: d = 0, q = 0
+    x[0, 1792 + 100] = -1e4  # single spike, no tie
+    return x
+
+
 def test_q8_K_first_index_and_ties():
-    k = 256 * 3
-    x = np.random.default_rng(5).normal(size=(1, k)).astype(np.float32)
-    x[0, 10] = 7.0
-    x[0, 20] = -7.0  # |x| tie: the first index (positive) decides the sign of iscale
-    x[0, 256 + 3] = -5.0
-    x[0, 256 + 200] = 5.0
-    x[0, 512:] = 0.0
+    x = tie_blocks()
     xq, xd, xb = run_quant("tq2_0", x)
     rq, rd, rb = O.quant_q8_K(x)
     assert np.array_equal(xq, rq) and np.array_equal(xd.view(np.uint32), rd.view(np.uint32)) and np.array_equal(xb, rb)
-    assert xq[0, 10] == -127 and xq[0, 20] == 127 and xd[0, 2] == 0.0
+    assert xq[0, 10] == -127 and xq[0, 20] == 127 and xq[0, 256 + 3] == -127 and xq[0, 512 + 5] == -127
+    assert xq[0, 768 + 5] == -127 and xq[0, 1280 + 254] == -127 and xd[0, 4] == 0.0 and xd[0, 6] == 0.0
+
+
+def test_q8_K_random_ties_standalone_and_fused():
+    # 64 blocks, each with its largest |x| planted at two random positions with opposite signs in random order
+    rng = np.random.default_rng(17)
+    nblk = 64
+    x = rng.normal(size=(nblk, 256)).astype(np.float32)
+    for b in range(nblk):
+        i, j = rng.choice(256, size=2, replace=False)
+        a = np.float32(abs(rng.normal()) + 8.0)
+        x[b, i], x[b, j] = (a, -a) if rng.random() < 0.5 else (-a, a)
+    x = x.reshape(1, -1)
+    xq, xd, xb = run_quant("tq2_0", x)
+    rq, rd, rb = O.quant_q8_K(x)
+    assert np.array_equal(xq, rq) and np.array_equal(xd.view(np.uint32), rd.view(np.uint32)) and np.array_equal(xb, rb)
+    n, k = 40, x.shape[1]
+    W, _ = O.problem("tq2_0", n, k, 1, 3)
+    wq, ws = host.split("tq2_0", W, n, k)
+    _, _, q = host.gemv_f32("tq2_0", dev(wq), dev(ws), dev(x), n, k, return_q=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(q[0].cpu().numpy(), rq) and np.array_equal(q[1].cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(q[2].cpu().numpy(), rb)
+
+
+def test_q8_K_tie_blocks_fused():
+    x = tie_blocks()
+    n, k = 24, x.shape[1]
+    W, _ = O.problem("tq2_0", n, k, 1, 4)
+    wq, ws = host.split("tq2_0", W, n, k)
+    y, s, q = host.gemv_f32("tq2_0", dev(wq), dev(ws), dev(x), n, k, store_s=True, return_q=True)
+    torch.cuda.synchronize()
+    rq, rd, rb = O.quant_q8_K(x)
+    assert np.array_equal(q[0].cpu().numpy(), rq) and np.array_equal(q[1].cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(q[2].cpu().numpy(), rb)
+    r, rs = O.gemv("tq2_0", wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs) and O.relerr(y.cpu().numpy(), r) <= TOL
 
 
 def run_gemv(fmt, n, k, m, seed, extreme, block_n, nb, mode, num_warps):
