@@ -42,7 +42,7 @@ SIGNATURES = {
     "komp_tq2_0_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_q4_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_tq2_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
-    "komp_gemv_auto_config": (_INT, [_INT, _I64, _I64, _I64, _P, _P, _P]),
+    "komp_gemv_auto_config": (_INT, [_INT, _INT, _I64, _I64, _I64, _P, _P, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
     "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
@@ -94,9 +94,10 @@ def call(name, *args):
     check(getattr(lib(), name)(*args), name)
 
 
-def auto_config(fmt_id, m, n, k):
+def auto_config(fmt_id, m, n, k, fused=False):
     bn, nb, nw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    call("komp_gemv_auto_config", fmt_id, m, n, k, ctypes.byref(bn), ctypes.byref(nb), ctypes.byref(nw))
+    call("komp_gemv_auto_config", fmt_id, int(bool(fused)), m, n, k, ctypes.byref(bn), ctypes.byref(nb),
+         ctypes.byref(nw))
     return bn.value, nb.value, nw.value
 
 

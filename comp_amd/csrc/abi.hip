@@ -57,26 +57,28 @@ struct TimingState {
 TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
-// Pick (block_n, nb, num_warps) for a shape.
+// The plan gemv uses when block_n == 0 (a knob set of the explicit tune space).
 //   Throughput regime (N >= 16384 rows: at 16 lanes per row the grid fields >= 16 wavefronts per CU): 16 lanes per row
 //   (a short row-group reduction, 4 rows per wave), a few K steps, and enough resident waves that one wave's compute
 //   overlaps the others' loads.
 //   Latency regime (fewer rows: every wave of the grid is resident at once): a wave must cover its rows in ONE K step,
-//   since each extra step adds a full HBM round trip to the wave's critical path.  Lanes per row ~ half the row's
-//   16-byte chunks (2 chunks per lane), nb just large enough for one step, 8 waves per workgroup.
+//   since each extra step adds a full HBM round trip to the wave's critical path, and short waves finish sooner than
+//   few long ones, so 8 waves per workgroup and as many lanes per row as the row has 16-byte chunks (at most 64).
+//   The fused launch quantizes the activations in every workgroup, so it halves the lanes per row (two chunks per
+//   lane), which halves the number of workgroups that pay for that staging.
 int pow2_ceil(int64_t v) {
   int p = 1;
   while (p < v) p <<= 1;
   return p;
 }
 
-void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warps) {
+void auto_config(int fmt, bool fused, int64_t n, int64_t k, int* block_n, int* nb, int* warps) {
   const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
   const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
   const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
   int lpr, cand_nb, w;
   if (n < 16384) {
-    lpr = pow2_ceil((chunks + 1) / 2);
+    lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
     lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
     const int64_t blocks_per_slot = lpr / bpb;
     cand_nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
@@ -93,6 +95,20 @@ void auto_config(int fmt, int64_t n, int64_t k, int* block_n, int* nb, int* warp
   *block_n = w * rpw;
   *nb = cand_nb;
   *warps = w;
+}
+
+GemvPlan knob_plan(int block_n, int nb, int num_warps) {
+  GemvPlan plan;
+  plan.block_n = block_n;
+  plan.nb = nb;
+  plan.waves = num_warps;
+  const int rpw = block_n / num_warps;
+  const int rpp = rpw < 16 ? rpw : 16;
+  plan.lpr_log2 = 0;
+  while ((64 >> plan.lpr_log2) > rpp) ++plan.lpr_log2;
+  plan.passes = rpw / rpp;
+  plan.rows_per_wave = rpw;
+  return plan;
 }
 
 struct GemvArgs {
@@ -123,7 +139,7 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
                 (long long)SW, (long long)row_bytes);
   if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A) return fail(KOMP_EINVAL, "%s: mode=%d not in {0,1,2}", name, mode);
   if (block_n == 0) {
-    auto_config(fmt, N, K, &block_n, &nb, &num_warps);
+    auto_config(fmt, fused, N, K, &block_n, &nb, &num_warps);
   } else {
     if (!in_set(block_n, kBlockN, 5)) return fail(KOMP_EINVAL, "%s: block_n=%d not in {8,16,32,64,128}", name, block_n);
     if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
@@ -152,15 +168,7 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
     return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
 
-  GemvPlan plan;
-  plan.block_n = block_n;
-  plan.nb = nb;
-  plan.waves = num_warps;
-  const int rpw = block_n / num_warps;
-  const int rpp = rpw < 16 ? rpw : 16;
-  plan.lpr_log2 = 0;
-  while ((64 >> plan.lpr_log2) > rpp) ++plan.lpr_log2;
-  plan.passes = rpw / rpp;
+  const GemvPlan plan = knob_plan(block_n, nb, num_warps);
 
   const int64_t nblk = K / blk;
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
@@ -270,12 +278,13 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
   return gemv_entry(FMT_TQ2_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
 }
 
-int komp_gemv_auto_config(int fmt, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps) {
+int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
+                          int* num_warps) {
   (void)M;
   if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
   if (N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)
     return fail(KOMP_EINVAL, "komp_gemv_auto_config: bad argument");
-  auto_config(fmt, N, K, block_n, nb, num_warps);
+  auto_config(fmt, fused != 0, N, K, block_n, nb, num_warps);
   return KOMP_OK;
 }
 

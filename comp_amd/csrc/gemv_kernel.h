@@ -377,7 +377,7 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
   const int bstep = (FMT == FMT_Q4_0 ? (1 << p.lpr_log2) : (1 << p.lpr_log2) / 4) * NB;
   const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
-  const int rows_per_wave = p.block_n / p.waves;
+  const int rows_per_wave = p.rows_per_wave;
   if (tm.on) {
     hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.k, c.sw, nblk, p.block_n,
                           rows_per_wave, p.lpr_log2, p.passes, nsteps, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,

@@ -1,4 +1,4 @@
-// Internal (C++) interface between the C-ABI layer (komp_abi.cpp) and the kernel translation units.
+// Internal (C++) interface between the C-ABI layer (abi.hip) and the kernel translation units.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,13 +11,14 @@ enum Fmt { FMT_Q4_0 = 0, FMT_TQ2_0 = 1 };
 // Kernel kinds, for the per-dispatch timing of the tuning harness.
 enum Kind { KIND_QUANT_Q8_0 = 0, KIND_QUANT_Q8_K = 1, KIND_Q4_0_GEMV = 2, KIND_TQ2_0_GEMV = 3, KIND_PROBE = 4, KIND_COUNT = 5 };
 
-// Work decomposition of one GEMV launch (see gemv.hip for the mapping of block_n / nb / num_warps).
+// Work decomposition of one GEMV launch (gemv_kernel.h describes the mapping of block_n / nb / num_warps).
 struct GemvPlan {
-  int block_n;    // rows per workgroup
-  int nb;         // 16-byte weight chunks each lane loads per row per K step
-  int waves;      // wavefronts per workgroup
-  int lpr_log2;   // log2(lanes per row group)
-  int passes;     // row groups each wave walks in sequence
+  int block_n;        // rows per workgroup
+  int nb;             // 16-byte weight chunks each lane loads per row per K step
+  int waves;          // wavefronts per workgroup (at most 8)
+  int rows_per_wave;  // block_n / waves = (64 >> lpr_log2) * passes
+  int lpr_log2;       // log2(lanes per row group)
+  int passes;         // row groups each wave walks in sequence
 };
 
 struct GemvCall {
@@ -45,7 +46,7 @@ struct Timing {
   hipEvent_t start;
   hipEvent_t stop;
 };
-Timing timing_slot(int kind);   // defined in komp_abi.cpp
+Timing timing_slot(int kind);   // defined in abi.hip
 
 size_t gemv_lds_bytes(int fmt, int m, int k);
 hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);

@@ -243,7 +243,7 @@ def _check_weights(fmt, wq, ws, n, k):
 def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps=4, s=None, xq=None, xd=None,
                   xb=None):  # fmt: skip
     """Quantize-and-GEMV in one launch into preallocated outputs: x f32 [M][K] -> y f32 [M][N] (and s, and the q8
-    planes xq / xd / xb when given, as quantize() would return them).  Bit-identical to quantize() then gemv()."""
+    planes xq / xd / xb when given, as quantize() would return them).  Bit-identical to quantize() then gemv() with the same knobs."""
     nblk = _check_weights(fmt, wq, ws, n, k)
     _need(x, "x", torch.float32, 2)
     if x.shape[1] != k or not x.is_contiguous():
@@ -279,7 +279,8 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
     """Quantize-and-GEMV in one launch: x f32 [M][K] -> (Y f32 [M][N], S or None[, (XQ, XD[, XB])]).
 
     Every workgroup quantizes x (q8_0 for q4_0, q8_K for tq2_0) with the quantizer kernels' arithmetic, so the result
-    equals quantize() followed by gemv() bit for bit, with one dispatch instead of two.  return_q also returns the q8
+    equals quantize() followed by gemv() with the same knobs bit for bit, with one dispatch instead of two
+    (block_n=None plans this launch with auto_config(..., fused=True)).  return_q also returns the q8
     planes (and the q8_K bsums).  No reference counterpart (the reference launches the two kernels separately)."""
     _need(x, "x", torch.float32, 2)
     x = x.contiguous()
@@ -299,9 +300,9 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
     return (y, s, q) if return_q else (y, s)
 
 
-def auto_config(fmt, m, n, k):
-    """(block_n, nb, num_warps) that gemv(..., block_n=None) uses for this shape."""
-    return _abi.auto_config(FMT_ID[fmt], m, n, k)
+def auto_config(fmt, m, n, k, fused=False):
+    """(block_n, nb, num_warps) that gemv(..., block_n=None) uses for this shape, or gemv_f32 with fused=True."""
+    return _abi.auto_config(FMT_ID[fmt], m, n, k, fused)
 
 
 def dp4a_probe(a, b, c, mode=2):

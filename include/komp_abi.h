@@ -70,7 +70,8 @@ int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, cons
 
 /* Quantize-and-GEMV in one launch: X is f32 [M][K] (16-byte aligned); every workgroup quantizes it (q8_0 for q4_0,
  * q8_K for tq2_0) into LDS with the quantizer kernels' arithmetic, then runs the GEMV, so Y and S equal
- * komp_quant_q8_* followed by komp_*_gemv bit for bit.  When XQ is not NULL, one workgroup also writes the q8 planes
+ * komp_quant_q8_* followed by komp_*_gemv with the same block_n / nb / num_warps bit for bit (block_n == 0 plans the
+ * fused launch with its own knobs, komp_gemv_auto_config with fused != 0).  When XQ is not NULL, one workgroup also writes the q8 planes
  * XQ [M][K] and XD (required with XQ), and for tq2_0 the bsums XB [M][K/16] when XB is not NULL (XB must be NULL for
  * q4_0).  Other arguments as komp_q4_0_gemv / komp_tq2_0_gemv.
  * No reference counterpart: the reference launches its quantizer and its GEMV separately (src/komp/host.py:63-85);
@@ -82,9 +83,10 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
                         float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
                         int mode, int num_warps, void* stream);
 
-/* The (block_n, nb, num_warps) that block_n == 0 selects for a GEMV shape; fmt 0 = q4_0, 1 = tq2_0.
+/* The (block_n, nb, num_warps) that block_n == 0 selects for a GEMV shape; fmt 0 = q4_0, 1 = tq2_0; fused != 0 for
+ * komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32 (which plan fewer, wider workgroups, since each quantizes the input).
  * No reference counterpart: the reference always takes the knobs from its caller. */
-int komp_gemv_auto_config(int fmt, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps);
+int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps);
 
 /* OUT[i] = dp4a(A[i], B[i], C[i]) for i < n; mode KOMP_MODE_DP4A (hardware) or KOMP_MODE_DP4A_EMU.
  * Replaces: kernels.dp4a_probe (src/komp/kernels.py:145-149). */

@@ -78,9 +78,14 @@ def test_python_errors_carry_the_message():
 
 @pytest.mark.parametrize("fmt,n,k", [(0, 4096, 4096), (0, 128256, 4096), (0, 4097, 4192), (1, 6912, 2560),
                                      (1, 2560, 6912), (1, 32768, 8192), (0, 1, 32), (1, 3, 256)])  # fmt: skip
-def test_auto_config_is_a_legal_knob_set(fmt, n, k):
-    bn, nb, nw = _abi.auto_config(fmt, 1, n, k)
+@pytest.mark.parametrize("fused", [False, True])
+def test_auto_config_is_a_legal_knob_set(fmt, n, k, fused):
+    bn, nb, nw = _abi.auto_config(fmt, 1, n, k, fused)
     assert bn in (8, 16, 32, 64, 128) and nb in (1, 2, 4, 8, 16) and nw in (1, 2, 4, 8) and bn % nw == 0
+    if n < 16384:  # latency regime: one K step covers the row (lanes per row = 64 / rows per wave, capped at 16 rows)
+        lanes = 64 // min(bn // nw, 16)
+        blocks_per_slot = lanes if fmt == 0 else lanes // 4
+        assert nb * blocks_per_slot >= k // (32 if fmt == 0 else 256)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -1,5 +1,6 @@
-"""The fused quantize-and-GEMV launch equals quantize() followed by gemv() bit for bit (Y, S and the q8 planes),
-for every mode, edge data, tails and 1..4 columns."""
+"""The fused quantize-and-GEMV launch equals quantize() followed by gemv() with the same knobs bit for bit (Y, S and
+the q8 planes), for every mode, edge data, tails and 1..4 columns; block_n=None plans the fused launch with
+auto_config(..., fused=True)."""
 
 import numpy as np
 import pytest
@@ -30,6 +31,8 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
     bn, nb, nw = knobs if knobs else (None, 0, 0)
     y1, s1, q = host.gemv_f32(fmt, wq, ws, xg, n, k, bn, nb, mode, nw, store_s=True, return_q=True)
     qq = host.quantize(fmt, xg, bsums=(fmt == "tq2_0"))
+    if knobs is None:  # the knobs the fused launch planned for itself
+        bn, nb, nw = host.auto_config(fmt, m, n, k, fused=True)
     y2, s2 = host.gemv(fmt, wq, ws, qq[0], qq[1], n, k, bn, nb, mode, nw, store_s=True)
     torch.cuda.synchronize()
     assert torch.equal(s1, s2)

@@ -156,7 +156,9 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
 
 
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 4096, 4096), ("q4_0", 4097, 4192), ("q4_0", 127, 4192),
-                                     ("tq2_0", 6912, 2560), ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816)])
+                                     ("q4_0", 16383, 4096), ("q4_0", 300, 96), ("tq2_0", 6912, 2560),
+                                     ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816), ("tq2_0", 16383, 256),
+                                     ("tq2_0", 513, 1280)])  # fmt: skip
 @pytest.mark.parametrize("m", [1, 3])
 def test_gemv_auto_config_shapes(fmt, n, k, m):
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 21, False, None, None, 2, None)
