@@ -4,7 +4,9 @@
 //
 // Y[m][n] = sum_b d_w(n, b) * d_x(m, b) * s(m, n, b), where s is the exact int32 dot of weight block b of row n with
 // activation block b of column m.  The weights stream once from HBM for all columns (1..3 per launch), with
-// non-temporal 16-byte loads (they are read once); the activation columns are staged in LDS once per workgroup.
+// non-temporal 16-byte loads (they are read once); the activation columns are staged in LDS once per workgroup, and
+// so is the workgroup's slab of weight scales when it is small and aligned (copied global -> LDS directly), so the
+// weight stream issues only 16-byte quant loads instead of a 2-byte scale load beside each of them.
 // The fused variant stages f32 activations instead: every workgroup quantizes them itself (q8_0 / q8_K, with the
 // same device functions as the quantizer kernels, so the bytes are identical) and one workgroup also writes the q8
 // planes out; that removes the separate quantizer dispatch from a decode step.
@@ -33,6 +35,9 @@
 
 namespace komp {
 namespace gemv_impl {
+
+constexpr size_t kScaleSlabMax = 16 * 1024;  // largest scale slab staged in LDS
+constexpr size_t kLdsLimit = 160 * 1024;      // LDS per workgroup on gfx950
 
 constexpr unsigned NIB = 0x0F0F0F0Fu;
 constexpr unsigned ONES = 0x01010101u;
@@ -95,13 +100,18 @@ __device__ __forceinline__ int tq2_0_chunk_dot(u32x4 w, const u32x4 (&x)[4], int
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 __global__ void __launch_bounds__(512)
 gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
-            int nsteps, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
+            int nsteps, int sc_mode, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
             const int8_t* __restrict__ XQ, const float* __restrict__ XD, const float* __restrict__ X,
             int8_t* __restrict__ XQo, float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y,
             int32_t* __restrict__ S) {
   // The scalars come first and the host precomputes every quotient (nblk = K / block, rows per wave, K steps), so
   // with the first 16 argument dwords preloaded into SGPRs the first weight load needs no memory round trip for its
   // address and the prologue no integer division.
+  //
+  // sc_mode 1: the workgroup's weight scales WS[row0 .. row0 + rows_per_wg) (one contiguous slab, 16-byte aligned, a
+  // multiple of 8 scales) are staged in LDS with the activations, and the weight stream issues only quant loads.
+  // sc_mode 0: each lane loads its scales beside its quants (one 2-byte load per 16-byte chunk), for slabs that are
+  // too large for LDS or not 16-byte aligned.
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int BB = FMT == FMT_Q4_0 ? 16 : 64;  // quant bytes per block
   const int tid = threadIdx.x;
@@ -124,6 +134,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
 
   u32x4 w[NB];
   int16_t sc[NB];
+  const bool sc_global = sc_mode == 0;
   auto load_tile = [&](int t) {
     const int p = t / nsteps;
     const int st = t - p * nsteps;
@@ -137,7 +148,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
       const int b = st * bstep + u * bpg + gblk;
       if (rv && b < nblk) {
         w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + static_cast<int64_t>(u) * bpg * BB));
-        sc[u] = stp[u * bpg];
+        sc[u] = sc_global ? stp[u * bpg] : static_cast<int16_t>(0);
       } else {
         w[u] = u32x4{0u, 0u, 0u, 0u};
         sc[u] = 0;
@@ -148,11 +159,32 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   // Issue the first tile's weight loads before staging the activations, so HBM latency overlaps the staging.
   load_tile(0);
 
-  // ---- stage the activation columns in LDS ----
+  // ---- LDS layout ----
   // Q4_0: xlo[m][b] = activations 0..15 of block b, xhi[m][b] = 16..31, meta[m][b] = {d_x bits, -8 * sum(x)}.
   // TQ2_0: x4[m][j][b][q] = the 16 activations that pair with crumb j of chunk q; meta[m][b] = {d_x bits, -sum(x)}.
+  // Then (sc_mode 1) the scale slab [rows_per_wg][nblk], 16-byte aligned (the activation bytes are a multiple of 8).
   u32x4* xv = reinterpret_cast<u32x4*>(lds);
   int2* meta = reinterpret_cast<int2*>(xv + (FMT == FMT_Q4_0 ? 2 : 16) * MC * nblk);
+  u32x4* scs16 = xv + ((MC * nblk * (FMT == FMT_Q4_0 ? 40 : 264) + 15) >> 4);
+  const int16_t* scs = reinterpret_cast<const int16_t*>(scs16);
+
+  // Then the scale slab (sc_mode 1): each wave copies 1 KB pieces of it from global memory straight into LDS
+  // (global_load_lds_dwordx4: lane i's 16 bytes land at the wave's LDS base + 16 i), so the copy holds no registers;
+  // the barrier after the activation staging waits for it with the other loads.
+  if (sc_mode == 1) {
+    const int wg_row0 = blockIdx.x * rows_per_wg;
+    const int sc_rows = min(rows_per_wg, N - wg_row0);
+    const int pieces = (sc_rows * nblk) >> 3;  // 16-byte pieces
+    const u32x4* src = reinterpret_cast<const u32x4*>(WS + static_cast<int64_t>(wg_row0) * nblk);
+    for (int c = wave * 64; c < pieces; c += nthreads) {  // wave-uniform
+      if (c + lane < pieces)
+        __builtin_amdgcn_global_load_lds(src + c + lane, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                                                             reinterpret_cast<uintptr_t>(scs16 + c)),
+                                         16, 0, 0);
+    }
+  }
+
+  // ---- stage the activation columns in LDS ----
   // Each loop below issues the global loads of up to SU iterations before using any of them, so a workgroup pays one
   // memory round trip per SU iterations of staging rather than one per iteration.  The unfused loops finish in one
   // iteration for every shape that fits LDS with 256+ lanes, and extra staging registers would cut the occupancy of
@@ -324,6 +356,16 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
 #pragma unroll
       for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
     }
+    if (!sc_global) {
+      // this tile's scales from the LDS slab (a lane of an idle row reads a slab row that was not loaded; its results
+      // are never stored)
+      const int16_t* scr = scs + (wave * rows_per_wave + rl) * nblk;
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int b = st * bstep + u * bpg + gblk;
+        sc[u] = b < nblk ? scr[b] : static_cast<int16_t>(0);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int b = st * bstep + u * bpg + gblk;
@@ -365,7 +407,16 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   auto kern = gemv_kernel<FMT, MODE, MC, NB, FUSED>;
   const dim3 grid(static_cast<unsigned>((c.n + p.block_n - 1) / p.block_n));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
-  const unsigned lds = static_cast<unsigned>(gemv_lds_bytes(FMT, MC, c.k));
+  const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
+  // the workgroup's scale slab goes to LDS when it is small (the weight stream then issues only quant loads)
+  const size_t base = gemv_lds_bytes(FMT, MC, c.k);
+  const size_t sc_off = (base + 15) & ~static_cast<size_t>(15);
+  const size_t sc_bytes = static_cast<size_t>(p.block_n) * nblk * 2;
+  int sc_mode = 0;
+  if (nblk > 0 && nblk % 8 == 0 && reinterpret_cast<uintptr_t>(c.ws) % 16 == 0 && sc_bytes <= kScaleSlabMax &&
+      sc_off + sc_bytes <= kLdsLimit)
+    sc_mode = 1;
+  const unsigned lds = static_cast<unsigned>(sc_mode != 0 ? sc_off + sc_bytes : base);
   static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
   if (lds > lds_attr) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -374,17 +425,16 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     lds_attr = lds;
   }
   const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
-  const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
   const int bstep = (FMT == FMT_Q4_0 ? (1 << p.lpr_log2) : (1 << p.lpr_log2) / 4) * NB;
   const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
   const int rows_per_wave = p.rows_per_wave;
   if (tm.on) {
     hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.k, c.sw, nblk, p.block_n,
-                          rows_per_wave, p.lpr_log2, p.passes, nsteps, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
+                          rows_per_wave, p.lpr_log2, p.passes, nsteps, sc_mode, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
                           c.xd_out, c.xb_out, c.y, c.s);
   } else {
     hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, c.k, c.sw, nblk, p.block_n, rows_per_wave, p.lpr_log2,
-                       p.passes, nsteps, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y, c.s);
+                       p.passes, nsteps, sc_mode, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y, c.s);
   }
   return hipGetLastError();
 }

@@ -192,3 +192,24 @@ def test_decode_probes():
     tq = rng.integers(0, 256, size=(5, 64), dtype=np.uint8)
     got = host.tq2_0_decode(dev(tq)).cpu().numpy()
     assert np.array_equal(got, O.tq2_0_values(tq))
+
+
+@pytest.mark.parametrize("fmt,n,k,knobs", [("q4_0", 300, 4096, (16, 4, 4)), ("q4_0", 4096, 4096, None),
+                                           ("tq2_0", 300, 8192, (32, 2, 8)), ("tq2_0", 2560, 8192, None)])  # fmt: skip
+def test_scale_slab_and_per_tile_scales_agree(fmt, n, k, knobs):
+    # a 16-byte aligned WS is staged in LDS per workgroup; a WS view at a 2-byte offset takes the per-tile scale loads
+    W, x = O.problem(fmt, n, k, 1, 31)
+    wq, ws = host.split(fmt, W, n, k)
+    xq, xd, *_ = host.quantize(fmt, dev(x))
+    bn, nb, nw = knobs if knobs else (None, 0, 0)
+    wq_d, ws_d = dev(wq), dev(ws)
+    big = torch.zeros(ws.size + 8, dtype=torch.int16, device="cuda")
+    ws_odd = big[1 : 1 + ws.size].view(ws.shape)
+    ws_odd.copy_(ws_d)
+    assert ws_d.data_ptr() % 16 == 0 and ws_odd.data_ptr() % 16 == 2
+    y1, s1 = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 2, nw, store_s=True)
+    y2, s2 = host.gemv(fmt, wq_d, ws_odd, xq, xd, n, k, bn, nb, 2, nw, store_s=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s1, s2) and torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    r, rs = O.gemv(fmt, wq, ws, *O.quantize(fmt, x)[:2], n, k)
+    assert np.array_equal(s1.cpu().numpy().astype(np.int64), rs) and O.relerr(y1.cpu().numpy(), r) <= TOL
