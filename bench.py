@@ -290,7 +290,9 @@ def detail(torch, host, abi, args):
         d_us = disp[kind][0] * 1e3 / disp[kind][1]
         b = gemv_bytes(fmt, n, k, m)
         us = ms * 1e3 / reps
-        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "knobs": list(host.auto_config(fmt, m, n, k)),
+        plan = host.auto_plan(fmt, m, n, k)
+        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "plan": [plan[key] for key in ("block_n", "nb", "waves",
+                                                                                        "lanes_per_row", "passes")],
                      "bytes": b, "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                      "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "dispatch_us": round(d_us, 3),
                      "gbs_dispatch": round(b / d_us / 1e3, 1), "copies": nc})  # fmt: skip

@@ -57,44 +57,66 @@ struct TimingState {
 TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
-// The plan gemv uses when block_n == 0 (a knob set of the explicit tune space).
-//   Throughput regime (N >= 16384 rows: at 16 lanes per row the grid fields >= 16 wavefronts per CU): 16 lanes per row
-//   (a short row-group reduction, 4 rows per wave), a few K steps, and enough resident waves that one wave's compute
-//   overlaps the others' loads.
-//   Latency regime (fewer rows: every wave of the grid is resident at once): a wave must cover its rows in ONE K step,
-//   since each extra step adds a full HBM round trip to the wave's critical path, and short waves finish sooner than
-//   few long ones, so 8 waves per workgroup and as many lanes per row as the row has 16-byte chunks (at most 64).
+// The plan gemv uses when block_n == 0.
+//   Throughput regime (N >= 16384 rows, several workgroups per CU): each row is read in ONE K step (lanes per row x
+//   nb x 16 bytes covers it), and each wave walks two rows in sequence.  Reading whole rows keeps the DRAM accesses of
+//   the grid in long runs: with every workgroup resident, plans that read each row in 1 KB pieces over several steps
+//   ran up to 17% slower at Llama-3-8B shapes.  Q4_0: nb 4 (8 past 256 chunks), lanes per row = chunks / nb within
+//   16..64, 4 waves; TQ2_0: nb 2, 32 lanes per row, 8 waves (its heavier dot favours more, shorter waves).
+//   Latency regime (fewer rows: every wave of the grid is resident at once): one K step where nb <= 4 allows, since
+//   each extra step adds a full HBM round trip to the wave's critical path, and short waves finish sooner than few
+//   long ones, so 8 waves per workgroup and as many lanes per row as the row has 16-byte chunks (at most 64).
 //   The fused launch quantizes the activations in every workgroup, so it halves the lanes per row (two chunks per
 //   lane), which halves the number of workgroups that pay for that staging.
+// In the latency regime the plan is a knob set of the explicit tune space; in the throughput regime the two passes per
+// wave at up to 64 lanes per row are beyond the knob mapping (which ties lanes per row to rows per wave).
 int pow2_ceil(int64_t v) {
   int p = 1;
   while (p < v) p <<= 1;
   return p;
 }
 
-void auto_config(int fmt, bool fused, int64_t n, int64_t k, int* block_n, int* nb, int* warps) {
+GemvPlan plan_of(int block_n, int nb, int waves, int lpr, int passes) {
+  GemvPlan plan;
+  plan.block_n = block_n;
+  plan.nb = nb;
+  plan.waves = waves;
+  plan.lpr_log2 = 0;
+  while ((1 << plan.lpr_log2) < lpr) ++plan.lpr_log2;
+  plan.passes = passes;
+  plan.rows_per_wave = (64 / lpr) * passes;
+  return plan;
+}
+
+GemvPlan auto_plan(int fmt, bool fused, int64_t n, int64_t k) {
   const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
   const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
   const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
-  int lpr, cand_nb, w;
-  if (n < 16384) {
-    lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
-    lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
-    const int64_t blocks_per_slot = lpr / bpb;
-    cand_nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
-    cand_nb = cand_nb < 1 ? 1 : (cand_nb > 16 ? 16 : cand_nb);
-    w = 8;
-  } else {
-    lpr = 16;
-    cand_nb = fmt == FMT_Q4_0 ? 4 : 2;
-    w = fmt == FMT_Q4_0 ? 4 : 8;
+  if (n >= 16384) {
+    int lpr, nb, w;
+    if (fmt == FMT_Q4_0) {
+      nb = chunks > 256 ? 8 : 4;
+      lpr = pow2_ceil((chunks + nb - 1) / nb);
+      lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
+      w = 4;
+    } else {
+      nb = 2;
+      lpr = 32;
+      w = 8;
+    }
+    return plan_of(w * (64 / lpr) * 2, nb, w, lpr, 2);
   }
+  int lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
+  lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
+  const int64_t blocks_per_slot = lpr / bpb;
+  int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
+  nb = nb < 1 ? 1 : (nb > 16 ? 16 : nb);
+  if (fmt == FMT_Q4_0 && nb > 4) nb = 4;
+  int w = 8;
   const int rpw = 64 / lpr;
   while (w * rpw > 128) w >>= 1;
   while (w * rpw < 8) w <<= 1;
-  *block_n = w * rpw;
-  *nb = cand_nb;
-  *warps = w;
+  return plan_of(w * rpw, nb, w, lpr, 1);
 }
 
 GemvPlan knob_plan(int block_n, int nb, int num_warps) {
@@ -138,9 +160,7 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
     return fail(KOMP_EINVAL, "%s: SW=%lld must be a multiple of 16 and >= %lld (the quant bytes of a row)", name,
                 (long long)SW, (long long)row_bytes);
   if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A) return fail(KOMP_EINVAL, "%s: mode=%d not in {0,1,2}", name, mode);
-  if (block_n == 0) {
-    auto_config(fmt, fused, N, K, &block_n, &nb, &num_warps);
-  } else {
+  if (block_n != 0) {
     if (!in_set(block_n, kBlockN, 5)) return fail(KOMP_EINVAL, "%s: block_n=%d not in {8,16,32,64,128}", name, block_n);
     if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
     if (!in_set(num_warps, kWarps, 4)) return fail(KOMP_EINVAL, "%s: num_warps=%d not in {1,2,4,8}", name, num_warps);
@@ -168,7 +188,7 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
     return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
 
-  const GemvPlan plan = knob_plan(block_n, nb, num_warps);
+  const GemvPlan plan = block_n == 0 ? auto_plan(fmt, fused, N, K) : knob_plan(block_n, nb, num_warps);
 
   const int64_t nblk = K / blk;
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
@@ -278,13 +298,18 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
   return gemv_entry(FMT_TQ2_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
 }
 
-int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
-                          int* num_warps) {
+int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps,
+                          int* lanes_per_row, int* passes) {
   (void)M;
   if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
   if (N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)
     return fail(KOMP_EINVAL, "komp_gemv_auto_config: bad argument");
-  auto_config(fmt, fused != 0, N, K, block_n, nb, num_warps);
+  const GemvPlan plan = auto_plan(fmt, fused != 0, N, K);
+  *block_n = plan.block_n;
+  *nb = plan.nb;
+  *num_warps = plan.waves;
+  if (lanes_per_row != nullptr) *lanes_per_row = 1 << plan.lpr_log2;
+  if (passes != nullptr) *passes = plan.passes;
   return KOMP_OK;
 }
 

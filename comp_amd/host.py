@@ -301,8 +301,16 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
 
 
 def auto_config(fmt, m, n, k, fused=False):
-    """(block_n, nb, num_warps) that gemv(..., block_n=None) uses for this shape, or gemv_f32 with fused=True."""
+    """(block_n, nb, num_warps) of the plan gemv(..., block_n=None) uses for this shape (gemv_f32 with fused=True).
+    Passed back as explicit knobs it reproduces the plan when auto_plan() reports lanes_per_row and passes that the
+    knob mapping gives (always below 16384 rows)."""
     return _abi.auto_config(FMT_ID[fmt], m, n, k, fused)
+
+
+def auto_plan(fmt, m, n, k, fused=False):
+    """The plan gemv(..., block_n=None) uses: rows per workgroup, nb, waves, lanes per row, passes per wave."""
+    keys = ("block_n", "nb", "waves", "lanes_per_row", "passes")
+    return dict(zip(keys, _abi.auto_plan(FMT_ID[fmt], m, n, k, fused)))
 
 
 def dp4a_probe(a, b, c, mode=2):

@@ -77,15 +77,22 @@ def test_python_errors_carry_the_message():
 
 
 @pytest.mark.parametrize("fmt,n,k", [(0, 4096, 4096), (0, 128256, 4096), (0, 4097, 4192), (1, 6912, 2560),
-                                     (1, 2560, 6912), (1, 32768, 8192), (0, 1, 32), (1, 3, 256)])  # fmt: skip
+                                     (1, 2560, 6912), (1, 32768, 8192), (0, 1, 32), (1, 3, 256), (0, 28672, 8192),
+                                     (0, 28672, 14336), (0, 4096, 14336), (0, 20000, 1024)])  # fmt: skip
 @pytest.mark.parametrize("fused", [False, True])
-def test_auto_config_is_a_legal_knob_set(fmt, n, k, fused):
-    bn, nb, nw = _abi.auto_config(fmt, 1, n, k, fused)
-    assert bn in (8, 16, 32, 64, 128) and nb in (1, 2, 4, 8, 16) and nw in (1, 2, 4, 8) and bn % nw == 0
-    if n < 16384:  # latency regime: one K step covers the row (lanes per row = 64 / rows per wave, capped at 16 rows)
-        lanes = 64 // min(bn // nw, 16)
-        blocks_per_slot = lanes if fmt == 0 else lanes // 4
-        assert nb * blocks_per_slot >= k // (32 if fmt == 0 else 256)
+def test_auto_plan(fmt, n, k, fused):
+    bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, 1, n, k, fused)
+    assert _abi.auto_config(fmt, 1, n, k, fused) == (bn, nb, nw)
+    assert nb in (1, 2, 4, 8, 16) and nw in (1, 2, 4, 8) and lanes in (4, 8, 16, 32, 64) and passes >= 1
+    assert bn == nw * (64 // lanes) * passes  # the waves' rows tile the workgroup's rows exactly
+    blocks_per_step = nb * (lanes if fmt == 0 else lanes // 4)
+    nblk = k // (32 if fmt == 0 else 256)
+    if n < 16384:  # latency regime: an explicit knob set, whose mapping gives the same lanes per row and passes
+        rpw = bn // nw
+        assert bn in (8, 16, 32, 64, 128) and lanes == 64 // min(rpw, 16) and passes == rpw // min(rpw, 16)
+        assert blocks_per_step >= nblk or (fmt == 0 and nb == 4)  # one K step unless the q4_0 nb cap applies
+    elif fmt == 0:  # throughput regime, q4_0: whole rows in one K step, two passes per wave
+        assert passes == 2 and (blocks_per_step >= nblk or lanes == 64)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

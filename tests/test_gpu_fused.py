@@ -31,8 +31,9 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
     bn, nb, nw = knobs if knobs else (None, 0, 0)
     y1, s1, q = host.gemv_f32(fmt, wq, ws, xg, n, k, bn, nb, mode, nw, store_s=True, return_q=True)
     qq = host.quantize(fmt, xg, bsums=(fmt == "tq2_0"))
-    if knobs is None:  # the knobs the fused launch planned for itself
+    if knobs is None:  # the knobs the fused launch planned for itself (these shapes plan within the knob mapping)
         bn, nb, nw = host.auto_config(fmt, m, n, k, fused=True)
+        assert host.auto_plan(fmt, m, n, k, fused=True)["passes"] == 1
     y2, s2 = host.gemv(fmt, wq, ws, qq[0], qq[1], n, k, bn, nb, mode, nw, store_s=True)
     torch.cuda.synchronize()
     assert torch.equal(s1, s2)

@@ -155,6 +155,16 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
     assert O.relerr(y, r) <= TOL
 
 
+@pytest.mark.parametrize("fmt,n,k", [("q4_0", 16384, 8192), ("q4_0", 16400, 4192), ("tq2_0", 16384, 2816),
+                                     ("q4_0", 20000, 1024)])  # fmt: skip
+def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
+    # N >= 16384: whole rows in one K step, two passes per wave (16400 and 20000 leave a partial last workgroup)
+    assert host.auto_plan(fmt, 1, n, k)["passes"] == 2
+    y, s, r, rs, _, _ = run_gemv(fmt, n, k, 1, 23, False, None, None, 2, None)
+    assert np.array_equal(s.astype(np.int64), rs)
+    assert O.relerr(y, r) <= TOL
+
+
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 4096, 4096), ("q4_0", 4097, 4192), ("q4_0", 127, 4192),
                                      ("q4_0", 16383, 4096), ("q4_0", 300, 96), ("tq2_0", 6912, 2560),
                                      ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816), ("tq2_0", 16383, 256),
