@@ -112,18 +112,21 @@ def run_graph(torch, fn, count, replays):
     return g
 
 
-def timed_steps(torch, step, ncopies, steps, warmup):
-    """Run `warmup` then exactly `steps` steps as graph replays; returns elapsed ms of the timed steps."""
-    g_full = run_graph(torch, step, ncopies, 1)
-    rem = steps % ncopies
+def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
+    """Run `warmup` then exactly `steps` steps as graph replays; returns elapsed ms of the timed steps.  Each graph holds
+    a whole number of passes over the weight copies and at least `min_graph` steps, so the gap between two replays is
+    shared by many steps, as in a decode loop captured once."""
+    per_graph = ncopies * max(1, math.ceil(min_graph / ncopies))
+    g_full = run_graph(torch, step, per_graph, 1)
+    rem = steps % per_graph
     g_rem = run_graph(torch, step, rem, 1) if rem else None
-    for _ in range(max(1, math.ceil(warmup / ncopies))):
+    for _ in range(max(1, math.ceil(warmup / per_graph))):
         g_full.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(steps // ncopies):
+    for _ in range(steps // per_graph):
         g_full.replay()
     if g_rem is not None:
         g_rem.replay()
@@ -282,9 +285,9 @@ def detail(torch, host, abi, args):
             wq, ws = copies[i % nc]
             host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, 2, 0)
 
-        reps = max(64, nc)
-        reps -= reps % nc
-        ms, _ = timed_steps(torch, call, nc, reps, nc)
+        per_graph = nc * math.ceil(64 / nc)
+        reps = 4 * per_graph
+        ms, _ = timed_steps(torch, call, nc, reps, per_graph)
         disp = dispatch_times(abi, torch, call, min(reps, 256))
         kind = "q4_0_gemv" if fmt == "q4_0" else "tq2_0_gemv"
         d_us = disp[kind][0] * 1e3 / disp[kind][1]
