@@ -6,7 +6,7 @@
 Workload (the headline): TQ2_0 (ternary, BitNet b1.58) decode steps at BitNet-2B FFN shapes.  One step runs the chain
 x[m][2560] -> W1[6912 x 2560] -> W2[2560 x 6912]: each GEMV quantizes its f32 input to q8_K inside the same launch
 (tq2_0_gemv_f32), so a step is two dependent dispatches.  The reference-shaped path (quant_q8_K then tq2_0_gemv, four
-dispatches, with the fused launches' knobs) is timed beside it and must agree bit for bit.  Weights are synthetic ternary ({-1, 0, +1} with
+dispatches) is timed beside it and must agree bit for bit (both plan alike at these shapes).  Weights are synthetic ternary ({-1, 0, +1} with
 p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), the input N(0, 1), all resident in HBM before the timed region.  Each step reads a different copy of both matrices (>= 1 GiB of copies), so no call is
 served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-graph replays, so the host launch rate
 does not bound them.
@@ -162,10 +162,14 @@ def headline(torch, host, abi, args):
     x = torch.randn((m, shapes[0][1]), generator=gen, device="cuda")
     y1 = torch.empty((m, shapes[0][0]), dtype=torch.float32, device="cuda")
     y2 = torch.empty((m, shapes[1][0]), dtype=torch.float32, device="cuda")
-    # block_n None = the library's own plan (its knobs are reported in the config)
+    # block_n None = the library's own plan for each launch (reported in the config)
     knobs = [(None, 0, 0) if args.block_n is None else (args.block_n, args.nb, args.num_warps) for _ in shapes]
-    plans = [host.auto_config("tq2_0", m, n, k, fused=True) if args.block_n is None else knobs[j]
-             for j, (n, k) in enumerate(shapes)]  # fmt: skip
+    plan_keys = ("block_n", "nb", "waves", "lanes_per_row", "passes")
+    plans = [[host.auto_plan("tq2_0", m, n, k, fused=True, mode=args.mode)[key] for key in plan_keys]
+             if args.block_n is None else list(knobs[j]) for j, (n, k) in enumerate(shapes)]  # fmt: skip
+    same_plans = args.block_n is not None or all(
+        host.auto_plan("tq2_0", m, n, k, True, args.mode) == host.auto_plan("tq2_0", m, n, k, False, args.mode)
+        for n, k in shapes)
     (n1, k1), (n2, k2) = shapes
 
     def step(i):  # fused: 2 dispatches
@@ -178,13 +182,13 @@ def headline(torch, host, abi, args):
     q2 = (torch.empty((m, k2), dtype=torch.int8, device="cuda"), torch.empty((m, k2 // 256), device="cuda"))
     u1, u2 = torch.empty_like(y1), torch.empty_like(y2)
 
-    def step_two_launch(i):  # the reference's shape: quantizer then GEMV, 4 dispatches, the fused launches' knobs
+    def step_two_launch(i):  # the reference's shape: quantizer then GEMV, 4 dispatches
         w1, s1 = copies[0][i % ncopies]
         w2, s2 = copies[1][i % ncopies]
         host.quantize_into("tq2_0", x, *q1)
-        host.gemv_into("tq2_0", w1, s1, *q1, u1, n1, k1, *plans[0][:2], args.mode, plans[0][2])
+        host.gemv_into("tq2_0", w1, s1, *q1, u1, n1, k1, *knobs[0][:2], args.mode, knobs[0][2])
         host.quantize_into("tq2_0", u1, *q2)
-        host.gemv_into("tq2_0", w2, s2, *q2, u2, n2, k2, *plans[1][:2], args.mode, plans[1][2])
+        host.gemv_into("tq2_0", w2, s2, *q2, u2, n2, k2, *knobs[1][:2], args.mode, knobs[1][2])
 
     ms, wall_ms = timed_steps(torch, step, ncopies, args.steps, args.warmup)
     # the graph must reproduce the eager result of the same (last) step bit for bit, and the fused and two-launch
@@ -196,8 +200,11 @@ def headline(torch, host, abi, args):
     torch.cuda.synchronize()
     if not (torch.equal(y1, got[0]) and torch.equal(y2, got[1])):
         raise RuntimeError("graph replay and eager outputs differ")
-    if not (torch.equal(y1, u1) and torch.equal(y2, u2)):
+    if same_plans and not (torch.equal(y1, u1) and torch.equal(y2, u2)):
         raise RuntimeError("fused and two-launch outputs differ")
+    rel = max(float((a - b).abs().max() / b.abs().max()) for a, b in ((y1, u1), (y2, u2)))
+    if rel > 1e-6:
+        raise RuntimeError(f"fused and two-launch outputs differ by {rel:.2e} (relative)")
     ms2, _ = timed_steps(torch, step_two_launch, ncopies, args.steps, args.warmup)
 
     step_bytes = sum(step_bytes_fused("tq2_0", n, k, m) for n, k in shapes)
@@ -217,7 +224,7 @@ def headline(torch, host, abi, args):
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
                           "activations quantized to q8_K inside each launch",  # fmt: skip
               "shapes_nk": [list(s) for s in shapes], "m": m, "mode": {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}[args.mode],
-              "knobs_block_n_nb_warps": [list(p) for p in plans], "cold_copies": ncopies, "seed": args.seed,
+              "plan_rows_nb_waves_lanes_passes": plans, "cold_copies": ncopies, "seed": args.seed,
               "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3), "us_per_step_graph": round(ms_per_step * 1e3, 3),
               "gemv_us_per_call_dispatch": round(g_us, 3),
               "two_launch_us_per_step_graph": round(ms2 / args.steps * 1e3, 3)}  # fmt: skip

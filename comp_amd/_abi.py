@@ -42,7 +42,7 @@ SIGNATURES = {
     "komp_tq2_0_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_q4_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_tq2_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
-    "komp_gemv_auto_config": (_INT, [_INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+    "komp_gemv_auto_config": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
     "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
@@ -94,15 +94,15 @@ def call(name, *args):
     check(getattr(lib(), name)(*args), name)
 
 
-def auto_plan(fmt_id, m, n, k, fused=False):
+def auto_plan(fmt_id, m, n, k, fused=False, mode=2):
     """(block_n, nb, num_warps, lanes_per_row, passes) of the plan block_n == 0 selects."""
     v = [ctypes.c_int() for _ in range(5)]
-    call("komp_gemv_auto_config", fmt_id, int(bool(fused)), m, n, k, *(ctypes.byref(x) for x in v))
+    call("komp_gemv_auto_config", fmt_id, int(bool(fused)), mode, m, n, k, *(ctypes.byref(x) for x in v))
     return tuple(x.value for x in v)
 
 
-def auto_config(fmt_id, m, n, k, fused=False):
-    return auto_plan(fmt_id, m, n, k, fused)[:3]
+def auto_config(fmt_id, m, n, k, fused=False, mode=2):
+    return auto_plan(fmt_id, m, n, k, fused, mode)[:3]
 
 
 def timing_begin(max_dispatches=1 << 16):

@@ -58,18 +58,24 @@ TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
 // The plan gemv uses when block_n == 0.
-//   Throughput regime (N >= 16384 rows, several workgroups per CU): each row is read in ONE K step (lanes per row x
-//   nb x 16 bytes covers it), and each wave walks two rows in sequence.  Reading whole rows keeps the DRAM accesses of
-//   the grid in long runs: with every workgroup resident, plans that read each row in 1 KB pieces over several steps
-//   ran up to 17% slower at Llama-3-8B shapes.  Q4_0: nb 4 (8 past 256 chunks), lanes per row = chunks / nb within
-//   16..64, 4 waves; TQ2_0: nb 2, 32 lanes per row, 8 waves (its heavier dot favours more, shorter waves).
-//   Latency regime (fewer rows: every wave of the grid is resident at once): one K step where nb <= 4 allows, since
-//   each extra step adds a full HBM round trip to the wave's critical path, and short waves finish sooner than few
-//   long ones, so 8 waves per workgroup and as many lanes per row as the row has 16-byte chunks (at most 64).
-//   The fused launch quantizes the activations in every workgroup, so it halves the lanes per row (two chunks per
-//   lane), which halves the number of workgroups that pay for that staging.
-// In the latency regime the plan is a knob set of the explicit tune space; in the throughput regime the two passes per
-// wave at up to 64 lanes per row are beyond the knob mapping (which ties lanes per row to rows per wave).
+//   Throughput regime (N >= 16384 rows, several workgroups per CU).  Q4_0: each row is read in ONE K step (lanes per
+//   row x nb x 16 bytes covers it) and each wave walks two rows in sequence, nb 4 (8 past 256 chunks), lanes per row
+//   = chunks / nb within 16..64, 4 waves.  Reading whole rows keeps the DRAM accesses of the grid in long runs: with
+//   every workgroup resident, plans that read each row in 1 KB pieces over several steps ran 5-17% slower at
+//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): 16 lanes per row, nb 2, 8 waves, K in
+//   steps of 8 blocks; whole-row and larger-nb plans measured 2-18% slower.
+//   Latency regime (fewer rows: every wave of the grid is resident at once), one column in dp4a mode, fused launches
+//   and TQ2_0: one workgroup per CU with ceil(N / CUs) rows, one row group per wave, one K step.  A grid of at most
+//   one workgroup per CU is spread one to a CU, so no CU stages (and, fused, quantizes) the activations twice or runs
+//   two workgroups' dots on the same SIMDs; 9-24% faster at the BitNet-2B and Llama-3-8B shapes than 8-wave
+//   workgroups of 8-16 rows.  Lanes per row start at 64 and halve while the rows would need more than 16 waves or a
+//   lane would get fewer than 1.5 of the row's 16-byte chunks.
+//   Otherwise (unfused Q4_0, other modes, 2-3 columns): 8 waves per workgroup, as many lanes per row as the row has
+//   16-byte chunks (at most 64; the fused launch halves that, since every workgroup pays for quantizing the input),
+//   and nb just large enough for one K step (Q4_0 caps it at 4), because each extra step adds a full HBM round trip to
+//   a wave's critical path.
+// The knob-mapped plans are knob sets of the explicit tune space; the two-pass Q4_0 throughput plan and the
+// one-workgroup-per-CU plans are beyond the knob mapping.
 int pow2_ceil(int64_t v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -88,23 +94,44 @@ GemvPlan plan_of(int block_n, int nb, int waves, int lpr, int passes) {
   return plan;
 }
 
-GemvPlan auto_plan(int fmt, bool fused, int64_t n, int64_t k) {
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+
+// CUs of the current device (256 on MI355X; also the answer when no device can be queried)
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int c = g_cus[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+  g_cus[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t k) {
   const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
   const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
   const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
   if (n >= 16384) {
-    int lpr, nb, w;
-    if (fmt == FMT_Q4_0) {
-      nb = chunks > 256 ? 8 : 4;
-      lpr = pow2_ceil((chunks + nb - 1) / nb);
-      lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
-      w = 4;
-    } else {
-      nb = 2;
-      lpr = 32;
-      w = 8;
+    if (fmt == FMT_TQ2_0) return plan_of(32, 2, 8, 16, 1);  // 16 lanes per row, 4 rows per wave, steps of 8 blocks
+    const int nb = chunks > 256 ? 8 : 4;
+    int lpr = pow2_ceil((chunks + nb - 1) / nb);
+    lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
+    return plan_of(4 * (64 / lpr) * 2, nb, 4, lpr, 2);  // 4 waves, two passes each
+  }
+  if (m == 1 && mode == KOMP_MODE_DP4A && (fused || fmt == FMT_TQ2_0)) {
+    const int cus = device_cus();
+    const int64_t rows = n < 1 ? 1 : (n + cus - 1) / cus;
+    int lpr = 64;
+    while (lpr > 4 && ((rows + 64 / lpr - 1) / (64 / lpr) > 16 || 2 * chunks < 3 * lpr)) lpr >>= 1;
+    const int rpp = 64 / lpr;
+    const int64_t waves = (rows + rpp - 1) / rpp;
+    if (waves <= 16) {
+      const int64_t blocks_per_slot = lpr / bpb;
+      int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
+      nb = nb < 1 ? 1 : (nb > 8 ? 8 : nb);
+      return plan_of(static_cast<int>(rows), nb, static_cast<int>(waves), lpr, 1);
     }
-    return plan_of(w * (64 / lpr) * 2, nb, w, lpr, 2);
   }
   int lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
   lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
@@ -188,7 +215,7 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
     return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
 
-  const GemvPlan plan = block_n == 0 ? auto_plan(fmt, fused, N, K) : knob_plan(block_n, nb, num_warps);
+  const GemvPlan plan = block_n == 0 ? auto_plan(fmt, fused, mode, M, N, K) : knob_plan(block_n, nb, num_warps);
 
   const int64_t nblk = K / blk;
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
@@ -298,13 +325,14 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
   return gemv_entry(FMT_TQ2_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
 }
 
-int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps,
-                          int* lanes_per_row, int* passes) {
-  (void)M;
+int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
+                          int* num_warps, int* lanes_per_row, int* passes) {
   if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
-  if (N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)
+  if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A)
+    return fail(KOMP_EINVAL, "komp_gemv_auto_config: mode=%d not in {0,1,2}", mode);
+  if (M < 1 || N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)
     return fail(KOMP_EINVAL, "komp_gemv_auto_config: bad argument");
-  const GemvPlan plan = auto_plan(fmt, fused != 0, N, K);
+  const GemvPlan plan = auto_plan(fmt, fused != 0, mode, M, N, K);
   *block_n = plan.block_n;
   *nb = plan.nb;
   *num_warps = plan.waves;

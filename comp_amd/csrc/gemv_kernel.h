@@ -97,8 +97,15 @@ __device__ __forceinline__ int tq2_0_chunk_dot(u32x4 w, const u32x4 (&x)[4], int
   }
 }
 
+// Largest workgroup an instantiation is built for.  One activation column in dp4a mode with nb <= 8 fits 16 waves
+// (at most 128 VGPRs per wave), which the one-workgroup-per-CU plans of small GEMVs use; the others stay at 8.
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
-__global__ void __launch_bounds__(512)
+constexpr int max_threads() {
+  return (MC == 1 && MODE == MODE_DP4A && NB <= 8) ? 1024 : 512;
+}
+
+template <int FMT, int MODE, int MC, int NB, bool FUSED>
+__global__ void __launch_bounds__((max_threads<FMT, MODE, MC, NB, FUSED>()))
 gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
             int nsteps, int sc_mode, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
             const int8_t* __restrict__ XQ, const float* __restrict__ XD, const float* __restrict__ X,
@@ -123,6 +130,8 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   const int grp = lane >> lpr_log2;
   const int rows_per_pass = 64 >> lpr_log2;
   const int row_base = blockIdx.x * rows_per_wg + wave * rows_per_wave;  // wave-uniform
+  // this wave's rows inside the workgroup's (a plan may give the waves more row slots than the workgroup has rows)
+  const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);  // wave-uniform, may be <= 0
   const int bpg = FMT == FMT_Q4_0 ? lpr : (lpr >> 2);  // blocks a row group covers per chunk slot
   const int bstep = bpg * NB;                            // blocks a row group covers per K step
   const int q = gl & 3;                                  // TQ2_0: chunk of the block this lane loads
@@ -139,7 +148,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
     const int p = t / nsteps;
     const int st = t - p * nsteps;
     const int rl = p * rows_per_pass + grp;
-    const bool rv = rl < rows_per_wave && row_base + rl < N;
+    const bool rv = rl < wave_rows && row_base + rl < N;
     const int64_t row0 = static_cast<int64_t>(row_base) + p * rows_per_pass;  // wave-uniform
     const uint8_t* wt = WQ + row0 * SW + static_cast<int64_t>(st) * bstep * BB + lane_w;
     const int16_t* stp = WS + row0 * nblk + st * bstep + lane_s;
@@ -162,7 +171,8 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   // ---- LDS layout ----
   // Q4_0: xlo[m][b] = activations 0..15 of block b, xhi[m][b] = 16..31, meta[m][b] = {d_x bits, -8 * sum(x)}.
   // TQ2_0: x4[m][j][b][q] = the 16 activations that pair with crumb j of chunk q; meta[m][b] = {d_x bits, -sum(x)}.
-  // Then (sc_mode 1) the scale slab [rows_per_wg][nblk], 16-byte aligned (the activation bytes are a multiple of 8).
+  // Then (sc_mode 1) the scale slab [waves * rows_per_wave][nblk] (rows past the workgroup's are never loaded nor
+  // used), 16-byte aligned (the activation bytes are a multiple of 8).
   u32x4* xv = reinterpret_cast<u32x4*>(lds);
   int2* meta = reinterpret_cast<int2*>(xv + (FMT == FMT_Q4_0 ? 2 : 16) * MC * nblk);
   u32x4* scs16 = xv + ((MC * nblk * (FMT == FMT_Q4_0 ? 40 : 264) + 15) >> 4);
@@ -351,7 +361,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
     const int st = t - p * nsteps;
     const int rl = p * rows_per_pass + grp;
     const int row = row_base + rl;
-    const bool rv = rl < rows_per_wave && row < N;
+    const bool rv = rl < wave_rows && row < N;
     if (st == 0) {
 #pragma unroll
       for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
@@ -405,13 +415,15 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   auto kern = gemv_kernel<FMT, MODE, MC, NB, FUSED>;
+  if (64 * p.waves > max_threads<FMT, MODE, MC, NB, FUSED>() || p.waves * p.rows_per_wave < p.block_n)
+    return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>((c.n + p.block_n - 1) / p.block_n));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
   // the workgroup's scale slab goes to LDS when it is small (the weight stream then issues only quant loads)
   const size_t base = gemv_lds_bytes(FMT, MC, c.k);
   const size_t sc_off = (base + 15) & ~static_cast<size_t>(15);
-  const size_t sc_bytes = static_cast<size_t>(p.block_n) * nblk * 2;
+  const size_t sc_bytes = static_cast<size_t>(p.waves) * p.rows_per_wave * nblk * 2;  // every wave's row slots
   int sc_mode = 0;
   if (nblk > 0 && nblk % 8 == 0 && reinterpret_cast<uintptr_t>(c.ws) % 16 == 0 && sc_bytes <= kScaleSlabMax &&
       sc_off + sc_bytes <= kLdsLimit)

@@ -300,17 +300,29 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
     return (y, s, q) if return_q else (y, s)
 
 
-def auto_config(fmt, m, n, k, fused=False):
-    """(block_n, nb, num_warps) of the plan gemv(..., block_n=None) uses for this shape (gemv_f32 with fused=True).
-    Passed back as explicit knobs it reproduces the plan when auto_plan() reports lanes_per_row and passes that the
-    knob mapping gives (always below 16384 rows)."""
-    return _abi.auto_config(FMT_ID[fmt], m, n, k, fused)
+def auto_config(fmt, m, n, k, fused=False, mode=2):
+    """(block_n, nb, num_warps) of the plan gemv(..., block_n=None, mode=mode) uses for this shape on the current
+    device (gemv_f32 with fused=True).  Passed back as explicit knobs it reproduces the plan only when it is a knob
+    set and auto_plan() reports the lanes_per_row and passes that the knob mapping gives."""
+    return _abi.auto_config(FMT_ID[fmt], m, n, k, fused, mode)
 
 
-def auto_plan(fmt, m, n, k, fused=False):
+def auto_plan(fmt, m, n, k, fused=False, mode=2):
     """The plan gemv(..., block_n=None) uses: rows per workgroup, nb, waves, lanes per row, passes per wave."""
     keys = ("block_n", "nb", "waves", "lanes_per_row", "passes")
-    return dict(zip(keys, _abi.auto_plan(FMT_ID[fmt], m, n, k, fused)))
+    return dict(zip(keys, _abi.auto_plan(FMT_ID[fmt], m, n, k, fused, mode)))
+
+
+def knob_equivalent(fmt, m, n, k, fused=False, mode=2):
+    """The explicit knobs that run exactly the auto plan, or None when the plan is beyond the knob mapping."""
+    p = auto_plan(fmt, m, n, k, fused, mode)
+    bn, w = p["block_n"], p["waves"]
+    if bn not in (8, 16, 32, 64, 128) or w not in (1, 2, 4, 8) or bn % w:
+        return None
+    rpw = bn // w
+    if p["lanes_per_row"] != 64 // min(rpw, 16) or p["passes"] != rpw // min(rpw, 16):
+        return None
+    return bn, p["nb"], w
 
 
 def dp4a_probe(a, b, c, mode=2):

@@ -83,16 +83,17 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
                         float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
                         int mode, int num_warps, void* stream);
 
-/* The plan that block_n == 0 selects for a GEMV shape; fmt 0 = q4_0, 1 = tq2_0; fused != 0 for komp_q4_0_gemv_f32 /
- * komp_tq2_0_gemv_f32 (which plan fewer, wider workgroups, since each quantizes the input).  block_n receives the rows
- * per workgroup, nb the 16-byte weight chunks each lane loads per row per K step, num_warps the waves per workgroup,
- * and (when not NULL) lanes_per_row the lanes that share a row and passes the row groups each wave walks in sequence.
- * The explicit knobs map (block_n, nb, num_warps) to lanes_per_row = 64 / min(block_n / num_warps, 16) and passes =
- * (block_n / num_warps) / min(block_n / num_warps, 16); an auto plan with other values (N >= 16384: whole rows in one
- * K step, two passes per wave) has no explicit knob equivalent.
+/* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0; fused != 0 for
+ * komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32; mode as in the GEMV entries; M the activation columns.  block_n receives
+ * the rows per workgroup, nb the 16-byte weight chunks each lane loads per row per K step, num_warps the waves per
+ * workgroup, and (when not NULL) lanes_per_row the lanes that share a row and passes the row groups each wave walks
+ * in sequence.  The explicit knobs map (block_n, nb, num_warps) to lanes_per_row = 64 / min(block_n / num_warps, 16)
+ * and passes = (block_n / num_warps) / min(block_n / num_warps, 16); an auto plan with other values, or with
+ * block_n / num_warps outside the knob sets (one workgroup of ceil(N / CUs) rows per CU, up to 16 waves, for small
+ * single-column GEMVs), has no explicit knob equivalent.
  * No reference counterpart: the reference always takes the knobs from its caller. */
-int komp_gemv_auto_config(int fmt, int fused, int64_t M, int64_t N, int64_t K, int* block_n, int* nb, int* num_warps,
-                          int* lanes_per_row, int* passes);
+int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
+                          int* num_warps, int* lanes_per_row, int* passes);
 
 /* OUT[i] = dp4a(A[i], B[i], C[i]) for i < n; mode KOMP_MODE_DP4A (hardware) or KOMP_MODE_DP4A_EMU.
  * Replaces: kernels.dp4a_probe (src/komp/kernels.py:145-149). */

@@ -81,18 +81,39 @@ def test_python_errors_carry_the_message():
                                      (0, 28672, 14336), (0, 4096, 14336), (0, 20000, 1024)])  # fmt: skip
 @pytest.mark.parametrize("fused", [False, True])
 def test_auto_plan(fmt, n, k, fused):
+    # without a device the library plans for 256 CUs (MI355X)
     bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, 1, n, k, fused)
     assert _abi.auto_config(fmt, 1, n, k, fused) == (bn, nb, nw)
-    assert nb in (1, 2, 4, 8, 16) and nw in (1, 2, 4, 8) and lanes in (4, 8, 16, 32, 64) and passes >= 1
-    assert bn == nw * (64 // lanes) * passes  # the waves' rows tile the workgroup's rows exactly
+    assert nb in (1, 2, 4, 8, 16) and lanes in (4, 8, 16, 32, 64) and passes >= 1
+    assert nw * (64 // lanes) * passes >= bn  # the waves' row slots cover the workgroup's rows
     blocks_per_step = nb * (lanes if fmt == 0 else lanes // 4)
     nblk = k // (32 if fmt == 0 else 256)
-    if n < 16384:  # latency regime: an explicit knob set, whose mapping gives the same lanes per row and passes
+    if n < 16384 and (fused or fmt == 1):  # one workgroup per CU, one row group per wave, one K step up to nb 8
+        assert bn == -(-n // 256) and 1 <= nw <= 16 and passes == 1 and nw == -(-bn // (64 // lanes))
+        assert blocks_per_step >= nblk or nb == 8
+    elif n < 16384:  # unfused q4_0: an explicit knob set whose mapping gives the same lanes per row and passes
         rpw = bn // nw
-        assert bn in (8, 16, 32, 64, 128) and lanes == 64 // min(rpw, 16) and passes == rpw // min(rpw, 16)
-        assert blocks_per_step >= nblk or (fmt == 0 and nb == 4)  # one K step unless the q4_0 nb cap applies
+        assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and bn % nw == 0
+        assert lanes == 64 // min(rpw, 16) and passes == rpw // min(rpw, 16)
+        assert blocks_per_step >= nblk or nb == 4  # one K step unless the q4_0 nb cap applies
     elif fmt == 0:  # throughput regime, q4_0: whole rows in one K step, two passes per wave
-        assert passes == 2 and (blocks_per_step >= nblk or lanes == 64)
+        assert passes == 2 and nw == 4 and bn == nw * (64 // lanes) * 2 and (blocks_per_step >= nblk or lanes == 64)
+    else:
+        assert (bn, nb, nw, lanes, passes) == (32, 2, 8, 16, 1)
+
+
+@pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])
+def test_auto_plan_other_modes_and_columns_use_knob_sets(mode, m):
+    for fmt, n, k in ((0, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912)):
+        for fused in (False, True):
+            bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, m, n, k, fused, mode)
+            assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and lanes == 64 // min(bn // nw, 16)
+
+
+def test_auto_plan_bitnet_shapes():
+    # the headline shapes: one workgroup per CU (256 CUs), fused and unfused alike
+    assert _abi.auto_plan(1, 1, 2560, 6912, True) == _abi.auto_plan(1, 1, 2560, 6912, False) == (10, 2, 10, 64, 1)
+    assert _abi.auto_plan(1, 1, 6912, 2560, True) == _abi.auto_plan(1, 1, 6912, 2560, False) == (27, 4, 7, 16, 1)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

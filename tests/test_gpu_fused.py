@@ -31,20 +31,20 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
     bn, nb, nw = knobs if knobs else (None, 0, 0)
     y1, s1, q = host.gemv_f32(fmt, wq, ws, xg, n, k, bn, nb, mode, nw, store_s=True, return_q=True)
     qq = host.quantize(fmt, xg, bsums=(fmt == "tq2_0"))
-    if knobs is None:  # the knobs the fused launch planned for itself (these shapes plan within the knob mapping)
-        bn, nb, nw = host.auto_config(fmt, m, n, k, fused=True)
-        assert host.auto_plan(fmt, m, n, k, fused=True)["passes"] == 1
     y2, s2 = host.gemv(fmt, wq, ws, qq[0], qq[1], n, k, bn, nb, mode, nw, store_s=True)
     torch.cuda.synchronize()
     assert torch.equal(s1, s2)
-    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    # with block_n=None each launch plans for itself: Y is bit-identical when both planned alike (the f32 sums then
+    # run in the same order), and within the oracle tolerance below otherwise
+    if knobs or host.auto_plan(fmt, m, n, k, True, mode) == host.auto_plan(fmt, m, n, k, False, mode):
+        assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
     for a, b in zip(q, qq):
         assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int16 else a, b.view(torch.uint8) if b.dtype != torch.int16 else b)
     rq, rd, rb = O.quantize(fmt, x)
     assert np.array_equal(q[0].cpu().numpy(), rq)
     r, rs = O.gemv(fmt, host.split(fmt, W, n, k)[0], host.split(fmt, W, n, k)[1], rq, rd, n, k)
     assert np.array_equal(s1.cpu().numpy().astype(np.int64), rs)
-    assert O.relerr(y1.cpu().numpy(), r) <= 1e-5
+    assert O.relerr(y1.cpu().numpy(), r) <= 1e-5 and O.relerr(y2.cpu().numpy(), r) <= 1e-5
 
 
 def test_fused_without_q_outputs():

@@ -158,8 +158,8 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 16384, 8192), ("q4_0", 16400, 4192), ("tq2_0", 16384, 2816),
                                      ("q4_0", 20000, 1024)])  # fmt: skip
 def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
-    # N >= 16384: whole rows in one K step, two passes per wave (16400 and 20000 leave a partial last workgroup)
-    assert host.auto_plan(fmt, 1, n, k)["passes"] == 2
+    # N >= 16384 (16400 and 20000 leave a partial last workgroup); q4_0 reads whole rows in one K step, two passes
+    assert host.auto_plan(fmt, 1, n, k)["passes"] == (2 if fmt == "q4_0" else 1)
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, 1, 23, False, None, None, 2, None)
     assert np.array_equal(s.astype(np.int64), rs)
     assert O.relerr(y, r) <= TOL
@@ -223,3 +223,25 @@ def test_scale_slab_and_per_tile_scales_agree(fmt, n, k, knobs):
     assert torch.equal(s1, s2) and torch.equal(y1.view(torch.int32), y2.view(torch.int32))
     r, rs = O.gemv(fmt, wq, ws, *O.quantize(fmt, x)[:2], n, k)
     assert np.array_equal(s1.cpu().numpy().astype(np.int64), rs) and O.relerr(y1.cpu().numpy(), r) <= TOL
+
+
+@pytest.mark.parametrize("fmt,n,k,fused", [("tq2_0", 6912, 2560, True), ("tq2_0", 6913, 2816, False),
+                                           ("q4_0", 4097, 4096, True), ("tq2_0", 4097, 2048, False),
+                                           ("tq2_0", 300, 1280, False), ("q4_0", 6144, 4096, True),
+                                           ("q4_0", 4096, 14336, True), ("tq2_0", 2560, 6912, True)])  # fmt: skip
+def test_one_workgroup_per_cu_plans(fmt, n, k, fused):
+    # small single-column GEMVs plan one workgroup of ceil(N / CUs) rows per CU; the first five shapes give the waves
+    # more row slots than rows (clipped per wave), q4_0 4097x4096 and tq2_0 4097x2048 with the scale slab in LDS
+    p = host.auto_plan(fmt, 1, n, k, fused)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert p["block_n"] == -(-n // cus) and p["passes"] == 1
+    W, x = O.problem(fmt, n, k, 1, 29)
+    wq, ws = host.split(fmt, W, n, k)
+    if fused:
+        y, s = host.gemv_f32(fmt, dev(wq), dev(ws), dev(x), n, k, store_s=True)
+    else:
+        xq, xd, *_ = host.quantize(fmt, dev(x))
+        y, s = host.gemv(fmt, dev(wq), dev(ws), xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    torch.cuda.synchronize()
+    r, rs = O.gemv(fmt, wq, ws, *O.quantize(fmt, x)[:2], n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs) and O.relerr(y.cpu().numpy(), r) <= TOL
