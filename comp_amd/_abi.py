@@ -42,6 +42,8 @@ SIGNATURES = {
     "komp_tq2_0_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_q4_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_tq2_0_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_q4_0_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_tq2_0_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_gemv_auto_config": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
     "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),

@@ -160,32 +160,45 @@ GemvPlan knob_plan(int block_n, int nb, int num_warps) {
   return plan;
 }
 
-struct GemvArgs {
+struct GemvMat {
   const uint8_t* wq;
   const int16_t* ws;
-  const int8_t* xq;   // unfused
+  float* y;
+  int32_t* s;
+  int64_t n;
+  int64_t sw;
+};
+
+struct GemvArgs {
+  const GemvMat* mats;  // 1..kMaxSegs matrices sharing the activation input
+  int count;
+  const int8_t* xq;     // unfused
   const float* xd;
-  const float* x;     // fused
+  const float* x;       // fused
   int8_t* xq_out;
   float* xd_out;
   int16_t* xb_out;
-  float* y;
-  int32_t* s;
 };
 
-int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t M, int64_t K, int block_n, int nb,
                int mode, int num_warps, void* stream) {
-  const char* name = fused ? (fmt == FMT_Q4_0 ? "komp_q4_0_gemv_f32" : "komp_tq2_0_gemv_f32")
-                           : (fmt == FMT_Q4_0 ? "komp_q4_0_gemv" : "komp_tq2_0_gemv");
   const int blk = fmt == FMT_Q4_0 ? 32 : 256;
   const int64_t row_bytes = fmt == FMT_Q4_0 ? K / 2 : K / 4;
-  if (M < 0 || N < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (M=%lld N=%lld K=%lld)", name,
-                                          (long long)M, (long long)N, (long long)K);
-  if (N > INT32_MAX || K > INT32_MAX) return fail(KOMP_EINVAL, "%s: N and K must be < 2^31", name);
+  if (a.count < 1 || a.count > kMaxSegs || a.mats == nullptr)
+    return fail(KOMP_EINVAL, "%s: count=%d must be 1..%d", name, a.count, kMaxSegs);
+  if (M < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (M=%lld K=%lld)", name, (long long)M, (long long)K);
+  if (K > INT32_MAX) return fail(KOMP_EINVAL, "%s: K must be < 2^31", name);
   if (K % blk) return fail(KOMP_EINVAL, "%s: K=%lld is not a multiple of the %d-value block", name, (long long)K, blk);
-  if (SW < row_bytes || SW % 16)
-    return fail(KOMP_EINVAL, "%s: SW=%lld must be a multiple of 16 and >= %lld (the quant bytes of a row)", name,
-                (long long)SW, (long long)row_bytes);
+  int64_t total_rows = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const GemvMat& w = a.mats[i];
+    if (w.n < 0 || w.n > INT32_MAX) return fail(KOMP_EINVAL, "%s: N=%lld out of range", name, (long long)w.n);
+    if (w.n > 0 && (w.sw < row_bytes || w.sw % 16))  // (a matrix without rows has no row stride)
+      return fail(KOMP_EINVAL, "%s: SW=%lld must be a multiple of 16 and >= %lld (the quant bytes of a row)", name,
+                  (long long)w.sw, (long long)row_bytes);
+    total_rows += w.n;
+  }
+  if (total_rows > INT32_MAX) return fail(KOMP_EINVAL, "%s: the matrices' rows must total < 2^31", name);
   if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A) return fail(KOMP_EINVAL, "%s: mode=%d not in {0,1,2}", name, mode);
   if (block_n != 0) {
     if (!in_set(block_n, kBlockN, 5)) return fail(KOMP_EINVAL, "%s: block_n=%d not in {8,16,32,64,128}", name, block_n);
@@ -198,48 +211,79 @@ int gemv_entry(int fmt, bool fused, const GemvArgs& a, int64_t M, int64_t N, int
     return fail(KOMP_EINVAL, "%s: XD / XB outputs need XQ as well", name);
   if (fused && a.xq_out != nullptr && a.xd_out == nullptr)
     return fail(KOMP_EINVAL, "%s: the XQ output needs XD as well", name);
-  if (M == 0 || N == 0) return KOMP_OK;
-  if (K > 0 && (a.wq == nullptr || a.ws == nullptr))
-    return fail(KOMP_EINVAL, "%s: WQ and WS must not be NULL", name);
+  if (M == 0 || total_rows == 0) return KOMP_OK;
   if (K > 0 && !fused && (a.xq == nullptr || a.xd == nullptr))
     return fail(KOMP_EINVAL, "%s: XQ and XD must not be NULL", name);
   if (K > 0 && fused && a.x == nullptr) return fail(KOMP_EINVAL, "%s: X must not be NULL", name);
-  if (a.y == nullptr) return fail(KOMP_EINVAL, "%s: Y must not be NULL", name);
-  if (!aligned(a.wq, 16) || !aligned(a.xq, 16) || !aligned(a.x, 16))
-    return fail(KOMP_EINVAL, "%s: WQ, XQ and X must be 16-byte aligned", name);
-  if (!aligned(a.ws, 2) || !aligned(a.xd, 4) || !aligned(a.y, 4) || !aligned(a.s, 4) || !aligned(a.xq_out, 4) ||
-      !aligned(a.xd_out, 4) || !aligned(a.xb_out, 2))
-    return fail(KOMP_EINVAL, "%s: WS, XD, Y, S and the q8 outputs must be aligned to their element size", name);
+  if (!aligned(a.xq, 16) || !aligned(a.x, 16)) return fail(KOMP_EINVAL, "%s: XQ and X must be 16-byte aligned", name);
+  if (!aligned(a.xd, 4) || !aligned(a.xq_out, 4) || !aligned(a.xd_out, 4) || !aligned(a.xb_out, 2))
+    return fail(KOMP_EINVAL, "%s: XD and the q8 outputs must be aligned to their element size", name);
+  GemvMat mats[kMaxSegs];  // the matrices with rows
+  int count = 0;
+  for (int i = 0; i < a.count; ++i) {
+    const GemvMat& w = a.mats[i];
+    if (w.n == 0) continue;
+    if (K > 0 && (w.wq == nullptr || w.ws == nullptr)) return fail(KOMP_EINVAL, "%s: WQ and WS must not be NULL", name);
+    if (w.y == nullptr) return fail(KOMP_EINVAL, "%s: Y must not be NULL", name);
+    if (!aligned(w.wq, 16)) return fail(KOMP_EINVAL, "%s: WQ must be 16-byte aligned", name);
+    if (!aligned(w.ws, 2) || !aligned(w.y, 4) || !aligned(w.s, 4))
+      return fail(KOMP_EINVAL, "%s: WS, Y and S must be aligned to their element size", name);
+    mats[count++] = w;
+  }
   int mc = static_cast<int>(M < 3 ? M : 3);
   while (mc > 1 && gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax) --mc;
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
     return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
 
-  const GemvPlan plan = block_n == 0 ? auto_plan(fmt, fused, mode, M, N, K) : knob_plan(block_n, nb, num_warps);
+  const GemvPlan plan =
+      block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K) : knob_plan(block_n, nb, num_warps);
 
   const int64_t nblk = K / blk;
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
-    GemvCall c;
+    GemvCall c = {};
     c.fmt = fmt;
-    c.wq = a.wq;
-    c.ws = a.ws;
+    c.wq = mats[0].wq;
+    c.ws = mats[0].ws;
     c.xq = fused ? nullptr : a.xq + m0 * K;
     c.xd = fused ? nullptr : a.xd + m0 * nblk;
     c.x = fused ? a.x + m0 * K : nullptr;
     c.xq_out = a.xq_out != nullptr ? a.xq_out + m0 * K : nullptr;
     c.xd_out = a.xd_out != nullptr ? a.xd_out + m0 * nblk : nullptr;
     c.xb_out = a.xb_out != nullptr ? a.xb_out + m0 * (K / 16) : nullptr;
-    c.y = a.y + m0 * N;
-    c.s = a.s != nullptr ? a.s + m0 * N * nblk : nullptr;
+    c.y = mats[0].y + m0 * mats[0].n;
+    c.s = mats[0].s != nullptr ? mats[0].s + m0 * mats[0].n * nblk : nullptr;
     c.m = static_cast<int>(M - m0 < mc ? M - m0 : mc);
-    c.n = static_cast<int>(N);
+    c.n = static_cast<int>(mats[0].n);
     c.k = static_cast<int>(K);
-    c.sw = SW;
+    c.sw = mats[0].sw;
     c.mode = mode;
+    c.nseg = count;
+    for (int i = 0; count > 1 && i < count; ++i) {
+      c.segs.wq[i] = mats[i].wq;
+      c.segs.ws[i] = mats[i].ws;
+      c.segs.y[i] = mats[i].y + m0 * mats[i].n;
+      c.segs.sw[i] = mats[i].sw;
+      c.segs.n[i] = static_cast<int>(mats[i].n);
+    }
     const int st = hip_status(launch_gemv(c, plan, static_cast<hipStream_t>(stream)), name);
     if (st != KOMP_OK) return st;
   }
   return KOMP_OK;
+}
+
+int gemv_multi_entry(int fmt, int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                     const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X, int64_t M,
+                     int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
+  const char* name = fmt == FMT_Q4_0 ? "komp_q4_0_gemv_multi" : "komp_tq2_0_gemv_multi";
+  if (count < 1 || count > kMaxSegs) return fail(KOMP_EINVAL, "%s: count=%d must be 1..%d", name, count, kMaxSegs);
+  if (WQ == nullptr || WS == nullptr || Y == nullptr || N == nullptr || SW == nullptr)
+    return fail(KOMP_EINVAL, "%s: the WQ, WS, Y, N and SW arrays must not be NULL", name);
+  if ((X != nullptr) == (XQ != nullptr || XD != nullptr))
+    return fail(KOMP_EINVAL, "%s: give either XQ and XD (q8 input) or X (f32 input)", name);
+  GemvMat mats[kMaxSegs];
+  for (int i = 0; i < count; ++i) mats[i] = GemvMat{WQ[i], WS[i], Y[i], nullptr, N[i], SW[i]};
+  const GemvArgs a{mats, count, XQ, XD, X, nullptr, nullptr, nullptr};
+  return gemv_entry(fmt, X != nullptr, name, a, M, K, block_n, nb, mode, num_warps, stream);
 }
 
 }  // namespace
@@ -300,29 +344,45 @@ int komp_quant_q8_K(const float* X, int8_t* XQ, float* XD, int16_t* XB, int64_t 
 int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                    void* stream) {
-  const GemvArgs a{WQ, WS, XQ, XD, nullptr, nullptr, nullptr, nullptr, Y, S};
-  return gemv_entry(FMT_Q4_0, false, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_Q4_0, false, "komp_q4_0_gemv", a, M, K, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                     int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                     void* stream) {
-  const GemvArgs a{WQ, WS, XQ, XD, nullptr, nullptr, nullptr, nullptr, Y, S};
-  return gemv_entry(FMT_TQ2_0, false, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_TQ2_0, false, "komp_tq2_0_gemv", a, M, K, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_q4_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
                        float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
                        int mode, int num_warps, void* stream) {
-  const GemvArgs a{WQ, WS, nullptr, nullptr, X, XQ, XD, XB, Y, S};
-  return gemv_entry(FMT_Q4_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, nullptr, nullptr, X, XQ, XD, XB};
+  return gemv_entry(FMT_Q4_0, true, "komp_q4_0_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
                         float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
                         int mode, int num_warps, void* stream) {
-  const GemvArgs a{WQ, WS, nullptr, nullptr, X, XQ, XD, XB, Y, S};
-  return gemv_entry(FMT_TQ2_0, true, a, M, N, K, SW, block_n, nb, mode, num_warps, stream);
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, nullptr, nullptr, X, XQ, XD, XB};
+  return gemv_entry(FMT_TQ2_0, true, "komp_tq2_0_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                         const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                         int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
+  return gemv_multi_entry(FMT_Q4_0, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                          const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                          int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
+  return gemv_multi_entry(FMT_TQ2_0, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);
 }
 
 int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,

@@ -106,11 +106,11 @@ constexpr int max_threads() {
 
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 __global__ void __launch_bounds__((max_threads<FMT, MODE, MC, NB, FUSED>()))
-gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
-            int nsteps, int sc_mode, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
+gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
+            int nsteps, int sc_mode, int nseg, const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
             const int8_t* __restrict__ XQ, const float* __restrict__ XD, const float* __restrict__ X,
-            int8_t* __restrict__ XQo, float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y,
-            int32_t* __restrict__ S) {
+            int8_t* __restrict__ XQo, float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y1,
+            int32_t* __restrict__ S, const GemvSegs segs) {
   // The scalars come first and the host precomputes every quotient (nblk = K / block, rows per wave, K steps), so
   // with the first 16 argument dwords preloaded into SGPRs the first weight load needs no memory round trip for its
   // address and the prologue no integer division.
@@ -119,8 +119,29 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   // multiple of 8 scales) are staged in LDS with the activations, and the weight stream issues only quant loads.
   // sc_mode 0: each lane loads its scales beside its quants (one 2-byte load per 16-byte chunk), for slabs that are
   // too large for LDS or not 16-byte aligned.
+  //
+  // nseg > 1: several matrices sharing the input; the workgroup takes its matrix from segs (scalar compares on the
+  // argument block) and from there on works as for one matrix, on its row range within it.
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int BB = FMT == FMT_Q4_0 ? 16 : 64;  // quant bytes per block
+  int N = N1;
+  int64_t SW = SW1;
+  const uint8_t* __restrict__ WQ = WQ1;
+  const int16_t* __restrict__ WS = WS1;
+  float* __restrict__ Y = Y1;
+  int wg = blockIdx.x;  // workgroup index within its matrix
+  if (nseg > 1) {
+    int sg = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; ++i)
+      if (i < nseg && wg >= segs.first_wg[i]) sg = i;
+    N = segs.n[sg];
+    SW = segs.sw[sg];
+    WQ = segs.wq[sg];
+    WS = segs.ws[sg];
+    Y = segs.y[sg];
+    wg -= segs.first_wg[sg];
+  }
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int lane = tid & 63;
@@ -129,7 +150,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   const int gl = lane & (lpr - 1);
   const int grp = lane >> lpr_log2;
   const int rows_per_pass = 64 >> lpr_log2;
-  const int row_base = blockIdx.x * rows_per_wg + wave * rows_per_wave;  // wave-uniform
+  const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   // this wave's rows inside the workgroup's (a plan may give the waves more row slots than the workgroup has rows)
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);  // wave-uniform, may be <= 0
   const int bpg = FMT == FMT_Q4_0 ? lpr : (lpr >> 2);  // blocks a row group covers per chunk slot
@@ -182,7 +203,7 @@ gemv_kernel(int N, int K, int64_t SW, int nblk, int rows_per_wg, int rows_per_wa
   // (global_load_lds_dwordx4: lane i's 16 bytes land at the wave's LDS base + 16 i), so the copy holds no registers;
   // the barrier after the activation staging waits for it with the other loads.
   if (sc_mode == 1) {
-    const int wg_row0 = blockIdx.x * rows_per_wg;
+    const int wg_row0 = wg * rows_per_wg;
     const int sc_rows = min(rows_per_wg, N - wg_row0);
     const int pieces = (sc_rows * nblk) >> 3;  // 16-byte pieces
     const u32x4* src = reinterpret_cast<const u32x4*>(WS + static_cast<int64_t>(wg_row0) * nblk);
@@ -417,7 +438,16 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   auto kern = gemv_kernel<FMT, MODE, MC, NB, FUSED>;
   if (64 * p.waves > max_threads<FMT, MODE, MC, NB, FUSED>() || p.waves * p.rows_per_wave < p.block_n)
     return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>((c.n + p.block_n - 1) / p.block_n));
+  GemvSegs segs = c.segs;
+  int64_t groups = (c.n + p.block_n - 1) / p.block_n;
+  if (c.nseg > 1) {
+    groups = 0;
+    for (int i = 0; i < c.nseg; ++i) {
+      segs.first_wg[i] = static_cast<int>(groups);
+      groups += (segs.n[i] + p.block_n - 1) / p.block_n;
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
   // the workgroup's scale slab goes to LDS when it is small (the weight stream then issues only quant loads)
@@ -425,8 +455,9 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const size_t sc_off = (base + 15) & ~static_cast<size_t>(15);
   const size_t sc_bytes = static_cast<size_t>(p.waves) * p.rows_per_wave * nblk * 2;  // every wave's row slots
   int sc_mode = 0;
-  if (nblk > 0 && nblk % 8 == 0 && reinterpret_cast<uintptr_t>(c.ws) % 16 == 0 && sc_bytes <= kScaleSlabMax &&
-      sc_off + sc_bytes <= kLdsLimit)
+  bool ws_aligned = reinterpret_cast<uintptr_t>(c.ws) % 16 == 0;
+  for (int i = 0; c.nseg > 1 && i < c.nseg; ++i) ws_aligned = ws_aligned && reinterpret_cast<uintptr_t>(segs.ws[i]) % 16 == 0;
+  if (nblk > 0 && nblk % 8 == 0 && ws_aligned && sc_bytes <= kScaleSlabMax && sc_off + sc_bytes <= kLdsLimit)
     sc_mode = 1;
   const unsigned lds = static_cast<unsigned>(sc_mode != 0 ? sc_off + sc_bytes : base);
   static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
@@ -442,11 +473,12 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const int rows_per_wave = p.rows_per_wave;
   if (tm.on) {
     hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.k, c.sw, nblk, p.block_n,
-                          rows_per_wave, p.lpr_log2, p.passes, nsteps, sc_mode, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out,
-                          c.xd_out, c.xb_out, c.y, c.s);
+                          rows_per_wave, p.lpr_log2, p.passes, nsteps, sc_mode, c.nseg, c.wq, c.ws, c.xq, c.xd, c.x,
+                          c.xq_out, c.xd_out, c.xb_out, c.y, c.s, segs);
   } else {
     hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, c.k, c.sw, nblk, p.block_n, rows_per_wave, p.lpr_log2,
-                       p.passes, nsteps, sc_mode, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y, c.s);
+                       p.passes, nsteps, sc_mode, c.nseg, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y,
+                       c.s, segs);
   }
   return hipGetLastError();
 }

@@ -21,6 +21,18 @@ struct GemvPlan {
   int passes;         // row groups each wave walks in sequence
 };
 
+// Several weight matrices that share one activation input, in one launch: segment i covers workgroups
+// [first_wg[i], first_wg[i + 1]) (the last one up to the grid's end), and no workgroup straddles two matrices.
+constexpr int kMaxSegs = 4;
+struct GemvSegs {
+  const uint8_t* wq[kMaxSegs];
+  const int16_t* ws[kMaxSegs];
+  float* y[kMaxSegs];
+  int64_t sw[kMaxSegs];
+  int n[kMaxSegs];
+  int first_wg[kMaxSegs];
+};
+
 struct GemvCall {
   int fmt;
   const uint8_t* wq;
@@ -38,6 +50,8 @@ struct GemvCall {
   int k;
   int64_t sw;     // WQ row stride in bytes
   int mode;
+  int nseg;       // 1: the single matrix above; 2..kMaxSegs: the matrices in segs (wq / ws / y / n / sw above unused)
+  GemvSegs segs;  // first_wg is filled in at launch, from the plan
 };
 
 // Dispatch hook: every launch goes through it so the tuning harness can time dispatches with hipExtLaunchKernel events.

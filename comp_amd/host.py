@@ -18,6 +18,8 @@ Differences a caller can observe:
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -146,7 +148,7 @@ def _check_gemv(fmt, wq, ws, xq, xd, n, k):
     _need(ws, "ws", torch.int16, 2)
     _need(xq, "xq", torch.int8, 2)
     _need(xd, "xd", torch.float32, 2)
-    if wq.stride(1) != 1:
+    if wq.numel() and wq.stride(1) != 1:
         raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
     nblk = k // f["block"]
     if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
@@ -230,7 +232,7 @@ def _check_weights(fmt, wq, ws, n, k):
     f = FORMATS[fmt]
     _need(wq, "wq", torch.uint8, 2)
     _need(ws, "ws", torch.int16, 2)
-    if wq.stride(1) != 1:
+    if wq.numel() and wq.stride(1) != 1:
         raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
     nblk = k // f["block"]
     if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
@@ -243,7 +245,8 @@ def _check_weights(fmt, wq, ws, n, k):
 def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps=4, s=None, xq=None, xd=None,
                   xb=None):  # fmt: skip
     """Quantize-and-GEMV in one launch into preallocated outputs: x f32 [M][K] -> y f32 [M][N] (and s, and the q8
-    planes xq / xd / xb when given, as quantize() would return them).  Bit-identical to quantize() then gemv() with the same knobs."""
+    planes xq / xd / xb when given, as quantize() would return them).  Bit-identical to quantize() then gemv() with
+    the same knobs."""
     nblk = _check_weights(fmt, wq, ws, n, k)
     _need(x, "x", torch.float32, 2)
     if x.shape[1] != k or not x.is_contiguous():
@@ -298,6 +301,64 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
             q = q + (torch.empty((m, k // 16), dtype=torch.int16, device=x.device),)
     gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n, nb, mode, num_warps, s, *(q or ()))
     return (y, s, q) if return_q else (y, s)
+
+
+def gemv_multi_into(fmt, mats, ys, k, xq=None, xd=None, x=None, block_n=None, nb=4, mode=2, num_warps=4):
+    """Several weight matrices that share one input, in one launch: mats = [(wq, ws, n), ...] (1..4 split planes, as
+    gemv takes them), ys = preallocated outputs f32 [M][n] in the same order.  Give xq and xd (q8 planes, as gemv) or
+    x (f32 [M][K], quantized inside the launch, as gemv_f32).  With the same knobs each ys[i] equals gemv / gemv_f32
+    on matrix i alone, bit for bit; block_n=None plans for the matrices' rows together.  For decoders that store Q, K,
+    V (or gate, up) apart: one dispatch, and one quantization per workgroup, instead of one per matrix.  No reference
+    counterpart (the reference launches one matrix per kernel)."""
+    if not 1 <= len(mats) <= 4 or len(ys) != len(mats):
+        raise _abi.KompArgumentError("gemv_multi: 1..4 matrices, one output each")
+    if (x is None) == (xq is None or xd is None) or (x is not None and (xq is not None or xd is not None)):
+        raise _abi.KompArgumentError("gemv_multi: give either xq and xd (q8 input) or x (f32 input)")
+    if x is not None:
+        _need(x, "x", torch.float32, 2)
+        if x.shape[1] != k or not x.is_contiguous():
+            raise _abi.KompArgumentError(f"x must be a contiguous [M][{k}] tensor, got {tuple(x.shape)}")
+        ref, m = x, x.shape[0]
+        blk = FORMATS[fmt]["block"]
+        if k % blk:
+            raise _abi.KompArgumentError(f"{fmt}: K={k} is not a multiple of {blk}")
+    for i, ((wq, ws, n), y) in enumerate(zip(mats, ys)):
+        if x is None:
+            m, _ = _check_gemv(fmt, wq, ws, xq, xd, n, k)
+            ref = xq
+        else:
+            _check_weights(fmt, wq, ws, n, k)
+        _need(y, f"ys[{i}]", torch.float32, 2)
+        if tuple(y.shape) != (m, n) or not y.is_contiguous():
+            raise _abi.KompArgumentError(f"ys[{i}] must be a contiguous [{m}][{n}] tensor")
+        for t, name in ((wq, "wq"), (ws, "ws"), (y, "y")):
+            if t.device != ref.device:
+                raise _abi.KompArgumentError(f"matrix {i}: {name} is on {t.device}, the input on {ref.device}")
+    if block_n is None:
+        block_n, nb, num_warps = 0, 0, 0
+    cnt = len(mats)
+    P = ctypes.c_void_p * cnt
+    I64 = ctypes.c_int64 * cnt
+    wqs = P(*(w.data_ptr() for w, _, _ in mats))
+    wss = P(*(s.data_ptr() for _, s, _ in mats))
+    yps = P(*(y.data_ptr() for y in ys))
+    ns = I64(*(n for _, _, n in mats))
+    sws = I64(*(w.stride(0) for w, _, _ in mats))
+    fn = "komp_q4_0_gemv_multi" if fmt == "q4_0" else "komp_tq2_0_gemv_multi"
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    with torch.cuda.device(ref.device):
+        _abi.call(fn, cnt, wqs, wss, yps, ns, sws, ptr(xq), ptr(xd), ptr(x), m, k, block_n, nb, mode, num_warps,
+                  _stream(ref))  # fmt: skip
+
+
+def gemv_multi(fmt, mats, k, xq=None, xd=None, x=None, block_n=None, nb=4, mode=2, num_warps=4):
+    """-> [Y f32 [M][n] per matrix]; arguments as gemv_multi_into."""
+    ref = x if x is not None else xq
+    if ref is None:
+        raise _abi.KompArgumentError("gemv_multi: give either xq and xd (q8 input) or x (f32 input)")
+    ys = [torch.empty((ref.shape[0], n), dtype=torch.float32, device=ref.device) for _, _, n in mats]
+    gemv_multi_into(fmt, mats, ys, k, xq, xd, x, block_n, nb, mode, num_warps)
+    return ys
 
 
 def auto_config(fmt, m, n, k, fused=False, mode=2):

@@ -83,6 +83,22 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
                         float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
                         int mode, int num_warps, void* stream);
 
+/* Several weight matrices that share one activation input, in one launch (for example Q, K and V, or gate and up,
+ * stored as separate tensors): matrix i (count 1..4) has WQ[i] u8 [N[i]][SW[i]] and WS[i] i16 [N[i]][K/32] (q4_0)
+ * or [N[i]][K/256] (tq2_0) and writes Y[i] f32 [M][N[i]].  Give either XQ and XD (q8 planes, as komp_q4_0_gemv /
+ * komp_tq2_0_gemv) or X (f32 [M][K], quantized inside the launch as komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32), the
+ * other NULL.  With the same block_n / nb / num_warps each Y[i] equals that entry run on matrix i alone, bit for bit;
+ * block_n == 0 plans the launch for the matrices' rows together (komp_gemv_auto_config with N = their sum).  WQ, WS,
+ * Y, N and SW are host arrays of count entries; the pointers they hold are device pointers.
+ * No reference counterpart: the reference launches one matrix per kernel (src/komp/host.py:76-85); this serves the
+ * per-token launch count of decoders that store their projections apart. */
+int komp_q4_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                         const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                         int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                          const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                          int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+
 /* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0; fused != 0 for
  * komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32; mode as in the GEMV entries; M the activation columns.  block_n receives
  * the rows per workgroup, nb the 16-byte weight chunks each lane loads per row per K step, num_warps the waves per

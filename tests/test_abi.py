@@ -61,6 +61,34 @@ def test_empty_shapes_are_no_ops():
     assert lib.komp_dp4a_probe(None, None, None, None, 0, 2, None) == 0
 
 
+def _multi(count=2, n=(4, 4), K=64, sw=(32, 32), wq_ptr=16, x=False, xq=True, mode=2, arrays=True):
+    lib = _abi.lib()
+    P = ctypes.c_void_p * 4
+    I64 = ctypes.c_int64 * 4
+    p = ctypes.c_void_p(16)
+    wq = P(*([wq_ptr] * 4)) if arrays else None
+    ws = P(*([16] * 4))
+    y = P(*([16] * 4))
+    ns = I64(*(list(n) + [4] * (4 - len(n))))
+    sws = I64(*(list(sw) + [32] * (4 - len(sw))))
+    return lib.komp_q4_0_gemv_multi(count, wq, ws, y, ns, sws, p if xq else None, p if xq else None, p if x else None,
+                                    1, K, 0, 0, mode, 0, None)  # fmt: skip
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(count=0), "count"), (dict(count=5), "count"), (dict(x=True), "either"), (dict(xq=False), "either"),
+    (dict(arrays=False), "arrays"), (dict(n=(4, -1)), "N="), (dict(sw=(32, 24)), "SW"), (dict(K=48), "multiple"),
+    (dict(wq_ptr=8), "16-byte aligned"), (dict(mode=5), "mode"),
+])  # fmt: skip
+def test_gemv_multi_rejects_bad_arguments(kw, needle):
+    assert _multi(**kw) == _abi.KOMP_EINVAL
+    assert needle in _abi.last_error()
+
+
+def test_gemv_multi_empty_is_a_no_op():
+    assert _multi(n=(0, 0)) == 0
+
+
 def test_quantizers_reject_bad_arguments():
     lib = _abi.lib()
     p = ctypes.c_void_p(16)

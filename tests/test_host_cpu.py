@@ -52,3 +52,9 @@ def test_cpu_tensors_fail_loudly():
         host.gemv("q4_0", wq, ws, xq, xd, 4, 64)
     with pytest.raises(KeyError):
         host.gemv("q8_0", wq, ws, xq, xd, 4, 64)
+    with pytest.raises(_abi.KompArgumentError, match="HIP device"):
+        host.gemv_multi("q4_0", [(wq, ws, 4), (wq, ws, 4)], 64, xq=xq, xd=xd)
+    with pytest.raises(_abi.KompArgumentError, match="either"):
+        host.gemv_multi("q4_0", [(wq, ws, 4)], 64, xq=xq, xd=xd, x=x)
+    with pytest.raises(_abi.KompArgumentError, match="1..4"):
+        host.gemv_multi("q4_0", [(wq, ws, 4)] * 5, 64, xq=xq, xd=xd)
