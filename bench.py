@@ -15,7 +15,9 @@ Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: wei
 / their wall time (GB/s); roofline = the tq2_0_gemv
 dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
 (the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
-sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold, library-chosen knobs).
+sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold,
+library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
+gemv_multi launch against one launch per matrix.
 """
 
 from __future__ import annotations
@@ -311,6 +313,55 @@ def detail(torch, host, abi, args):
     return rows
 
 
+MULTI_CASES = (  # (name, fmt, [rows per matrix], K): projections stored as separate tensors that share one input
+    ("bitnet2b_ffn_gate_up", "tq2_0", (6912, 6912), 2560),
+    ("llama3_8b_q_k_v", "q4_0", (4096, 1024, 1024), 4096),
+)
+
+
+def multi_detail(torch, host, args):
+    """Several matrices sharing one f32 input (quantized inside each launch): one gemv_multi launch vs one gemv_f32
+    launch per matrix, both as graph replays over cold weight copies, m=1, dp4a, library plans."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 2)
+    for name, fmt, ns, k in MULTI_CASES:
+        make = q4_0_weights if fmt == "q4_0" else tq2_0_weights
+        per = sum(gemv_bytes(fmt, n, k, 0) for n in ns)
+        ncopy = max(2, math.ceil((COLD_BYTES // 2) / per))
+        base = [make(n, k, gen, torch) for n in ns]
+        copies = [[(wq.clone(), ws.clone(), n) for (wq, ws), n in zip(base, ns)] for _ in range(ncopy)]
+        x = torch.randn((1, k), generator=gen, device="cuda")
+        ys = [torch.empty((1, n), dtype=torch.float32, device="cuda") for n in ns]
+        ys1 = [torch.empty_like(y) for y in ys]
+
+        def multi(i, copies=copies, x=x, ys=ys, fmt=fmt, k=k):
+            host.gemv_multi_into(fmt, copies[i % len(copies)], ys, k, x=x)
+
+        def singles(i, copies=copies, x=x, ys1=ys1, fmt=fmt, k=k):
+            for (wq, ws, n), y in zip(copies[i % len(copies)], ys1):
+                host.gemv_f32_into(fmt, wq, ws, x, y, n, k)
+
+        per_graph = ncopy * math.ceil(64 / ncopy)
+        reps = 4 * per_graph
+        ms_m, _ = timed_steps(torch, multi, ncopy, reps, per_graph)
+        ms_s, _ = timed_steps(torch, singles, ncopy, reps, per_graph)
+        multi(0)
+        singles(0)
+        torch.cuda.synchronize()
+        rel = max(float((a - b).abs().max() / b.abs().max()) for a, b in zip(ys, ys1))
+        if rel > 1e-6:
+            raise RuntimeError(f"{name}: multi-matrix and single launches differ by {rel:.2e} (relative)")
+        b = sum(n * k * (18 if fmt == "q4_0" else 66) // (32 if fmt == "q4_0" else 256) for n in ns) + 4 * k + 4 * sum(ns)
+        us_m, us_s = ms_m * 1e3 / reps, ms_s * 1e3 / reps
+        rows.append({"case": name, "fmt": fmt, "rows": list(ns), "k": k, "bytes": b, "us_multi": round(us_m, 3),
+                     "us_singles": round(us_s, 3), "launches_singles": len(ns), "speedup": round(us_s / us_m, 3),
+                     "gbs_multi": round(b / us_m / 1e3, 1), "copies": ncopy})  # fmt: skip
+        del copies, base
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -364,6 +415,7 @@ def main():
         out["cpu_baseline"] = cpu_baseline(args, step_bytes, args.cpu_seconds)
     if not args.no_detail:
         out["detail"] = detail(torch, host, _abi, args)
+        out["multi_matrix"] = multi_detail(torch, host, args)
     print(json.dumps(out), flush=True)
     return 0
 
