@@ -45,6 +45,9 @@ SIGNATURES = {
     "komp_q4_0_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_tq2_0_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_gemv_auto_config": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+    "komp_q4_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "komp_tq2_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "komp_gemm_plan": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
     "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
@@ -105,6 +108,13 @@ def auto_plan(fmt_id, m, n, k, fused=False, mode=2):
 
 def auto_config(fmt_id, m, n, k, fused=False, mode=2):
     return auto_plan(fmt_id, m, n, k, fused, mode)[:3]
+
+
+def gemm_plan(fmt_id, m, n, k, sw):
+    """(rows per workgroup, columns per workgroup, waves) of the matrix-core GEMM, or None past its limits."""
+    v = [ctypes.c_int(0) for _ in range(3)]
+    st = lib().komp_gemm_plan(fmt_id, m, n, k, sw, *(ctypes.byref(x) for x in v))
+    return tuple(x.value for x in v) if st == 0 else None
 
 
 def timing_begin(max_dispatches=1 << 16):

@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkomp_hip.so")
-SOURCES = ("abi.hip", "quant.hip", "gemv.hip", "gemv_fused.hip")
+SOURCES = ("abi.hip", "quant.hip", "gemv.hip", "gemv_fused.hip", "gemm.hip")
 ARCH = "gfx950"
 
 
@@ -44,6 +44,10 @@ def compile_flags():
         # the first 16 kernel-argument dwords arrive in SGPRs at wave launch (gfx950 kernarg preloading)
         "-mllvm",
         "-amdgpu-kernarg-preload-count=16",
+        # MFMA results in ordinary VGPRs (the matrix-core GEMM converts every result right away; without this the
+        # compiler parks them in AGPRs and copies each one back)
+        "-mllvm",
+        "-amdgpu-mfma-vgpr-form",
     ]
 
 

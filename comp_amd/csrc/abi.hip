@@ -160,6 +160,30 @@ GemvPlan knob_plan(int block_n, int nb, int num_warps) {
   return plan;
 }
 
+// ---- matrix-core GEMM ----------------------------------------------------------------------------------------------
+// From gemm_min_m(fmt) activation columns on, block_n == 0 in dp4a mode (unfused) runs the matrix-core GEMM, which
+// reads the weights once per 64 columns, instead of the GEMV in column chunks of 3 (measured crossover: Q4_0 between
+// 4 and 8 columns at Llama-3-8B shapes, TQ2_0 below 4 at BitNet-2B shapes).
+int64_t gemm_min_m(int fmt) { return fmt == FMT_Q4_0 ? 8 : 4; }
+constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (grid.y = columns / 64 at most 16384)
+
+// The GEMM's plan for m columns (one launch) and n rows: 8 waves; columns in groups of at most 64 (4 tiles of 16),
+// split evenly; two 16-row tiles per workgroup (with at most 2 column tiles) when that still gives every CU a
+// workgroup.  False when the shape is past the kernel's 32-bit buffer offsets (64 * K and 32 * SW below 2^31) or its
+// scale slab does not fit in LDS.
+bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p) {
+  if (64 * k > INT32_MAX || 32 * sw > INT32_MAX) return false;
+  const int64_t c16 = (m + 15) / 16;
+  const int64_t groups = (c16 + 3) / 4;
+  p->waves = 8;
+  p->cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
+  p->wn = p->cn <= 2 && ((n + 31) / 32) * groups >= device_cus() ? 2 : 1;
+  if (p->wn == 2 && gemm_lds_bytes(fmt, *p, static_cast<int>(k)) > kLdsMax) p->wn = 1;
+  return gemm_lds_bytes(fmt, *p, static_cast<int>(k)) <= kLdsMax;
+}
+
+enum Route { kRouteAuto = 0, kRouteGemm = 1 };
+
 struct GemvMat {
   const uint8_t* wq;
   const int16_t* ws;
@@ -181,7 +205,7 @@ struct GemvArgs {
 };
 
 int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t M, int64_t K, int block_n, int nb,
-               int mode, int num_warps, void* stream) {
+               int mode, int num_warps, void* stream, int route = kRouteAuto) {
   const int blk = fmt == FMT_Q4_0 ? 32 : 256;
   const int64_t row_bytes = fmt == FMT_Q4_0 ? K / 2 : K / 4;
   if (a.count < 1 || a.count > kMaxSegs || a.mats == nullptr)
@@ -230,6 +254,39 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
       return fail(KOMP_EINVAL, "%s: WS, Y and S must be aligned to their element size", name);
     mats[count++] = w;
   }
+  const int64_t nblk = K / blk;
+  if (route == kRouteGemm || (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && M >= gemm_min_m(fmt))) {
+    GemmPlan gp;
+    bool fits = true;
+    for (int i = 0; i < count; ++i)
+      fits = fits && gemm_plan(fmt, M < kGemmMaxCols ? M : kGemmMaxCols, mats[i].n, K, mats[i].sw, &gp);
+    if (fits) {
+      for (int i = 0; i < count; ++i) {
+        for (int64_t m0 = 0; m0 < M; m0 += kGemmMaxCols) {
+          const int64_t mc = M - m0 < kGemmMaxCols ? M - m0 : kGemmMaxCols;
+          gemm_plan(fmt, mc, mats[i].n, K, mats[i].sw, &gp);
+          GemmCall c = {};
+          c.fmt = fmt;
+          c.wq = mats[i].wq;
+          c.ws = mats[i].ws;
+          c.xq = a.xq != nullptr ? a.xq + m0 * K : nullptr;
+          c.xd = a.xd != nullptr ? a.xd + m0 * nblk : nullptr;
+          c.y = mats[i].y + m0 * mats[i].n;
+          c.s = mats[i].s != nullptr ? mats[i].s + m0 * mats[i].n * nblk : nullptr;
+          c.m = static_cast<int>(mc);
+          c.n = static_cast<int>(mats[i].n);
+          c.k = static_cast<int>(K);
+          c.sw = mats[i].sw;
+          const int st = hip_status(launch_gemm(c, gp, static_cast<hipStream_t>(stream)), name);
+          if (st != KOMP_OK) return st;
+        }
+      }
+      return KOMP_OK;
+    }
+    if (route == kRouteGemm)
+      return fail(KOMP_EINVAL, "%s: K=%lld / SW past the GEMM's limits (64*K and 32*SW below 2^31, scale slab in LDS)",
+                  name, (long long)K);
+  }
   int mc = static_cast<int>(M < 3 ? M : 3);
   while (mc > 1 && gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax) --mc;
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
@@ -238,7 +295,6 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
   const GemvPlan plan =
       block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K) : knob_plan(block_n, nb, num_warps);
 
-  const int64_t nblk = K / blk;
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
     GemvCall c = {};
     c.fmt = fmt;
@@ -371,6 +427,33 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
   const GemvMat w{WQ, WS, Y, S, N, SW};
   const GemvArgs a{&w, 1, nullptr, nullptr, X, XQ, XD, XB};
   return gemv_entry(FMT_TQ2_0, true, "komp_tq2_0_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, void* stream) {
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_Q4_0, false, "komp_q4_0_gemm", a, M, K, 0, 0, KOMP_MODE_DP4A, 0, stream, kRouteGemm);
+}
+
+int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                    int64_t M, int64_t N, int64_t K, int64_t SW, void* stream) {
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_TQ2_0, false, "komp_tq2_0_gemm", a, M, K, 0, 0, KOMP_MODE_DP4A, 0, stream, kRouteGemm);
+}
+
+int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
+                   int* waves) {
+  if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemm_plan: fmt=%d", fmt);
+  if (M < 1 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemm_plan: bad argument");
+  GemmPlan p;
+  if (!gemm_plan(fmt, M < kGemmMaxCols ? M : kGemmMaxCols, N, K, SW, &p))
+    return fail(KOMP_EINVAL, "komp_gemm_plan: K=%lld / SW=%lld past the GEMM's limits", (long long)K, (long long)SW);
+  if (rows_per_wg != nullptr) *rows_per_wg = 16 * p.wn;
+  if (cols_per_wg != nullptr) *cols_per_wg = 16 * p.cn;
+  if (waves != nullptr) *waves = p.waves;
+  return KOMP_OK;
 }
 
 int komp_q4_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,

@@ -1,0 +1,343 @@
+// Batched-column GEMMs on the gfx950 matrix cores: Q4_0 x q8_0 and TQ2_0 x q8_K for any number M of activation
+// columns, with the decode GEMVs' result definition (src/komp/kernels.py:48-94 and :97-142):
+//   Y[m][n] = sum_b d_w(n, b) * d_x(m, b) * s(m, n, b),  s = the exact int32 dot of weight block b of row n with
+//   activation block b of column m,
+// and the same optional S [M][N][K/block] of exact block dots.  The GEMVs stream the weights once per 1..3 columns;
+// this kernel streams them once per 64 columns, so a batch of decode tokens reads each weight byte once.
+//
+// Tiles.  A workgroup (W waves) owns 16*WN weight rows x 16*CN activation columns and all of K.  Its waves split K:
+// a K step is 64 contiguous bytes of each weight row (4 Q4_0 blocks or 1 TQ2_0 block) and wave w takes steps
+// w, w + W, w + 2W, ...; at the end the waves add their f32 partials in wave order.  Lane (r, g) (r = lane % 16,
+// g = lane / 16) loads bytes 16g..16g+15 of a step for row r, so one load instruction reads 64 bytes of each of 16
+// rows.  Each wave keeps D steps of loads in flight (a register ring).  Loads go through buffer descriptors whose
+// range ends at the tile's last valid row / column: a load past it, or one the kernel points past it on purpose
+// (blocks past K, steps past the wave's last), returns zeros without touching memory.
+//
+// Integer dots.  Operand lane l holds k slots of group l / 16 for row / column l % 16, the same slots in A and B
+// (v_mfma_i32_16x16x32_i8: 8 bytes a lane, v_mfma_i32_16x16x64_i8: 16 bytes), so a block dot needs all four lane
+// groups to hold pieces of the same block:
+//   Q4_0   after the load, group g holds block 4s+g whole.  A 4x4 dword transpose across the groups
+//          (v_permlane32_swap, v_permlane16_swap) leaves dword g of each of the four blocks in group g; dword g holds
+//          values 4g..4g+3 (low nibbles) and 16+4g..16+4g+3 (high nibbles), so A = {w & 0x0F0F0F0F, (w >> 4) &
+//          0x0F0F0F0F}.  The activations are loaded the same way (32 bytes of block 4s+g of column r in group g) and
+//          transposed into B = {x[4g..4g+3], x[16+4g..16+4g+3]}.
+//   TQ2_0  group g holds bytes 16g..16g+15 of the block; crumb j of byte 16g+e is value (g/2)*128 + 32j + 16(g%2) + e
+//          (kernels.py:102), so B for crumb j is 16 contiguous activation bytes and nothing is transposed.
+// Nibbles and crumbs go in unsigned (0..15, 0..2).  Their offset (-8, resp. -1, times the block's activation sum)
+// comes from one more MFMA of a constant A (every byte -8, resp. -1) with the same B, which starts the accumulator,
+// so every C element is the exact block dot s.  C element r of lane (c, g) is row 4g + r, column c.
+//
+// Scales.  The workgroup's rows of WS (16*WN rows, contiguous in WS) are copied to LDS once and read back per step in
+// the C layout; d_x comes with each step's loads.  Per block: Q4_0 acc += (f32(s) * d_w) * d_x, TQ2_0
+// acc += (d_x * d_w) * f32(s), each with one fused multiply-add (the GEMVs' operand order, kernels.py:93, :141).
+#include <hip/hip_ext.h>
+
+#include "komp_device.h"
+#include "komp_internal.h"
+
+namespace komp {
+namespace gemm_impl {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRsrcWord3 = 0x00020000;     // buffer descriptor word 3 on gfx9: 32-bit data, no swizzle
+constexpr unsigned kOob = 0x7FFFFFF0u;     // an offset (or offset part) past every descriptor's range: zeros
+constexpr unsigned NIB = 0x0F0F0F0Fu;
+constexpr unsigned CRUMB = 0x03030303u;
+
+// A raw buffer descriptor over [base, base + bytes), the range capped at 0x7FFFFFF0 (every offset the kernel uses
+// below the cap is also below 2^31, which the host checks).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  const int n = static_cast<int>(bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, kRsrcWord3);
+}
+
+// 4x4 dword transpose across the four 16-lane rows of a wave: on entry row g of v[q] holds element (q, g), on exit
+// row g of t[j] holds element (g, j).  permlane32_swap(x, y) exchanges x's rows 2-3 with y's rows 0-1;
+// permlane16_swap(x, y) exchanges x's rows 1 and 3 with y's rows 0 and 2.
+__device__ __forceinline__ void transpose4(const u32x4& v, unsigned (&t)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  t[0] = c[0];
+  t[1] = c[1];
+  t[2] = d[0];
+  t[3] = d[1];
+}
+
+// Row stride (in floats) of the f32 scale slab: nblk rounded up to a multiple of 4.
+__host__ __device__ constexpr int slab_stride(int nblk) { return (nblk + 3) & ~3; }
+
+__device__ __forceinline__ long pack2(unsigned lo, unsigned hi) {
+  return static_cast<long>(static_cast<unsigned long>(lo) | (static_cast<unsigned long>(hi) << 32));
+}
+
+// FMT: FMT_Q4_0 / FMT_TQ2_0; W waves; WN 16-row and CN 16-column tiles per workgroup; D steps in flight per wave.
+template <int FMT, int W, int WN, int CN, int D>
+__global__ void __launch_bounds__(64 * W)
+gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const uint8_t* __restrict__ WQ,
+            const int16_t* __restrict__ WS, const int8_t* __restrict__ XQ, const float* __restrict__ XD,
+            float* __restrict__ Y, int32_t* __restrict__ S) {
+  // ss: row stride of the f32 scale slab in LDS, nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four
+  // scales of a row with one 16-byte LDS load).
+  constexpr bool Q4 = FMT == FMT_Q4_0;
+  constexpr int XV = Q4 ? 2 : 4;   // 16-byte activation loads per column tile per step
+  constexpr int DXN = Q4 ? 4 : 1;  // activation scales per column per step
+  constexpr int RPW = 16 * WN / W;  // slab rows each wave stages
+  static_assert(RPW >= 1 && RPW * W == 16 * WN, "the waves split the workgroup's rows evenly");
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int n0 = blockIdx.x * (16 * WN);
+  const int m0 = blockIdx.y * (16 * CN);
+  const int rows = min(16 * WN, N - n0);  // valid rows and columns of the tile
+  const int cols = min(16 * CN, M - m0);
+  const auto wq = rsrc(WQ + n0 * SW, rows * SW);
+  const auto xq = rsrc(XQ + static_cast<int64_t>(m0) * K, static_cast<int64_t>(cols) * K);
+  const auto xd = rsrc(XD + static_cast<int64_t>(m0) * nblk, static_cast<int64_t>(cols) * nblk * 4);
+
+  // Per-lane offsets are fixed; a step adds a wave-uniform offset (SGPR), and a step past the wave's last adds kOob,
+  // which makes all of its loads return zeros.  In a partial last Q4_0 step the lanes of blocks past K read other
+  // bytes of the tensor (never past the descriptors' ranges); those blocks are skipped when the step is computed.
+  unsigned va[WN];
+#pragma unroll
+  for (int t = 0; t < WN; ++t) va[t] = static_cast<unsigned>((16 * t + r16) * SW + 16 * g);
+  unsigned vx[CN], vd[CN];
+#pragma unroll
+  for (int u = 0; u < CN; ++u) {
+    const int c = 16 * u + r16;
+    vx[u] = static_cast<unsigned>(Q4 ? c * K + 32 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
+    vd[u] = static_cast<unsigned>(c * nblk * 4);
+  }
+
+  struct Step {
+    u32x4 a[WN];
+    u32x4 x[CN][XV];
+    float dx[CN][DXN];
+  };
+  auto load = [&](Step& st, int s) {
+    const bool sv = s < nsteps;  // wave-uniform
+    const unsigned sa = sv ? 64u * s : kOob;
+    const unsigned sx = sv ? (Q4 ? 128u : 256u) * s : kOob;
+    const unsigned sd = sv ? (Q4 ? 16u : 4u) * s : kOob;
+#pragma unroll
+    for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t], sa, 2);  // nt: read once
+#pragma unroll
+    for (int u = 0; u < CN; ++u) {
+#pragma unroll
+      for (int v = 0; v < XV; ++v)
+        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (Q4 ? 16 * v : 32 * v), sx, 0);
+#pragma unroll
+      for (int j = 0; j < DXN; ++j)
+        st.dx[u][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u] + 4 * j, sd, 0));
+    }
+  };
+
+  const int my = nsteps > wave ? (nsteps - wave + W - 1) / W : 0;  // this wave's steps (wave-uniform)
+  Step ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(ring[d], wave + W * d);
+
+  // ---- the scale slab: f32 d_w of rows n0 .. n0 + 16*WN, row stride ss, zero past row N and past block nblk ----
+  float* slab = reinterpret_cast<float*>(lds);
+  {
+    const auto ws = rsrc(WS + static_cast<int64_t>(n0) * nblk, static_cast<int64_t>(rows) * nblk * 2);
+    constexpr int kBatch = 8;  // 2-byte loads per row per batch, all issued before the first conversion
+    for (int c0 = 0; c0 < ss; c0 += 64 * kBatch) {
+      unsigned short h[RPW][kBatch];
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int row = wave * RPW + i;
+          const int col = c0 + 64 * b + lane;
+          h[i][b] = __builtin_amdgcn_raw_buffer_load_b16(
+              ws, col < nblk ? static_cast<unsigned>((row * nblk + col) * 2) : kOob, 0, 0);
+        }
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int col = c0 + 64 * b + lane;
+          if (col < ss) slab[(wave * RPW + i) * ss + col] = f16_bits_to_f32(static_cast<int16_t>(h[i][b]));
+        }
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[WN][CN];
+#pragma unroll
+  for (int t = 0; t < WN; ++t)
+#pragma unroll
+    for (int u = 0; u < CN; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto store_s = [&](const i32x4& cc, int t, int u, int b) {
+    const int col = m0 + 16 * u + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = n0 + 16 * t + 4 * g + r;
+      if (col < M && row < N) S[(static_cast<int64_t>(col) * N + row) * nblk + b] = cc[r];
+    }
+  };
+
+  auto compute = [&](const Step& st, int s) {
+    if constexpr (Q4) {
+      unsigned ta[WN][4], tu[CN][4], tv[CN][4];
+#pragma unroll
+      for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
+#pragma unroll
+      for (int u = 0; u < CN; ++u) {
+        transpose4(st.x[u][0], tu[u]);
+        transpose4(st.x[u][1], tv[u]);
+      }
+      f32x4 dw[WN][4];  // [t][r] = d_w of row 16t + 4g + r, blocks 4s .. 4s+3
+#pragma unroll
+      for (int t = 0; t < WN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dw[t][r] = *reinterpret_cast<const f32x4*>(slab + (16 * t + 4 * g + r) * ss + 4 * s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = 4 * s + j;
+        if (b >= nblk) break;  // wave-uniform: the step's last blocks past K
+        long bj[CN];
+        i32x4 corr[CN];
+#pragma unroll
+        for (int u = 0; u < CN; ++u) {
+          bj[u] = pack2(tu[u][j], tv[u][j]);
+          corr[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(0xF8F8F8F8F8F8F8F8ull), bj[u],
+                                                          i32x4{0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < WN; ++t) {
+          const long aj = pack2(ta[t][j] & NIB, (ta[t][j] >> 4) & NIB);
+#pragma unroll
+          for (int u = 0; u < CN; ++u) {
+            const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(aj, bj[u], corr[u], 0, 0, 0);
+            if (S != nullptr) store_s(cc, t, u, b);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[t][u][r] = __builtin_fmaf(static_cast<float>(cc[r]) * dw[t][r][j], st.dx[u][j], acc[t][u][r]);
+          }
+        }
+      }
+    } else {
+      i32x4 corr[CN];
+#pragma unroll
+      for (int u = 0; u < CN; ++u) {
+        corr[u] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          corr[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(i32x4{-1, -1, -1, -1},
+                                                          reinterpret_cast<const i32x4&>(st.x[u][v]), corr[u], 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < WN; ++t) {
+        float dw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dw[r] = slab[(16 * t + 4 * g + r) * ss + s];
+        i32x4 aj[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const u32x4 cr = (st.a[t] >> (2u * v)) & CRUMB;
+          aj[v] = reinterpret_cast<const i32x4&>(cr);
+        }
+#pragma unroll
+        for (int u = 0; u < CN; ++u) {
+          i32x4 cc = corr[u];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aj[v], reinterpret_cast<const i32x4&>(st.x[u][v]), cc, 0, 0,
+                                                        0);
+          if (S != nullptr) store_s(cc, t, u, s);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[t][u][r] = __builtin_fmaf(st.dx[u][0] * dw[r], static_cast<float>(cc[r]), acc[t][u][r]);
+        }
+      }
+    }
+  };
+
+  for (int i0 = 0; i0 < my; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i = i0 + d;
+      if (i < my) {
+        compute(ring[d], wave + W * i);
+        load(ring[d], i + D < my ? wave + W * (i + D) : nsteps);  // past the wave's last step: zeros, no traffic
+      }
+    }
+  }
+
+  // ---- partials of the W waves, added in wave order ----
+  __syncthreads();  // every wave is done with the slab
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int t = 0; t < WN; ++t)
+#pragma unroll
+    for (int u = 0; u < CN; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((((wave * WN + t) * CN + u) * 4 + r) << 6) + lane] = acc[t][u][r];
+  __syncthreads();
+  for (int idx = wave; idx < WN * CN * 4; idx += W) {
+    const int r = idx & 3;
+    const int u = (idx >> 2) % CN;
+    const int t = (idx >> 2) / CN;
+    float sum = red[(((t * CN + u) * 4 + r) << 6) + lane];
+    for (int w = 1; w < W; ++w) sum += red[((((w * WN + t) * CN + u) * 4 + r) << 6) + lane];
+    const int row = n0 + 16 * t + 4 * g + r;
+    const int col = m0 + 16 * u + r16;
+    if (row < N && col < M) Y[static_cast<int64_t>(col) * N + row] = sum;
+  }
+}
+
+}  // namespace gemm_impl
+
+namespace {
+
+template <int FMT, int W, int WN, int CN, int D>
+hipError_t launch_t(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+  const int blk = FMT == FMT_Q4_0 ? 32 : 256;
+  const int nblk = c.k / blk;
+  const int nsteps = FMT == FMT_Q4_0 ? (nblk + 3) / 4 : nblk;
+  const dim3 grid((c.n + 16 * WN - 1) / (16 * WN), (c.m + 16 * CN - 1) / (16 * CN));
+  const dim3 block(64 * W);
+  const size_t lds = gemm_lds_bytes(FMT, p, c.k);
+  auto kern = gemm_impl::gemm_kernel<FMT, W, WN, CN, D>;
+  const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
+  hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, nsteps,
+                        gemm_impl::slab_stride(nblk), c.sw, c.wq, c.ws, c.xq, c.xd, c.y, c.s);
+  return hipGetLastError();
+}
+
+// Instantiated plans: 8 waves; one 16-row tile with 1..4 column tiles, or two with 1..2 (two row tiles with more
+// columns would not fit 256 VGPRs).  Four steps in flight with one column tile, two with more.
+template <int FMT>
+hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+  if (p.wn == 2) return p.cn == 1 ? launch_t<FMT, 8, 2, 1, 4>(c, p, stream) : launch_t<FMT, 8, 2, 2, 2>(c, p, stream);
+  switch (p.cn) {
+    case 1: return launch_t<FMT, 8, 1, 1, 4>(c, p, stream);
+    case 2: return launch_t<FMT, 8, 1, 2, 2>(c, p, stream);
+    case 3: return launch_t<FMT, 8, 1, 3, 2>(c, p, stream);
+    default: return launch_t<FMT, 8, 1, 4, 2>(c, p, stream);
+  }
+}
+
+}  // namespace
+
+size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k) {
+  const int nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
+  const size_t slab = static_cast<size_t>(16) * p.wn * gemm_impl::slab_stride(nblk) * 4;
+  const size_t red = static_cast<size_t>(p.waves) * p.wn * p.cn * 4 * 64 * 4;
+  return slab > red ? slab : red;
+}
+
+hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+  if (p.waves != 8 || p.wn < 1 || p.wn > 2 || p.cn < 1 || p.cn > 4 || (p.wn == 2 && p.cn > 2))
+    return hipErrorInvalidConfiguration;
+  return c.fmt == FMT_Q4_0 ? launch_fmt<FMT_Q4_0>(c, p, stream) : launch_fmt<FMT_TQ2_0>(c, p, stream);
+}
+
+}  // namespace komp

@@ -54,6 +54,28 @@ struct GemvCall {
   GemvSegs segs;  // first_wg is filled in at launch, from the plan
 };
 
+// Matrix-core GEMM (any number of activation columns): waves per workgroup, 16-row tiles (wn) and 16-column tiles
+// (cn) per workgroup.
+struct GemmPlan {
+  int waves;
+  int wn;
+  int cn;
+};
+
+struct GemmCall {
+  int fmt;
+  const uint8_t* wq;
+  const int16_t* ws;
+  const int8_t* xq;
+  const float* xd;
+  float* y;
+  int32_t* s;
+  int m;
+  int n;
+  int k;
+  int64_t sw;
+};
+
 // Dispatch hook: every launch goes through it so the tuning harness can time dispatches with hipExtLaunchKernel events.
 struct Timing {
   bool on;
@@ -65,6 +87,8 @@ Timing timing_slot(int kind);   // defined in abi.hip
 size_t gemv_lds_bytes(int fmt, int m, int k);
 hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
+hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
 hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,

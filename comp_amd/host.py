@@ -31,6 +31,7 @@ FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale off
 }
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
 FMT_ID = {"q4_0": 0, "tq2_0": 1}
+GEMM_MIN_M = {"q4_0": 8, "tq2_0": 4}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
 
 
 def split(fmt, W, n, k):
@@ -185,6 +186,54 @@ def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store
     s = torch.zeros((m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
     _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
     return y, s
+
+
+def _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k):
+    fn = "komp_q4_0_gemm" if fmt == "q4_0" else "komp_tq2_0_gemm"
+    with torch.cuda.device(xq.device):
+        _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
+                  None if s is None else s.data_ptr(), xq.shape[0], n, k, wq.stride(0), _stream(xq))  # fmt: skip
+
+
+def gemm(fmt, wq, ws, xq, xd, n, k, store_s=False):
+    """-> (Y f32 [M][N], S int32 [M][N][blocks] or None) on the matrix cores, for any number M of columns.
+
+    The result definition of gemv (exact int32 block dots, then d_w * d_x scaling, src/komp/kernels.py:48-142); the
+    weights are read once per 64 columns.  gemv(..., block_n=None, mode=2) runs this kernel from GEMM_MIN_M columns
+    on."""
+    m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
+    y = torch.empty((m, n), dtype=torch.float32, device=xq.device)
+    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
+    _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k)
+    return y, s
+
+
+def gemm_into(fmt, wq, ws, xq, xd, y, n, k, s=None):
+    """Allocation-free gemm into preallocated y f32 [M][N] (and s int32 [M][N][blocks] when given)."""
+    m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
+    _need(y, "y", torch.float32, 2)
+    if tuple(y.shape) != (m, n) or not y.is_contiguous():
+        raise _abi.KompArgumentError(f"gemm_into: y must be a contiguous [{m}][{n}] tensor")
+    if s is not None:
+        _need(s, "s", torch.int32, 3)
+        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"gemm_into: s must be a contiguous [{m}][{n}][{nblk}] tensor")
+    _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k)
+
+
+def gemm_plan(fmt, m, n, k, sw=None):
+    """{rows, cols, waves} per workgroup of the matrix-core GEMM for this shape (sw: the weight row stride in bytes,
+    default the packed row), or None when the shape is past the kernel's limits."""
+    if sw is None:
+        sw = k // FORMATS[fmt]["block"] * FORMATS[fmt]["qbytes"]
+    p = _abi.gemm_plan(FMT_ID[fmt], m, n, k, sw)
+    return None if p is None else dict(zip(("rows", "cols", "waves"), p))
+
+
+def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
+    """True when gemv(..., block_n=None) runs the matrix-core GEMM for this shape (unfused, dp4a, from 8 columns for
+    q4_0 and from 4 for tq2_0)."""
+    return not fused and mode == 2 and m >= GEMM_MIN_M[fmt] and gemm_plan(fmt, m, n, k, sw) is not None
 
 
 def quantize_into(fmt, x, xq, xd, xb=None, bb=4):
@@ -375,7 +424,10 @@ def auto_plan(fmt, m, n, k, fused=False, mode=2):
 
 
 def knob_equivalent(fmt, m, n, k, fused=False, mode=2):
-    """The explicit knobs that run exactly the auto plan, or None when the plan is beyond the knob mapping."""
+    """The explicit knobs that run exactly the auto plan, or None when the plan is beyond the knob mapping (or the
+    shape runs on the matrix-core GEMM)."""
+    if uses_gemm(fmt, m, n, k, fused, mode):
+        return None
     p = auto_plan(fmt, m, n, k, fused, mode)
     bn, w = p["block_n"], p["waves"]
     if bn not in (8, 16, 32, 64, 128) or w not in (1, 2, 4, 8) or bn % w:

@@ -111,6 +111,26 @@ int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* co
 int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
                           int* num_warps, int* lanes_per_row, int* passes);
 
+/* Y [M][N] (and S when not NULL) as komp_q4_0_gemv / komp_tq2_0_gemv compute them, for any M, on the matrix cores
+ * (v_mfma_i32_16x16x32_i8 / v_mfma_i32_16x16x64_i8): each workgroup reads its weight rows once for up to 64
+ * activation columns, where the GEMVs read them once per 3.  S is bit-identical to the GEMVs'; Y agrees to f32
+ * rounding (the f32 sums run in another order).  Arguments and alignment as komp_q4_0_gemv / komp_tq2_0_gemv without
+ * the knobs; also 64*K and 32*SW must be below 2^31 and the 16 or 32 rows of WS a workgroup stages must fit in LDS
+ * (komp_gemm_plan says whether a shape qualifies).  komp_q4_0_gemv with block_n == 0 and KOMP_MODE_DP4A runs this
+ * kernel for M >= 8 when the shape qualifies, komp_tq2_0_gemv for M >= 4.
+ * No reference counterpart: the reference launches its GEMV once per column (grid (cdiv(N, BLOCK_N), M),
+ * src/komp/kernels.py:50); this serves batched decode, where M columns share every weight byte. */
+int komp_q4_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
+int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                    int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
+
+/* The matrix-core GEMM's plan for a shape on the current device (fmt 0 = q4_0, 1 = tq2_0): weight rows and activation
+ * columns per workgroup, waves per workgroup.  Returns KOMP_EINVAL when the shape is past the kernel's limits.
+ * No reference counterpart. */
+int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
+                   int* waves);
+
 /* OUT[i] = dp4a(A[i], B[i], C[i]) for i < n; mode KOMP_MODE_DP4A (hardware) or KOMP_MODE_DP4A_EMU.
  * Replaces: kernels.dp4a_probe (src/komp/kernels.py:145-149). */
 int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,

@@ -1,0 +1,152 @@
+"""Matrix-core GEMM (komp_q4_0_gemm / komp_tq2_0_gemm) vs the oracle: int32 block dots S exact, Y within 1e-5
+(norm-wise) of the f64 reference_dot, on the same seeded problems.  Shapes cover the kernel's tails: rows not a
+multiple of 16, column counts around the 16-column tiles and the 64-column workgroups, Q4_0 block counts that are not
+a multiple of the 4-block K step, scale planes that take the 2-byte staging path, padded weight rows, and the
+two-row-tile workgroups of tall matrices.  Everything goes through the C ABI."""
+
+import numpy as np
+import pytest
+import torch
+
+from comp_amd import host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+# (n, k, m)
+SHAPES = {
+    "q4_0": [(16, 128, 1), (16, 128, 2), (64, 512, 4), (37, 416, 5), (5, 96, 17), (33, 1024, 31), (100, 4096, 33),
+             (48, 2048, 64), (40, 640, 65), (300, 768, 130)],
+    "tq2_0": [(16, 256, 1), (16, 256, 3), (64, 1024, 4), (37, 768, 5), (5, 1280, 17), (33, 2560, 31),
+              (100, 2560, 33), (40, 6912, 64), (48, 256, 65), (300, 512, 130)],
+}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def check(fmt, n, k, m, seed, extreme=False, ws_offset=0, pad=0):
+    W, x = O.problem(fmt, n, k, m, seed, extreme)
+    wq, ws = host.split(fmt, W, n, k)
+    rq, rd, _ = O.quantize(fmt, x)
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    wq_d = dev(np.pad(wq, ((0, 0), (0, pad))))[:, : wq.shape[1] + pad]
+    if ws_offset:  # a scale plane that starts 2 bytes into its allocation (not 16-byte aligned)
+        base = torch.zeros(ws.size + ws_offset, dtype=torch.int16, device="cuda")
+        base[ws_offset:] = dev(ws.reshape(-1))
+        ws_d = base[ws_offset:].view(n, -1)
+    else:
+        ws_d = dev(ws)
+    print(f"gemm {fmt} n={n} k={k} m={m} seed={seed} extreme={extreme} ws_offset={ws_offset} pad={pad}", flush=True)
+    y, s = host.gemm(fmt, wq_d, ws_d, dev(rq), dev(rd), n, k, store_s=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
+    assert O.relerr(y.cpu().numpy(), r) <= TOL
+    return y
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("shape", range(10))
+@pytest.mark.parametrize("extreme", [False, True])
+def test_gemm_matches_oracle(fmt, shape, extreme):
+    n, k, m = SHAPES[fmt][shape]
+    check(fmt, n, k, m, 300 + shape, extreme)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemm_unaligned_scales_and_padded_rows(fmt):
+    k = 416 if fmt == "q4_0" else 768
+    check(fmt, 45, k, 20, 11, ws_offset=1, pad=48)
+    check(fmt, 64, 2 * k if fmt == "q4_0" else 1024, 8, 12, ws_offset=3)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemm_two_row_tiles(fmt):
+    # tall enough that each workgroup takes 32 rows (one per CU or more)
+    n = 32 * 300
+    k = 256
+    assert host.gemm_plan(fmt, 4, n, k)["rows"] == 32 and host.gemm_plan(fmt, 70, n, k)["rows"] == 16
+    check(fmt, n + 7, k, 4, 21)
+    check(fmt, n, k, 20, 22)
+    check(fmt, n, k, 70, 23)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemv_auto_routes_batches_to_gemm(fmt):
+    n, k, m = (96, 1024, 12) if fmt == "q4_0" else (96, 1536, 12)
+    W, x = O.problem(fmt, n, k, m, 31)
+    wq, ws = host.split(fmt, W, n, k)
+    xq, xd, *_ = host.quantize(fmt, dev(x))
+    lo = host.GEMM_MIN_M[fmt]
+    assert host.uses_gemm(fmt, m, n, k) and host.uses_gemm(fmt, lo, n, k) and not host.uses_gemm(fmt, lo - 1, n, k)
+    assert not host.uses_gemm(fmt, m, n, k, mode=1) and not host.uses_gemm(fmt, m, n, k, fused=True)
+    assert host.knob_equivalent(fmt, m, n, k) is None
+    y_auto, s_auto = host.gemv(fmt, dev(wq), dev(ws), xq, xd, n, k, block_n=None, mode=2, store_s=True)
+    y_gemm, s_gemm = host.gemm(fmt, dev(wq), dev(ws), xq, xd, n, k, store_s=True)
+    y_gemv, s_gemv = host.gemv(fmt, dev(wq), dev(ws), xq, xd, n, k, 32, 2, 2, 4, store_s=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_auto, y_gemm) and torch.equal(s_auto, s_gemm)
+    assert torch.equal(s_gemm, s_gemv)
+    rq, rd, _ = O.quantize(fmt, x)
+    r, _ = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    assert O.relerr(y_gemm.cpu().numpy(), r) <= TOL and O.relerr(y_gemv.cpu().numpy(), r) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemm_multi_matrix_batches(fmt):
+    k = 512
+    ns = (40, 24, 64)
+    m = 9
+    rng = np.random.default_rng(41)
+    mats, refs = [], []
+    x = O.activations(rng, k, m, block=32 if fmt == "q4_0" else 256)
+    rq, rd, _ = O.quantize(fmt, x)
+    for n in ns:
+        W = O.weights(fmt, rng, n, k)
+        wq, ws = host.split(fmt, W, n, k)
+        mats.append((dev(wq), dev(ws), n))
+        refs.append(O.gemv(fmt, wq, ws, rq, rd, n, k)[0])
+    ys = host.gemv_multi(fmt, mats, k, xq=dev(rq), xd=dev(rd))
+    torch.cuda.synchronize()
+    for y, r in zip(ys, refs):
+        assert O.relerr(y.cpu().numpy(), r) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemm_empty_k_writes_zeros(fmt):
+    n, m = 20, 5
+    wq = torch.zeros((n, 16), dtype=torch.uint8, device="cuda")  # a row stride of 16 bytes, no quant bytes used
+    ws = torch.zeros((n, 0), dtype=torch.int16, device="cuda")
+    xq = torch.zeros((m, 0), dtype=torch.int8, device="cuda")
+    xd = torch.zeros((m, 0), dtype=torch.float32, device="cuda")
+    y = torch.full((m, n), 7.0, device="cuda")
+    host.gemm_into(fmt, wq, ws, xq, xd, y, n, 0)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+def test_gemm_graph_replays(fmt):
+    n, k, m = (200, 1024, 24) if fmt == "q4_0" else (200, 1280, 24)
+    W, x = O.problem(fmt, n, k, m, 51)
+    wq, ws = host.split(fmt, W, n, k)
+    wq, ws = dev(wq), dev(ws)
+    xq, xd, *_ = host.quantize(fmt, dev(x))
+    y_eager, _ = host.gemm(fmt, wq, ws, xq, xd, n, k)
+    y = torch.empty_like(y_eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)
+    for _ in range(3):
+        y.fill_(-1.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager)
