@@ -161,25 +161,36 @@ GemvPlan knob_plan(int block_n, int nb, int num_warps) {
 }
 
 // ---- matrix-core GEMM ----------------------------------------------------------------------------------------------
-// From gemm_min_m(fmt) activation columns on, block_n == 0 in dp4a mode (unfused) runs the matrix-core GEMM, which
-// reads the weights once per 64 columns, instead of the GEMV in column chunks of 3 (measured crossover: Q4_0 between
-// 4 and 8 columns at Llama-3-8B shapes, TQ2_0 below 4 at BitNet-2B shapes).
-int64_t gemm_min_m(int fmt) { return fmt == FMT_Q4_0 ? 8 : 4; }
+// From kGemmMinM activation columns on, block_n == 0 in dp4a mode (unfused) runs the matrix-core GEMM, which reads the
+// weights once per 64 columns, instead of the GEMV in column chunks of 3 (which reads them once for up to 3 columns,
+// in one launch: faster below 4).  At 4 columns the GEMM is 1.2-1.8x faster at Llama-3-8B and BitNet-2B shapes.
+constexpr int64_t kGemmMinM = 4;
 constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (grid.y = columns / 64 at most 16384)
 
-// The GEMM's plan for m columns (one launch) and n rows: 8 waves; columns in groups of at most 64 (4 tiles of 16),
-// split evenly; two 16-row tiles per workgroup (with at most 2 column tiles) when that still gives every CU a
-// workgroup.  False when the shape is past the kernel's 32-bit buffer offsets (64 * K and 32 * SW below 2^31) or its
-// scale slab does not fit in LDS.
+// The GEMM's plan for m columns (one launch) and n rows.  Columns go in groups of at most 64 (4 tiles of 16), split
+// evenly.  The waves of a workgroup split K (wk) and rows (wr) by how many 16-row tiles each CU gets (r, counting
+// column groups): with about one per CU every wave of a CU must share the tile's K, so K is split 8 ways; with a few
+// per CU, 2-4 ways; with many, each wave owns its rows and no partial sums meet.  Measured on MI355X at Llama-3-8B
+// (4096x4096, 14336x4096, 4096x14336, 128256x4096) and BitNet-2B shapes, 1..64 columns.  False when the shape is past
+// the kernel's 32-bit buffer offsets (64 * K and 32 * SW below 2^31) or its scale slab does not fit in LDS.
 bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p) {
   if (64 * k > INT32_MAX || 32 * sw > INT32_MAX) return false;
   const int64_t c16 = (m + 15) / 16;
   const int64_t groups = (c16 + 3) / 4;
-  p->waves = 8;
-  p->cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
-  p->wn = p->cn <= 2 && ((n + 31) / 32) * groups >= device_cus() ? 2 : 1;
-  if (p->wn == 2 && gemm_lds_bytes(fmt, *p, static_cast<int>(k)) > kLdsMax) p->wn = 1;
-  return gemm_lds_bytes(fmt, *p, static_cast<int>(k)) <= kLdsMax;
+  const int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
+  const double r = static_cast<double>((n + 15) / 16) * groups / device_cus();
+  GemmPlan q = {8, 1, 1, cn, 2};
+  if (r > 8.0)
+    q = cn == 1 ? GemmPlan{1, 8, m > 8 ? 2 : 1, 1, 2} : GemmPlan{1, 8, 1, cn, cn == 2 ? 2 : 1};
+  else if (r > 2.0)
+    q = cn == 1 ? GemmPlan{4, 2, 2, 1, 4} : GemmPlan{2, 4, 1, cn, 2};
+  else if (r > 1.25 && cn > 1)
+    q = GemmPlan{4, 2, 1, cn, 2};
+  while (gemm_lds_bytes(fmt, q, static_cast<int>(k)) > kLdsMax && q.wn * q.wr > 1) {  // long rows: fewer rows a group
+    if (q.wn > 1) q.wn = 1; else q = GemmPlan{8, 1, 1, cn, 2};
+  }
+  *p = q;
+  return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;
 }
 
 enum Route { kRouteAuto = 0, kRouteGemm = 1 };
@@ -255,7 +266,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     mats[count++] = w;
   }
   const int64_t nblk = K / blk;
-  if (route == kRouteGemm || (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && M >= gemm_min_m(fmt))) {
+  if (route == kRouteGemm || (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && M >= kGemmMinM)) {
     GemmPlan gp;
     bool fits = true;
     for (int i = 0; i < count; ++i)
@@ -450,9 +461,9 @@ int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* ro
   GemmPlan p;
   if (!gemm_plan(fmt, M < kGemmMaxCols ? M : kGemmMaxCols, N, K, SW, &p))
     return fail(KOMP_EINVAL, "komp_gemm_plan: K=%lld / SW=%lld past the GEMM's limits", (long long)K, (long long)SW);
-  if (rows_per_wg != nullptr) *rows_per_wg = 16 * p.wn;
+  if (rows_per_wg != nullptr) *rows_per_wg = 16 * p.wn * p.wr;
   if (cols_per_wg != nullptr) *cols_per_wg = 16 * p.cn;
-  if (waves != nullptr) *waves = p.waves;
+  if (waves != nullptr) *waves = p.wk * p.wr;
   return KOMP_OK;
 }
 

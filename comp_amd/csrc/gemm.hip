@@ -69,33 +69,52 @@ __device__ __forceinline__ void transpose4(const u32x4& v, unsigned (&t)[4]) {
 // Row stride (in floats) of the f32 scale slab: nblk rounded up to a multiple of 4.
 __host__ __device__ constexpr int slab_stride(int nblk) { return (nblk + 3) & ~3; }
 
+// Row broadcasts: on exit b[j] holds, in every row, row j of v.  permlane32_swap(v, v) gives rows (0 1 0 1) and
+// (2 3 2 3); permlane16_swap of each with itself splits those into single rows.
+__device__ __forceinline__ void bcast_rows(float v, float (&b)[4]) {
+  const unsigned u = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const auto lo = __builtin_amdgcn_permlane16_swap(h[0], h[0], false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(h[1], h[1], false, false);
+  b[0] = __uint_as_float(lo[0]);
+  b[1] = __uint_as_float(lo[1]);
+  b[2] = __uint_as_float(hi[0]);
+  b[3] = __uint_as_float(hi[1]);
+}
+
 __device__ __forceinline__ long pack2(unsigned lo, unsigned hi) {
   return static_cast<long>(static_cast<unsigned long>(lo) | (static_cast<unsigned long>(hi) << 32));
 }
 
-// FMT: FMT_Q4_0 / FMT_TQ2_0; W waves; WN 16-row and CN 16-column tiles per workgroup; D steps in flight per wave.
-template <int FMT, int W, int WN, int CN, int D>
-__global__ void __launch_bounds__(64 * W)
+// FMT: FMT_Q4_0 / FMT_TQ2_0.  WK x WR waves: WR row groups of WN 16-row tiles each, every group's K split over WK
+// waves.  CN 16-column tiles.  D steps in flight per wave.  STORE_S: also write the block dots to S (a separate
+// instantiation, so the plain kernel's step loop has no branch between an MFMA and the scaling of its result).
+template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
+__global__ void __launch_bounds__(64 * WK * WR)
 gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const uint8_t* __restrict__ WQ,
             const int16_t* __restrict__ WS, const int8_t* __restrict__ XQ, const float* __restrict__ XD,
             float* __restrict__ Y, int32_t* __restrict__ S) {
   // ss: row stride of the f32 scale slab in LDS, nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four
   // scales of a row with one 16-byte LDS load).
   constexpr bool Q4 = FMT == FMT_Q4_0;
-  constexpr int XV = Q4 ? 2 : 4;   // 16-byte activation loads per column tile per step
-  constexpr int DXN = Q4 ? 4 : 1;  // activation scales per column per step
-  constexpr int RPW = 16 * WN / W;  // slab rows each wave stages
-  static_assert(RPW >= 1 && RPW * W == 16 * WN, "the waves split the workgroup's rows evenly");
+  constexpr int W = WK * WR;
+  constexpr int XV = Q4 ? 2 : 4;        // 16-byte activation loads per column tile per step
+  constexpr int WGR = 16 * WN * WR;     // rows per workgroup
+  constexpr int RPW = WGR / W;          // slab rows each wave stages
+  static_assert(RPW >= 1 && RPW * W == WGR, "the waves split the workgroup's rows evenly");
   extern __shared__ __align__(16) unsigned char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wk = wave % WK;  // this wave's K share ...
+  const int wr = wave / WK;  // ... of row group wr
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int n0 = blockIdx.x * (16 * WN);
+  const int n0 = blockIdx.x * WGR;
+  const int nw = n0 + 16 * WN * wr;  // first row of this wave's tiles
   const int m0 = blockIdx.y * (16 * CN);
-  const int rows = min(16 * WN, N - n0);  // valid rows and columns of the tile
+  const int rows = max(0, min(16 * WN, N - nw));  // valid rows of this wave's tiles, valid columns of the workgroup
   const int cols = min(16 * CN, M - m0);
-  const auto wq = rsrc(WQ + n0 * SW, rows * SW);
+  const auto wq = rsrc(WQ + nw * SW, rows * SW);
   const auto xq = rsrc(XQ + static_cast<int64_t>(m0) * K, static_cast<int64_t>(cols) * K);
   const auto xd = rsrc(XD + static_cast<int64_t>(m0) * nblk, static_cast<int64_t>(cols) * nblk * 4);
 
@@ -105,18 +124,20 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
   unsigned va[WN];
 #pragma unroll
   for (int t = 0; t < WN; ++t) va[t] = static_cast<unsigned>((16 * t + r16) * SW + 16 * g);
+  // Q4_0 activations: load v of column c takes bytes 64v + 16g .. +15 of the step (64 contiguous bytes per column per
+  // load); after the dword transpose these are exactly the B halves of blocks 2v and 2v + 1 (see compute).
   unsigned vx[CN], vd[CN];
 #pragma unroll
   for (int u = 0; u < CN; ++u) {
     const int c = 16 * u + r16;
-    vx[u] = static_cast<unsigned>(Q4 ? c * K + 32 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
-    vd[u] = static_cast<unsigned>(c * nblk * 4);
+    vx[u] = static_cast<unsigned>(Q4 ? c * K + 16 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
+    vd[u] = static_cast<unsigned>(c * nblk * 4 + (Q4 ? 4 * g : 0));
   }
 
   struct Step {
     u32x4 a[WN];
     u32x4 x[CN][XV];
-    float dx[CN][DXN];
+    float dx[CN];  // Q4_0: d_x of block 4s+g (row group g's own block); TQ2_0: d_x of block s
   };
   auto load = [&](Step& st, int s) {
     const bool sv = s < nsteps;  // wave-uniform
@@ -129,42 +150,47 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
     for (int u = 0; u < CN; ++u) {
 #pragma unroll
       for (int v = 0; v < XV; ++v)
-        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (Q4 ? 16 * v : 32 * v), sx, 0);
-#pragma unroll
-      for (int j = 0; j < DXN; ++j)
-        st.dx[u][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u] + 4 * j, sd, 0));
+        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (Q4 ? 64 * v : 32 * v), sx, 0);
+      st.dx[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u], sd, 0));
     }
   };
 
-  const int my = nsteps > wave ? (nsteps - wave + W - 1) / W : 0;  // this wave's steps (wave-uniform)
+  // ---- the scale slab: f32 d_w of the workgroup's rows, row stride ss, zero past row N and past block nblk ----
+  // Its first batch of loads is issued before the step loads, so converting it waits for nothing else.
+  float* slab = reinterpret_cast<float*>(lds);
+  const auto ws = rsrc(WS + static_cast<int64_t>(n0) * nblk, static_cast<int64_t>(max(0, min(WGR, N - n0))) * nblk * 2);
+  constexpr int kBatch = 4;  // 64-block column chunks per slab row per batch
+  unsigned short h[RPW][kBatch];
+  auto slab_load = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int col = c0 + 64 * b + lane;
+        h[i][b] = __builtin_amdgcn_raw_buffer_load_b16(
+            ws, col < nblk ? static_cast<unsigned>(((wave * RPW + i) * nblk + col) * 2) : kOob, 0, 0);
+      }
+  };
+  auto slab_store = [&](int c0) {  // columns past ss go to a per-lane spill slot after the slab (no branch)
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int col = c0 + 64 * b + lane;
+        slab[col < ss ? (wave * RPW + i) * ss + col : WGR * ss + lane] = f16_bits_to_f32(static_cast<int16_t>(h[i][b]));
+      }
+  };
+  slab_load(0);
+
+  const int my = nsteps > wk ? (nsteps - wk + WK - 1) / WK : 0;  // this wave's steps (wave-uniform)
   Step ring[D];
 #pragma unroll
-  for (int d = 0; d < D; ++d) load(ring[d], wave + W * d);
+  for (int d = 0; d < D; ++d) load(ring[d], wk + WK * d);
 
-  // ---- the scale slab: f32 d_w of rows n0 .. n0 + 16*WN, row stride ss, zero past row N and past block nblk ----
-  float* slab = reinterpret_cast<float*>(lds);
-  {
-    const auto ws = rsrc(WS + static_cast<int64_t>(n0) * nblk, static_cast<int64_t>(rows) * nblk * 2);
-    constexpr int kBatch = 8;  // 2-byte loads per row per batch, all issued before the first conversion
-    for (int c0 = 0; c0 < ss; c0 += 64 * kBatch) {
-      unsigned short h[RPW][kBatch];
-#pragma unroll
-      for (int i = 0; i < RPW; ++i)
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-          const int row = wave * RPW + i;
-          const int col = c0 + 64 * b + lane;
-          h[i][b] = __builtin_amdgcn_raw_buffer_load_b16(
-              ws, col < nblk ? static_cast<unsigned>((row * nblk + col) * 2) : kOob, 0, 0);
-        }
-#pragma unroll
-      for (int i = 0; i < RPW; ++i)
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-          const int col = c0 + 64 * b + lane;
-          if (col < ss) slab[(wave * RPW + i) * ss + col] = f16_bits_to_f32(static_cast<int16_t>(h[i][b]));
-        }
-    }
+  slab_store(0);
+  for (int c0 = 64 * kBatch; c0 < ss; c0 += 64 * kBatch) {  // rows of more than 64 * kBatch blocks
+    slab_load(c0);
+    slab_store(c0);
   }
   __syncthreads();
 
@@ -178,26 +204,34 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
     const int col = m0 + 16 * u + r16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = n0 + 16 * t + 4 * g + r;
+      const int row = nw + 16 * t + 4 * g + r;
       if (col < M && row < N) S[(static_cast<int64_t>(col) * N + row) * nblk + b] = cc[r];
     }
   };
 
   auto compute = [&](const Step& st, int s) {
     if constexpr (Q4) {
-      unsigned ta[WN][4], tu[CN][4], tv[CN][4];
+      // weights: row group g holds block 4s+g; after the transpose ta[t][j] (row group g) is dword g of block 4s+j.
+      // activations: load v, row group g holds dwords 0..3 of half g%2 of block 2v + g/2; after the transpose
+      // xt[u][v][2i + h] (row group g) is dword g of half h of block 2v + i, i.e. xt[u][j / 2][2 (j % 2) + h] holds
+      // x[4g .. 4g+3] (h = 0) and x[16 + 4g .. 16 + 4g+3] (h = 1) of block 4s+j.
+      // d_x: row group g holds block 4s+g's; dxb[u][j] is block 4s+j's in every row group (row broadcasts).
+      unsigned ta[WN][4], xt[CN][2][4];
+      float dxb[CN][4];
 #pragma unroll
       for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
 #pragma unroll
       for (int u = 0; u < CN; ++u) {
-        transpose4(st.x[u][0], tu[u]);
-        transpose4(st.x[u][1], tv[u]);
+        transpose4(st.x[u][0], xt[u][0]);
+        transpose4(st.x[u][1], xt[u][1]);
+        bcast_rows(st.dx[u], dxb[u]);
       }
       f32x4 dw[WN][4];  // [t][r] = d_w of row 16t + 4g + r, blocks 4s .. 4s+3
 #pragma unroll
       for (int t = 0; t < WN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dw[t][r] = *reinterpret_cast<const f32x4*>(slab + (16 * t + 4 * g + r) * ss + 4 * s);
+        for (int r = 0; r < 4; ++r)
+          dw[t][r] = *reinterpret_cast<const f32x4*>(slab + (16 * (WN * wr + t) + 4 * g + r) * ss + 4 * s);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int b = 4 * s + j;
@@ -206,7 +240,7 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
         i32x4 corr[CN];
 #pragma unroll
         for (int u = 0; u < CN; ++u) {
-          bj[u] = pack2(tu[u][j], tv[u][j]);
+          bj[u] = pack2(xt[u][j >> 1][2 * (j & 1)], xt[u][j >> 1][2 * (j & 1) + 1]);
           corr[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(0xF8F8F8F8F8F8F8F8ull), bj[u],
                                                           i32x4{0, 0, 0, 0}, 0, 0, 0);
         }
@@ -216,10 +250,10 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
 #pragma unroll
           for (int u = 0; u < CN; ++u) {
             const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(aj, bj[u], corr[u], 0, 0, 0);
-            if (S != nullptr) store_s(cc, t, u, b);
+            if constexpr (STORE_S) store_s(cc, t, u, b);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              acc[t][u][r] = __builtin_fmaf(static_cast<float>(cc[r]) * dw[t][r][j], st.dx[u][j], acc[t][u][r]);
+              acc[t][u][r] = __builtin_fmaf(static_cast<float>(cc[r]) * dw[t][r][j], dxb[u][j], acc[t][u][r]);
           }
         }
       }
@@ -237,7 +271,7 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
       for (int t = 0; t < WN; ++t) {
         float dw[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dw[r] = slab[(16 * t + 4 * g + r) * ss + s];
+        for (int r = 0; r < 4; ++r) dw[r] = slab[(16 * (WN * wr + t) + 4 * g + r) * ss + s];
         i32x4 aj[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -251,10 +285,10 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
           for (int v = 0; v < 4; ++v)
             cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aj[v], reinterpret_cast<const i32x4&>(st.x[u][v]), cc, 0, 0,
                                                         0);
-          if (S != nullptr) store_s(cc, t, u, s);
+          if constexpr (STORE_S) store_s(cc, t, u, s);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            acc[t][u][r] = __builtin_fmaf(st.dx[u][0] * dw[r], static_cast<float>(cc[r]), acc[t][u][r]);
+            acc[t][u][r] = __builtin_fmaf(st.dx[u] * dw[r], static_cast<float>(cc[r]), acc[t][u][r]);
         }
       }
     }
@@ -265,31 +299,43 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
     for (int d = 0; d < D; ++d) {
       const int i = i0 + d;
       if (i < my) {
-        compute(ring[d], wave + W * i);
-        load(ring[d], i + D < my ? wave + W * (i + D) : nsteps);  // past the wave's last step: zeros, no traffic
+        compute(ring[d], wk + WK * i);
+        load(ring[d], i + D < my ? wk + WK * (i + D) : nsteps);  // past the wave's last step: zeros, no traffic
       }
     }
   }
 
-  // ---- partials of the W waves, added in wave order ----
-  __syncthreads();  // every wave is done with the slab
-  float* red = reinterpret_cast<float*>(lds);
+  if constexpr (WK == 1) {  // each wave holds whole dots: store them
 #pragma unroll
-  for (int t = 0; t < WN; ++t)
+    for (int t = 0; t < WN; ++t)
 #pragma unroll
-    for (int u = 0; u < CN; ++u)
+      for (int u = 0; u < CN; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[((((wave * WN + t) * CN + u) * 4 + r) << 6) + lane] = acc[t][u][r];
-  __syncthreads();
-  for (int idx = wave; idx < WN * CN * 4; idx += W) {
-    const int r = idx & 3;
-    const int u = (idx >> 2) % CN;
-    const int t = (idx >> 2) / CN;
-    float sum = red[(((t * CN + u) * 4 + r) << 6) + lane];
-    for (int w = 1; w < W; ++w) sum += red[((((w * WN + t) * CN + u) * 4 + r) << 6) + lane];
-    const int row = n0 + 16 * t + 4 * g + r;
-    const int col = m0 + 16 * u + r16;
-    if (row < N && col < M) Y[static_cast<int64_t>(col) * N + row] = sum;
+        for (int r = 0; r < 4; ++r) {
+          const int row = nw + 16 * t + 4 * g + r;
+          const int col = m0 + 16 * u + r16;
+          if (row < N && col < M) Y[static_cast<int64_t>(col) * N + row] = acc[t][u][r];
+        }
+  } else {  // partials of the WK waves of a row group, added in wave order
+    __syncthreads();  // every wave is done with the slab
+    float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int t = 0; t < WN; ++t)
+#pragma unroll
+      for (int u = 0; u < CN; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((((wave * WN + t) * CN + u) * 4 + r) << 6) + lane] = acc[t][u][r];
+    __syncthreads();
+    for (int idx = wk; idx < WN * CN * 4; idx += WK) {
+      const int r = idx & 3;
+      const int u = (idx >> 2) % CN;
+      const int t = (idx >> 2) / CN;
+      float sum = 0.f;
+      for (int w = 0; w < WK; ++w) sum += red[(((((wr * WK + w) * WN + t) * CN + u) * 4 + r) << 6) + lane];
+      const int row = nw + 16 * t + 4 * g + r;
+      const int col = m0 + 16 * u + r16;
+      if (row < N && col < M) Y[static_cast<int64_t>(col) * N + row] = sum;
+    }
   }
 }
 
@@ -297,46 +343,62 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
 
 namespace {
 
-template <int FMT, int W, int WN, int CN, int D>
-hipError_t launch_t(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
+hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
   const int blk = FMT == FMT_Q4_0 ? 32 : 256;
   const int nblk = c.k / blk;
   const int nsteps = FMT == FMT_Q4_0 ? (nblk + 3) / 4 : nblk;
-  const dim3 grid((c.n + 16 * WN - 1) / (16 * WN), (c.m + 16 * CN - 1) / (16 * CN));
-  const dim3 block(64 * W);
+  const dim3 grid((c.n + 16 * WN * WR - 1) / (16 * WN * WR), (c.m + 16 * CN - 1) / (16 * CN));
+  const dim3 block(64 * WK * WR);
   const size_t lds = gemm_lds_bytes(FMT, p, c.k);
-  auto kern = gemm_impl::gemm_kernel<FMT, W, WN, CN, D>;
+  auto kern = gemm_impl::gemm_kernel<FMT, WK, WR, WN, CN, D, STORE_S>;
   const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
   hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, nsteps,
                         gemm_impl::slab_stride(nblk), c.sw, c.wq, c.ws, c.xq, c.xd, c.y, c.s);
   return hipGetLastError();
 }
 
-// Instantiated plans: 8 waves; one 16-row tile with 1..4 column tiles, or two with 1..2 (two row tiles with more
-// columns would not fit 256 VGPRs).  Four steps in flight with one column tile, two with more.
+template <int FMT, int WK, int WR, int WN, int CN, int D>
+hipError_t launch_t(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+  return c.s != nullptr ? launch_s<FMT, WK, WR, WN, CN, D, true>(c, p, stream)
+                        : launch_s<FMT, WK, WR, WN, CN, D, false>(c, p, stream);
+}
+
+// The instantiated plans (gemm_plan in abi.hip picks one): (wk, wr, wn, cn, d).
 template <int FMT>
 hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
-  if (p.wn == 2) return p.cn == 1 ? launch_t<FMT, 8, 2, 1, 4>(c, p, stream) : launch_t<FMT, 8, 2, 2, 2>(c, p, stream);
-  switch (p.cn) {
-    case 1: return launch_t<FMT, 8, 1, 1, 4>(c, p, stream);
-    case 2: return launch_t<FMT, 8, 1, 2, 2>(c, p, stream);
-    case 3: return launch_t<FMT, 8, 1, 3, 2>(c, p, stream);
-    default: return launch_t<FMT, 8, 1, 4, 2>(c, p, stream);
-  }
+#define KOMP_GEMM_PLAN(WK, WR, WN, CN, D) \
+  if (p.wk == WK && p.wr == WR && p.wn == WN && p.cn == CN && p.d == D) return launch_t<FMT, WK, WR, WN, CN, D>(c, p, stream);
+  KOMP_GEMM_PLAN(8, 1, 1, 1, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 2, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 3, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 4, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 2, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 3, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 4, 2)
+  KOMP_GEMM_PLAN(4, 2, 2, 1, 4)
+  KOMP_GEMM_PLAN(2, 4, 1, 2, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 3, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 4, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 1, 2)
+  KOMP_GEMM_PLAN(1, 8, 2, 1, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 2, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 3, 1)
+  KOMP_GEMM_PLAN(1, 8, 1, 4, 1)
+#undef KOMP_GEMM_PLAN
+  return hipErrorInvalidConfiguration;
 }
 
 }  // namespace
 
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k) {
   const int nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
-  const size_t slab = static_cast<size_t>(16) * p.wn * gemm_impl::slab_stride(nblk) * 4;
-  const size_t red = static_cast<size_t>(p.waves) * p.wn * p.cn * 4 * 64 * 4;
+  const size_t slab = (static_cast<size_t>(16) * p.wn * p.wr * gemm_impl::slab_stride(nblk) + 64) * 4;  // + spill slots
+  const size_t red = p.wk > 1 ? static_cast<size_t>(p.wk) * p.wr * p.wn * p.cn * 4 * 64 * 4 : 0;
   return slab > red ? slab : red;
 }
 
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
-  if (p.waves != 8 || p.wn < 1 || p.wn > 2 || p.cn < 1 || p.cn > 4 || (p.wn == 2 && p.cn > 2))
-    return hipErrorInvalidConfiguration;
   return c.fmt == FMT_Q4_0 ? launch_fmt<FMT_Q4_0>(c, p, stream) : launch_fmt<FMT_TQ2_0>(c, p, stream);
 }
 

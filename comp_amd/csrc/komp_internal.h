@@ -54,12 +54,14 @@ struct GemvCall {
   GemvSegs segs;  // first_wg is filled in at launch, from the plan
 };
 
-// Matrix-core GEMM (any number of activation columns): waves per workgroup, 16-row tiles (wn) and 16-column tiles
-// (cn) per workgroup.
+// Matrix-core GEMM (any number of activation columns): a workgroup of wk x wr waves covers wr row groups of wn
+// 16-row tiles (wk waves split each group's K) and cn 16-column tiles; d K steps in flight per wave.
 struct GemmPlan {
-  int waves;
+  int wk;
+  int wr;
   int wn;
   int cn;
+  int d;
 };
 
 struct GemmCall {

@@ -31,7 +31,7 @@ FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale off
 }
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
 FMT_ID = {"q4_0": 0, "tq2_0": 1}
-GEMM_MIN_M = {"q4_0": 8, "tq2_0": 4}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
+GEMM_MIN_M = {"q4_0": 4, "tq2_0": 4}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
 
 
 def split(fmt, W, n, k):
@@ -231,8 +231,7 @@ def gemm_plan(fmt, m, n, k, sw=None):
 
 
 def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
-    """True when gemv(..., block_n=None) runs the matrix-core GEMM for this shape (unfused, dp4a, from 8 columns for
-    q4_0 and from 4 for tq2_0)."""
+    """True when gemv(..., block_n=None) runs the matrix-core GEMM for this shape (unfused, dp4a, from 4 columns)."""
     return not fused and mode == 2 and m >= GEMM_MIN_M[fmt] and gemm_plan(fmt, m, n, k, sw) is not None
 
 

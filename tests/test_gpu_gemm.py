@@ -63,15 +63,28 @@ def test_gemm_unaligned_scales_and_padded_rows(fmt):
     check(fmt, 64, 2 * k if fmt == "q4_0" else 1024, 8, 12, ws_offset=3)
 
 
+# one shape per plan family on a 256-CU device: (n, k, m, rows per workgroup, columns per workgroup)
+FAMILIES = [
+    (4000, 512, 20, 16, 32),    # ~1 row tile per CU: K split over 8 waves
+    (6144, 512, 20, 32, 32),    # 1.5 per CU, 2 column tiles: 4 x 2 waves
+    (9600 + 7, 512, 12, 64, 16),  # 2..8 per CU, 1 column tile: 4 x 2 waves, 2 row tiles each
+    (9600, 256, 20, 64, 32),    # 2..8 per CU, 2 column tiles: 2 x 4 waves
+    (33600, 256, 4, 128, 16),   # > 8 per CU: 8 waves, each its own rows
+    (33600 - 5, 256, 12, 256, 16),  # ... 2 row tiles each
+    (16400, 256, 70, 128, 48),  # ... 3 column tiles, 2 column groups
+]
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
-def test_gemm_two_row_tiles(fmt):
-    # tall enough that each workgroup takes 32 rows (one per CU or more)
-    n = 32 * 300
-    k = 256
-    assert host.gemm_plan(fmt, 4, n, k)["rows"] == 32 and host.gemm_plan(fmt, 70, n, k)["rows"] == 16
-    check(fmt, n + 7, k, 4, 21)
-    check(fmt, n, k, 20, 22)
-    check(fmt, n, k, 70, 23)
+@pytest.mark.parametrize("fam", range(len(FAMILIES)))
+def test_gemm_plan_families(fmt, fam):
+    n, k, m, rows, cols = FAMILIES[fam]
+    if fmt == "tq2_0":
+        k = 512 if k == 256 else 1024
+    plan = host.gemm_plan(fmt, m, n, k)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert (plan["rows"], plan["cols"]) == (rows, cols), plan
+    check(fmt, n, k, m, 60 + fam)
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
