@@ -17,7 +17,8 @@ dispatches' algorithmic bytes / their average dispatch duration, timed per dispa
 (the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
 sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold,
 library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
-gemv_multi launch against one launch per matrix.
+gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
+(Q4_0) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3 columns.
 """
 
 from __future__ import annotations
@@ -362,6 +363,65 @@ def multi_detail(torch, host, args):
     return rows
 
 
+BATCH_CASES = (  # (name, fmt, N, K): decode projections, several tokens at once
+    ("llama3_8b_attn_o", "q4_0", 4096, 4096),
+    ("llama3_8b_ffn_gate", "q4_0", 14336, 4096),
+    ("llama3_8b_ffn_down", "q4_0", 4096, 14336),
+    ("bitnet2b_ffn_gate", "tq2_0", 6912, 2560),
+    ("bitnet2b_ffn_down", "tq2_0", 2560, 6912),
+)
+BATCH_M = (4, 16, 64)
+
+
+def batched_detail(torch, host, args):
+    """Several activation columns (batched decode tokens) per weight matrix, q8 activations in: the matrix-core GEMM
+    (what gemv with block_n=None runs from 4 columns) vs the GEMV in launches of 3 columns (its own knobs for that
+    column count), both as graph replays over cold weight copies.  Bytes: weights + q8 activations + f32 outputs."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 3)
+    for name, fmt, n, k in BATCH_CASES:
+        copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
+        nc = len(copies)
+        for m in BATCH_M:
+            x = torch.randn((m, k), generator=gen, device="cuda")
+            xq, xd = host.quantize(fmt, x)
+            y_g = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            y_c = torch.empty_like(y_g)
+            bn, nb, nw = host.auto_config(fmt, m, n, k)
+
+            def gemm(i, copies=copies, xq=xq, xd=xd, y=y_g, fmt=fmt, n=n, k=k):
+                wq, ws = copies[i % nc]
+                host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)
+
+            def chunks(i, copies=copies, xq=xq, xd=xd, y=y_c, fmt=fmt, n=n, k=k, knobs=(bn, nb, nw)):
+                wq, ws = copies[i % nc]
+                host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, knobs[0], knobs[1], 2, knobs[2])
+
+            per_graph = nc * math.ceil(64 / nc)
+            reps = 2 * per_graph
+            ms_g, _ = timed_steps(torch, gemm, nc, reps, per_graph)
+            ms_c, _ = timed_steps(torch, chunks, nc, reps, per_graph)
+            gemm(0)
+            chunks(0)
+            torch.cuda.synchronize()
+            rel = float((y_g - y_c).abs().max() / y_c.abs().max())
+            if rel > 1e-5:
+                raise RuntimeError(f"{name} m={m}: GEMM and GEMV outputs differ by {rel:.2e} (relative)")
+            b = gemv_bytes(fmt, n, k, m)
+            us_g, us_c = ms_g * 1e3 / reps, ms_c * 1e3 / reps
+            plan = host.gemm_plan(fmt, m, n, k)
+            rows.append({"case": name, "fmt": fmt, "n": n, "k": k, "m": m, "bytes": b,
+                         "gemm_plan_rows_cols_waves": [plan["rows"], plan["cols"], plan["waves"]],
+                         "us_gemm": round(us_g, 3), "us_gemv_chunks": round(us_c, 3),
+                         "launches_chunks": math.ceil(m / 3), "speedup": round(us_c / us_g, 3),
+                         "gbs_gemm": round(b / us_g / 1e3, 1), "pct_peak_gemm": round(b / us_g / 1e3 / PEAK_GBS * 100, 1),
+                         "copies": nc})  # fmt: skip
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -416,6 +476,7 @@ def main():
     if not args.no_detail:
         out["detail"] = detail(torch, host, _abi, args)
         out["multi_matrix"] = multi_detail(torch, host, args)
+        out["batched_gemm"] = batched_detail(torch, host, args)
     print(json.dumps(out), flush=True)
     return 0
 
