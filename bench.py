@@ -40,7 +40,7 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
 # profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
-TRAFFIC_FUSED_BITNET_M1 = 4877592
+TRAFFIC_FUSED_BITNET_M1 = 4882640
 
 
 def gemv_bytes(fmt, n, k, m):
@@ -422,6 +422,29 @@ def batched_detail(torch, host, args):
     return rows
 
 
+def batched_calls(torch, host, args):
+    """The batched_gemm cases' GEMMs, args.batched_calls eager calls each over cold weight copies, untimed: the
+    dispatches a hardware-counter run reads (graph replays of hundreds of calls per case are too many for one)."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 3)
+    for name, fmt, n, k in BATCH_CASES:
+        copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
+        for m in BATCH_M:
+            x = torch.randn((m, k), generator=gen, device="cuda")
+            xq, xd = host.quantize(fmt, x)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            for i in range(args.batched_calls):
+                wq, ws = copies[i % len(copies)]
+                host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)
+            torch.cuda.synchronize()
+            rows.append({"case": name, "fmt": fmt, "n": n, "k": k, "m": m, "calls": args.batched_calls,
+                         "bytes": gemv_bytes(fmt, n, k, m)})
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -436,6 +459,11 @@ def main():
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only run the batched_gemm block (for profiling the GEMM by itself)")
+    ap.add_argument("--batched-calls", type=int, default=0, metavar="N",
+                    help="with --batched-only: run each case's GEMM N times eagerly instead of timing it (a few "
+                         "dispatches, for hardware-counter runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB device buffer 10 times (the known-size kernel that scales the PMC "
                          "FETCH_SIZE / WRITE_SIZE readings)")  # fmt: skip
@@ -464,6 +492,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 10}), flush=True)
+        return 0
+
+    if args.batched_only:
+        rows = batched_calls(torch, host, args) if args.batched_calls > 0 else batched_detail(torch, host, args)
+        print(json.dumps({"batched_gemm": rows}), flush=True)
         return 0
 
     value, ms_per_step, roofline, config, step_bytes = headline(torch, host, _abi, args)
