@@ -18,7 +18,8 @@ dispatches' algorithmic bytes / their average dispatch duration, timed per dispa
 sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold,
 library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
 gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
-(Q4_0) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3 columns.
+(Q4_0) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3 columns; ingest = ggml block
+bytes split into the planes on the device.
 """
 
 from __future__ import annotations
@@ -422,6 +423,44 @@ def batched_detail(torch, host, args):
     return rows
 
 
+INGEST_CASES = (  # (name, fmt, N, K): one weight matrix's ggml block bytes, split on the device
+    ("llama3_8b_ffn_gate", "q4_0", 14336, 4096),
+    ("llama3_8b_lm_head", "q4_0", 128256, 4096),
+    ("bitnet2b_ffn_gate", "tq2_0", 6912, 2560),
+)
+
+
+def ingest_detail(torch, host, args):
+    """ggml block bytes -> split planes on the device (split_into), graph replays over copies of the block bytes;
+    bytes = block bytes read + plane bytes written."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 4)
+    for name, fmt, n, k in INGEST_CASES:
+        f = host.FORMATS[fmt]
+        nb = k // f["block"]
+        size = n * nb * f["nbytes"]
+        ncopy = max(2, math.ceil((COLD_BYTES // 2) / size))
+        blocks = [torch.randint(0, 256, (size,), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(ncopy)]
+        wq = torch.empty((n, nb * f["qbytes"]), dtype=torch.uint8, device="cuda")
+        ws = torch.empty((n, nb), dtype=torch.int16, device="cuda")
+
+        def call(i, blocks=blocks, wq=wq, ws=ws, fmt=fmt, n=n, k=k):
+            host.split_into(fmt, blocks[i % len(blocks)], wq, ws, n, k)
+
+        per_graph = ncopy * math.ceil(16 / ncopy)
+        reps = 2 * per_graph
+        ms, _ = timed_steps(torch, call, ncopy, reps, per_graph)
+        b = size + n * nb * (f["qbytes"] + 2)
+        us = ms * 1e3 / reps
+        rows.append({"case": name, "fmt": fmt, "n": n, "k": k, "bytes": b, "us": round(us, 3),
+                     "gbs": round(b / us / 1e3, 1), "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1),
+                     "copies": ncopy})  # fmt: skip
+        del blocks, wq, ws
+        torch.cuda.empty_cache()
+    return rows
+
+
 def batched_calls(torch, host, args):
     """The batched_gemm cases' GEMMs, args.batched_calls eager calls each over cold weight copies, untimed: the
     dispatches a hardware-counter run reads (graph replays of hundreds of calls per case are too many for one)."""
@@ -510,6 +549,7 @@ def main():
         out["detail"] = detail(torch, host, _abi, args)
         out["multi_matrix"] = multi_detail(torch, host, args)
         out["batched_gemm"] = batched_detail(torch, host, args)
+        out["ingest"] = ingest_detail(torch, host, args)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkomp_hip.so")
-SOURCES = ("abi.hip", "quant.hip", "gemv.hip", "gemv_fused.hip", "gemm.hip")
+SOURCES = ("abi.hip", "quant.hip", "gemv.hip", "gemv_fused.hip", "gemm.hip", "split.hip")
 ARCH = "gfx950"
 
 

@@ -440,6 +440,34 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
   return gemv_entry(FMT_TQ2_0, true, "komp_tq2_0_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);
 }
 
+namespace {
+int split_entry(int fmt, const char* name, const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K,
+                int64_t SW, void* stream) {
+  const int blk = fmt == FMT_Q4_0 ? 32 : 256;
+  const int64_t qbytes = fmt == FMT_Q4_0 ? 16 : 64;
+  if (N < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (N=%lld K=%lld)", name, (long long)N, (long long)K);
+  if (K % blk) return fail(KOMP_EINVAL, "%s: K=%lld is not a multiple of the %d-value block", name, (long long)K, blk);
+  if (K > INT32_MAX) return fail(KOMP_EINVAL, "%s: K must be < 2^31", name);
+  const int64_t row_bytes = K / blk * qbytes;
+  if (N > 0 && (SW < row_bytes || SW % 16))
+    return fail(KOMP_EINVAL, "%s: SW=%lld must be a multiple of 16 and >= %lld (the quant bytes of a row)", name,
+                (long long)SW, (long long)row_bytes);
+  if (N == 0 || K == 0) return KOMP_OK;
+  if (W == nullptr || WQ == nullptr || WS == nullptr) return fail(KOMP_EINVAL, "%s: NULL pointer", name);
+  if (!aligned(W, 4) || !aligned(WQ, 16) || !aligned(WS, 2))
+    return fail(KOMP_EINVAL, "%s: W must be 4-byte aligned, WQ 16-byte aligned, WS 2-byte aligned", name);
+  return hip_status(launch_split(fmt, W, WQ, WS, N, K, SW, static_cast<hipStream_t>(stream)), name);
+}
+}  // namespace
+
+int komp_q4_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream) {
+  return split_entry(FMT_Q4_0, "komp_q4_0_split", W, WQ, WS, N, K, SW, stream);
+}
+
+int komp_tq2_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream) {
+  return split_entry(FMT_TQ2_0, "komp_tq2_0_split", W, WQ, WS, N, K, SW, stream);
+}
+
 int komp_q4_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                    int64_t M, int64_t N, int64_t K, int64_t SW, void* stream) {
   const GemvMat w{WQ, WS, Y, S, N, SW};

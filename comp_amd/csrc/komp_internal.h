@@ -91,6 +91,8 @@ hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream)
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
+hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,
+                        hipStream_t stream);
 hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,

@@ -46,6 +46,47 @@ def split(fmt, W, n, k):
     return wq, ws
 
 
+def split_device(fmt, W, n, k, sw=None):
+    """ggml blocks already on the device (uint8 tensor of n * (k / block) blocks) -> (WQ uint8 [n][sw], WS int16
+    [n][blocks]) on the same device, bytes equal to split()'s.  sw: WQ row stride in bytes (default the packed row,
+    rounded up to 16).  The device counterpart of src/komp/host.py:16-22."""
+    f = FORMATS[fmt]
+    _need(W, "W", torch.uint8)
+    nb = k // f["block"]
+    if k % f["block"] or n < 0:
+        raise _abi.KompArgumentError(f"split_device: k={k} must be a multiple of {f['block']}")
+    if W.numel() != n * nb * f["nbytes"] or not W.is_contiguous():
+        raise _abi.KompArgumentError(f"split_device: W must be {n * nb * f['nbytes']} contiguous bytes, got {W.numel()}")
+    row = nb * f["qbytes"]
+    sw = (row + 15) // 16 * 16 if sw is None else sw
+    wq = torch.empty((n, sw), dtype=torch.uint8, device=W.device)
+    ws = torch.empty((n, nb), dtype=torch.int16, device=W.device)
+    split_into(fmt, W, wq, ws, n, k)
+    return wq[:, :row], ws
+
+
+def split_into(fmt, W, wq, ws, n, k):
+    """Allocation-free split_device into preallocated wq uint8 [n][sw] (row stride sw, a multiple of 16) and ws int16
+    [n][blocks]."""
+    f = FORMATS[fmt]
+    _need(W, "W", torch.uint8)
+    _need(wq, "wq", torch.uint8, 2)
+    _need(ws, "ws", torch.int16, 2)
+    nb = k // f["block"]
+    if tuple(ws.shape) != (n, nb) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"split_into: ws must be a contiguous [{n}][{nb}] plane")
+    if wq.shape[0] != n or wq.shape[1] < nb * f["qbytes"] or (wq.numel() and wq.stride(1) != 1):
+        raise _abi.KompArgumentError(f"split_into: wq must be [{n}][>= {nb * f['qbytes']}] with contiguous rows")
+    if W.numel() != n * nb * f["nbytes"] or not W.is_contiguous():
+        raise _abi.KompArgumentError(f"split_into: W must be {n * nb * f['nbytes']} contiguous bytes")
+    for t, name in ((wq, "wq"), (ws, "ws")):
+        if t.device != W.device:
+            raise _abi.KompArgumentError(f"{name} is on {t.device}, W on {W.device}")
+    fn = "komp_q4_0_split" if fmt == "q4_0" else "komp_tq2_0_split"
+    with torch.cuda.device(W.device):
+        _abi.call(fn, W.data_ptr(), wq.data_ptr(), ws.data_ptr(), n, k, wq.stride(0) if n else 16, _stream(W))
+
+
 def split_q4_0(W, n, k):
     return split("q4_0", W, n, k)
 

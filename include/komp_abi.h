@@ -131,6 +131,14 @@ int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, cons
 int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
                    int* waves);
 
+/* ggml block bytes -> KURN's split planes on the device.  W: N rows of K/32 Q4_0 blocks (18 bytes: f16 d, 16 quant
+ * bytes) or K/256 TQ2_0 blocks (66 bytes: 64 quant bytes, f16 d), contiguous, 4-byte aligned.  Writes WQ u8 [N][SW]
+ * (16-byte aligned, SW % 16 == 0, SW >= K/2 resp. K/4; the padding past a row's quant bytes is left as it was) and
+ * WS i16 [N][K/blk] (2-byte aligned); the bytes equal the reference's host split.
+ * Replaces: host.split (src/komp/host.py:16-22), which does this with numpy on the host. */
+int komp_q4_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
+int komp_tq2_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
+
 /* OUT[i] = dp4a(A[i], B[i], C[i]) for i < n; mode KOMP_MODE_DP4A (hardware) or KOMP_MODE_DP4A_EMU.
  * Replaces: kernels.dp4a_probe (src/komp/kernels.py:145-149). */
 int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,
@@ -146,7 +154,8 @@ int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* strea
  * Between komp_timing_begin() and komp_timing_end(), every launch made by this library on the calling process is
  * issued with hipExtLaunchKernel start/stop events, which the runtime stamps with the dispatch's own begin and end.
  * komp_timing_end() waits for those events and returns, per kernel kind, the summed dispatch time in milliseconds and
- * the dispatch count.  Kinds: 0 quant_q8_0, 1 quant_q8_K, 2 q4_0_gemv, 3 tq2_0_gemv, 4 probes (arrays of length 5).
+ * the dispatch count.  Kinds: 0 quant_q8_0, 1 quant_q8_K, 2 q4_0 GEMV / GEMM, 3 tq2_0 GEMV / GEMM, 4 probes and
+ * weight splits (arrays of length 5).
  * max_dispatches bounds the events created. */
 #define KOMP_TIMING_KINDS 5
 int komp_timing_begin(int64_t max_dispatches);

@@ -149,3 +149,33 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_abi, "LIB_PATH", str(tmp_path / "libkomp_hip.so"))
     with pytest.raises(_abi.KompError, match="not built"):
         _abi.lib()
+
+
+@pytest.mark.parametrize("fn,blk,row", [("komp_q4_0_split", 32, 16), ("komp_tq2_0_split", 256, 64)])
+def test_split_rejects_bad_arguments(fn, blk, row):
+    lib = _abi.lib()
+    f = getattr(lib, fn)
+    p = ctypes.c_void_p(256)
+    assert f(p, p, p, 4, 3 * blk + 1, 3 * row, None) == _abi.KOMP_EINVAL and "multiple" in _abi.last_error()
+    assert f(p, p, p, 4, 3 * blk, 3 * row - 16, None) == _abi.KOMP_EINVAL and "SW" in _abi.last_error()
+    assert f(p, p, p, 4, 3 * blk, 3 * row + 8, None) == _abi.KOMP_EINVAL and "SW" in _abi.last_error()
+    assert f(ctypes.c_void_p(258), p, p, 4, 3 * blk, 3 * row, None) == _abi.KOMP_EINVAL and "aligned" in _abi.last_error()
+    assert f(p, ctypes.c_void_p(264), p, 4, 3 * blk, 3 * row, None) == _abi.KOMP_EINVAL
+    assert f(p, p, ctypes.c_void_p(257), 4, 3 * blk, 3 * row, None) == _abi.KOMP_EINVAL
+    assert f(None, p, p, 4, 3 * blk, 3 * row, None) == _abi.KOMP_EINVAL
+    assert f(p, p, p, -1, 3 * blk, 3 * row, None) == _abi.KOMP_EINVAL
+    assert f(None, None, None, 0, 3 * blk, 0, None) == 0 and f(None, None, None, 5, 0, 16, None) == 0
+
+
+def test_gemm_rejects_bad_arguments():
+    lib = _abi.lib()
+    p = ctypes.c_void_p(256)
+    assert lib.komp_q4_0_gemm(p, p, p, p, p, None, 4, 8, 100, 64, None) == _abi.KOMP_EINVAL
+    assert lib.komp_tq2_0_gemm(p, p, p, p, p, None, 4, 8, 256, 48, None) == _abi.KOMP_EINVAL and "SW" in _abi.last_error()
+    assert lib.komp_q4_0_gemm(p, p, p, p, p, None, 4, 8, 1 << 26, 1 << 25, None) == _abi.KOMP_EINVAL
+    assert "limits" in _abi.last_error()
+    assert lib.komp_q4_0_gemm(p, p, p, p, p, None, 0, 8, 64, 32, None) == 0
+    rows, cols, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.komp_gemm_plan(0, 16, 4096, 4096, 2048, ctypes.byref(rows), ctypes.byref(cols), ctypes.byref(waves)) == 0
+    assert cols.value == 16 and waves.value == 8 and rows.value % 16 == 0
+    assert lib.komp_gemm_plan(2, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL
