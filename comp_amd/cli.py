@@ -4,13 +4,22 @@
     python -m comp_amd verify SPEC [k=v ...]   every config of the spec on the GPU vs KURN's exact references
     python -m comp_amd verify --all            the full verification set (dp4a, decode, both GEMVs, every mode)
 
-`gen`, `mix` and `fork` of the reference compile or inspect NVIDIA PTX/SASS and report the Triton fork; they have no
-counterpart on this build and exit 2.  `kurn check|verify SPEC` reaches this module through spec_command
-(comp_amd.kurn_ext registers it as KURN's backend for specs with `target triton`).
+    python -m comp_amd gen    SPEC [k=v ...] [-o DIR] [--emit hsaco,s]
+                                               the spec's GEMV and quantizer as built for gfx950: registers,
+                                               spills, approximate math, v_dot4c_i32_i8 in the hot loop, its
+                                               instruction mix; -o writes the code object and the kernel's ISA
+    python -m comp_amd mix    [--archs gfx950]  hot-loop instruction mixes of the GEMV configs (and the matrix-core
+                                               GEMM plans) of this build
+
+`gen` and `mix` read the gfx950 code objects inside this build's own library (comp_amd.isa), where the reference
+compiles Triton to PTX/SASS and reads those (src/komp/cli.py:88-158).  `fork` (the Triton fork) has no counterpart and
+exits 2.  `kurn check|gen|verify SPEC` reaches this module through spec_command (comp_amd.kurn_ext registers it as
+KURN's backend for specs with `target triton`).
 """
 
 from __future__ import annotations
 
+import os
 import sys
 
 USAGE = __doc__
@@ -75,17 +84,124 @@ def cmd_verify(args):
         return 2
 
 
+# GEMV configs listed by `mix` (block_n, nb, num_warps), the reference's set (src/komp/cli.py:136)
+MIX_KOMP = {"q4_0": ((64, 4, 4), (32, 8, 4)), "tq2_0": ((64, 1, 4), (32, 2, 4))}
+VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64}  # weights per 16-byte weight load
+
+
+def _gemv_kernel(fmt, mode, nb, m=1):
+    """The gemv_kernel instantiation a launch of this config runs: <format, mode, columns per launch, nb, fused>."""
+    return f"gemv_impl::gemv_kernel<{0 if fmt == 'q4_0' else 1}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
+
+
+def _mix_line(r, name):
+    lp = r["loop"]
+    return (f"{name:34} hot loop {r['loop_len']:4} insts / {r['values_per_thread']:5.0f} weights per thread: "
+            f"{r['insts_per_value']:.2f} insts, {r['int_per_value']:.2f} int, {r['dot4_per_value']:.3f} v_dot4c per "
+            f"weight; loads 128-bit {lp.get('ld128', 0)}, 64-bit {lp.get('ld64', 0)}, 32-bit {lp.get('ld32', 0)}, "
+            f"16-bit {lp.get('ld16', 0)}, 8-bit {lp.get('ld8', 0)}; LDS {lp.get('lds', 0)}")  # fmt: skip
+
+
+def _regs(r):
+    return (f"vgpr={r['vgpr']} agpr={r['agpr']} sgpr={r['sgpr']} lds={r['lds']} spill={r['vgpr_spill'] + r['sgpr_spill']} "
+            f"scratch={r['scratch']} approx-ops={','.join(r['approx']) or 'none'}")  # fmt: skip
+
+
+def cmd_gen(args):
+    from . import isa
+    from .spec import SpecError
+
+    try:
+        spec, base, tune = _spec(args)
+        c = spec.resolve(base)
+    except (SpecError, OSError) as e:
+        print(f"komp gen: {e}", file=sys.stderr)
+        return 2
+    if c["arch"] != "gfx950":
+        print(f"komp gen: arch {c['arch']}: this build holds gfx950 code only", file=sys.stderr)
+        return 2
+    out = args[args.index("-o") + 1] if "-o" in args else None
+    emit = (args[args.index("--emit") + 1] if "--emit" in args else "hsaco,s").split(",")
+    mode = spec.MODE[c["mode"]]
+    fmt = c["weights"]
+    quant = "quant_q8_0" if fmt == "q4_0" else "quant_q8_K"
+    try:
+        r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1)), VALUES_PER_LOAD[fmt], keep=out is not None)
+        q = isa.summary(f"{quant}_kernel", 1, keep=out is not None)
+    except (OSError, RuntimeError, KeyError) as e:
+        print(f"komp gen: {e}", file=sys.stderr)
+        return 2
+    fails = 0
+    dots = r["loop"].get("dot4", 0)
+    bad = r["vgpr_spill"] or r["sgpr_spill"] or r["approx"] or (mode == 2 and not dots)
+    fails += bool(bad)
+    print(f"{'FAIL' if bad else 'ok  '} {c['kernel']} {c['arch']} {spec.label(c)}: {_regs(r)} "
+          f"v_dot4c_i32_i8={r['dot4_total']} in hot loop={dots}")  # fmt: skip
+    print("     " + _mix_line(r, f"{fmt} {c['mode']}"))
+    print(f"     kernel {r['kernel'].split('(')[0]} (block_n and num_warps are launch parameters on gfx950)")
+    qbad = q["vgpr_spill"] or q["sgpr_spill"] or q["approx"]
+    fails += bool(qbad)
+    print(f"{'FAIL' if qbad else 'ok  '} {quant} {c['arch']}: {_regs(q)}")
+    if out:
+        os.makedirs(out, exist_ok=True)
+        for name, res in ((c["kernel"], r), (quant, q)):
+            for e in emit:
+                path = os.path.join(out, f"{name}.{c['arch']}.{e}")
+                if e == "hsaco":
+                    with open(path, "wb") as fh:
+                        fh.write(res["code_object"])
+                elif e == "s":
+                    with open(path, "w") as fh:
+                        fh.write(f"; {res['kernel']}\n" + res["asm"])
+                else:
+                    print(f"komp gen: --emit {e}: one of hsaco, s", file=sys.stderr)
+                    return 2
+                print(f"     wrote {path}")
+    return 1 if fails else 0
+
+
+def cmd_mix(args):
+    from . import isa
+
+    archs = (args[args.index("--archs") + 1] if "--archs" in args else "gfx950").split(",")
+    fails = 0
+    for arch in archs:
+        print(f"== {arch}")
+        if arch != "gfx950":
+            print(f"{arch}: not built (this build holds gfx950 code only)")
+            continue
+        for fmt in ("q4_0", "tq2_0"):
+            for bn, nb, nw in MIX_KOMP[fmt]:
+                for mode in (0, 2):
+                    r = isa.summary(_gemv_kernel(fmt, mode, nb), VALUES_PER_LOAD[fmt])
+                    spill = r["vgpr_spill"] + r["sgpr_spill"]
+                    fails += bool(spill or r["approx"])
+                    name = (f"KOMP {fmt} {'dp4a ' if mode else 'bytes'} {bn}/{nb}/{nw}w v{r['vgpr']}"
+                            + (" SPILL" if spill else ""))  # fmt: skip
+                    print(_mix_line(r, name))
+            print(f"KURN-CUDA {fmt}: not available (NVIDIA target; this build holds gfx950 code only)")
+        for prefix, label in (("gemm_impl::gemm_kernel<0, 8, 1, 1, 1, 2, false>", "GEMM q4_0 16 rows x 16 cols"),
+                              ("gemm_impl::gemm_kernel<0, 8, 1, 1, 4, 2, false>", "GEMM q4_0 16 rows x 64 cols"),
+                              ("gemm_impl::gemm_kernel<1, 8, 1, 1, 1, 2, false>", "GEMM tq2_0 16 rows x 16 cols")):
+            r = isa.summary(prefix, 1)
+            lp = r["loop"]
+            spill = r["vgpr_spill"] + r["sgpr_spill"]
+            fails += bool(spill or r["approx"])
+            print(f"{label:34} hot loop {r['loop_len']:4} insts: v_mfma {lp.get('mfma', 0)}, VALU {lp.get('valu', 0)}, "
+                  f"loads 128-bit {lp.get('ld128', 0)}, 32-bit {lp.get('ld32', 0)}, LDS {lp.get('lds', 0)}; v{r['vgpr']}"
+                  + (" SPILL" if spill else ""))  # fmt: skip
+    return 1 if fails else 0
+
+
 def _unavailable(name):
     def cmd(_args):
-        print(f"komp {name}: not available on the gfx950 build (it compiles or inspects NVIDIA PTX/SASS or reports the "
-              f"Triton fork)", file=sys.stderr)  # fmt: skip
+        print(f"komp {name}: not available on the gfx950 build (it reports the Triton fork)", file=sys.stderr)
         return 2
 
     return cmd
 
 
-COMMANDS = {"check": cmd_check, "verify": cmd_verify, "gen": _unavailable("gen"), "mix": _unavailable("mix"),
-            "fork": _unavailable("fork")}  # fmt: skip
+COMMANDS = {"check": cmd_check, "verify": cmd_verify, "gen": cmd_gen, "mix": cmd_mix, "fork": _unavailable("fork")}
 
 
 def main(argv=None):
@@ -98,8 +214,8 @@ def main(argv=None):
 
 def spec_command(cmd, argv):
     """Entry for kurn.hooks.TARGET_BACKENDS["triton"] (src/komp/cli.py:195-200)."""
-    if cmd not in ("check", "verify"):
-        print(f"kurn {cmd}: not available for target triton on the gfx950 build (komp supports check, verify)",
+    if cmd not in ("check", "gen", "verify"):
+        print(f"kurn {cmd}: not available for target triton on the gfx950 build (komp supports check, gen, verify)",
               file=sys.stderr)  # fmt: skip
         return 2
     return main([cmd, *argv])

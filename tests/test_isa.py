@@ -1,0 +1,77 @@
+"""`komp gen` / `komp mix` on the gfx950 build (no GPU needed): the code objects inside the built library, their
+register and spill metadata, approximate math, and hot-loop instruction mixes; the ISA reader's loop and class logic
+on synthetic instruction lists."""
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+from comp_amd import cli, isa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SPEC_Q4 = os.path.join(ROOT, "comp_amd", "examples", "q4_0_gemv.kurn")
+SPEC_TQ2 = os.path.join(ROOT, "comp_amd", "examples", "tq2_0_gemv.kurn")
+
+
+def run(*args):
+    return subprocess.run([sys.executable, "-m", "comp_amd", *args], capture_output=True, text=True, cwd=ROOT)
+
+
+def test_library_holds_gfx950_code_objects_with_every_kernel_family():
+    names = [n for co in isa.library_code_objects() for n in co.kernels]
+    for family in ("gemv_impl::gemv_kernel<", "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel",
+                   "split_impl::split_kernel"):
+        assert any(family in n for n in names), family
+
+
+@pytest.mark.parametrize("spec,fmt", [(SPEC_Q4, "q4_0"), (SPEC_TQ2, "tq2_0")])
+def test_gen_reports_and_writes(spec, fmt, tmp_path):
+    r = run("gen", spec, "-o", str(tmp_path))
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = r.stdout.splitlines()
+    assert lines[0].startswith("ok   ") and "spill=0" in lines[0] and "approx-ops=none" in lines[0]
+    hot = int(lines[0].rsplit("in hot loop=", 1)[1])
+    assert hot > 0  # dp4a mode: v_dot4c_i32_i8 in the hot loop
+    assert any(ln.startswith("ok   quant_q8_") for ln in lines)
+    files = sorted(os.listdir(tmp_path))
+    assert len(files) == 4 and all(f.endswith((".hsaco", ".s")) for f in files)
+    for f in files:
+        data = open(tmp_path / f, "rb").read()
+        if f.endswith(".hsaco"):
+            assert data[:4] == b"\x7fELF"
+    asm = open(tmp_path / [f for f in files if f.endswith(".s") and "gemv" in f][0]).read()
+    assert "v_dot4c_i32_i8" in asm and "s_endpgm" in asm
+
+
+def test_gen_bytes_mode_has_no_dot4_and_rejects_other_archs():
+    r = run("gen", SPEC_Q4, "mode=bytes")
+    assert r.returncode == 0 and "in hot loop=0" in r.stdout.splitlines()[0]
+    assert run("gen", SPEC_Q4, "arch=sm_80").returncode == 2
+
+
+def test_mix_lists_every_config():
+    r = run("mix")
+    assert r.returncode == 0, r.stdout + r.stderr
+    for fmt, cfgs in cli.MIX_KOMP.items():
+        for bn, nb, nw in cfgs:
+            for mode in ("bytes", "dp4a "):
+                assert f"KOMP {fmt} {mode} {bn}/{nb}/{nw}w" in r.stdout
+    assert "GEMM q4_0 16 rows x 64 cols" in r.stdout and "v_mfma 64" in r.stdout
+    assert run("mix", "--archs", "sm_80").stdout.count("not built") == 1
+
+
+def test_loops_classes_and_approx_on_synthetic_code():
+    insts = [(0x100, "s_mov_b32", "s0, 0", None), (0x104, "global_load_dwordx4", "v[0:3]", None),
+             (0x10C, "v_dot4c_i32_i8", "v4, v0, v1", None), (0x110, "v_and_b32", "v1, v2, v3", None),
+             (0x114, "s_cbranch_scc1", "-4", 0x104), (0x118, "s_branch", "2", 0x120), (0x11C, "s_nop", "0", None),
+             (0x120, "s_endpgm", "", None)]  # fmt: skip
+    assert isa.loops(insts) == [(1, 4)]
+    c = isa.mix(insts, 1, 4)
+    assert c["ld128"] == 1 and c["dot4"] == 1 and c["int"] == 2 and c["insts"] == 4
+    rcp = [(0, "v_rcp_f32", "", None), (4, "v_div_fixup_f32", "", None)]
+    assert isa.approx_ops(rcp) == [] and isa.approx_ops(rcp[:1]) == ["v_rcp_f32"]
+    assert isa.approx_ops([(0, "v_exp_f32", "", None)]) == ["v_exp_f32"]
+    assert isa.classify("buffer_load_ushort") == "ld16" and isa.classify("ds_read_b128") == "lds"
+    assert isa.classify("v_mfma_i32_16x16x32_i8") == "mfma"
