@@ -44,17 +44,20 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 TRAFFIC_FUSED_BITNET_M1 = 4882640
 
 
+# (values per weight block, weight bytes per block, values per activation block) of each weight format
+BLOCKS = {"q4_0": (32, 18, 32), "tq2_0": (256, 66, 256), "q8_0": (32, 34, 32), "iq4_nl": (32, 18, 32)}
+
+
 def gemv_bytes(fmt, n, k, m):
     """Algorithmic HBM bytes of one GEMV call: weights (quant + scale planes), q8 activations, f32 outputs."""
-    if fmt == "q4_0":
-        return n * k * 18 // 32 + m * (k + 4 * k // 32) + 4 * m * n
-    return n * k * 66 // 256 + m * (k + 4 * k // 256) + 4 * m * n
+    blk, nbytes, ablk = BLOCKS[fmt]
+    return n * k * nbytes // blk + m * (k + 4 * k // ablk) + 4 * m * n
 
 
 def quant_bytes(fmt, k, m):
     """Algorithmic bytes of one quantizer call: f32 read, int8 + f32 scale written (no bsums)."""
-    blk = 32 if fmt == "q4_0" else 256
-    return 4 * m * k + m * k + 4 * m * (k // blk)
+    ablk = BLOCKS[fmt][2]
+    return 4 * m * k + m * k + 4 * m * (k // ablk)
 
 
 # ---------------------------------------------------------------------------------------------------------------------
@@ -89,8 +92,35 @@ def q4_0_weights(n, k, gen, torch):
     return wq, ws
 
 
+def q8_0_weights(n, k, gen, torch):
+    """Split planes of Q8_0 weights: W ~ N(0, 0.02), d = max |w| / 127 per block, q = round(w / d)."""
+    nb = k // 32
+    w = torch.randn((n, nb, 32), generator=gen, device="cuda") * 0.02
+    d = w.abs().amax(dim=2, keepdim=True) / 127.0
+    q = torch.round(w / torch.where(d > 0, d, torch.ones_like(d))).clamp(-127, 127).to(torch.int8)
+    return q.view(torch.uint8).reshape(n, nb * 32).contiguous(), d[:, :, 0].half().view(torch.int16).contiguous()
+
+
+IQ4_NL_VALUES = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
+
+
+def iq4_nl_weights(n, k, gen, torch):
+    """Split planes of IQ4_NL weights: W ~ N(0, 0.02), d = max |w| / 127 per block, each value the nearest entry of
+    the IQ4_NL table to w / d (index i of value i in the low nibble of byte i, value i + 16 in the high nibble)."""
+    nb = k // 32
+    w = torch.randn((n, nb, 32), generator=gen, device="cuda") * 0.02
+    d = w.abs().amax(dim=2, keepdim=True) / 127.0
+    t = torch.tensor(IQ4_NL_VALUES, dtype=torch.float32, device="cuda")
+    q = torch.bucketize(w / torch.where(d > 0, d, torch.ones_like(d)), (t[1:] + t[:-1]) / 2).to(torch.uint8)
+    wq = (q[:, :, :16] | (q[:, :, 16:] << 4)).reshape(n, nb * 16).contiguous()
+    return wq, d[:, :, 0].half().view(torch.int16).contiguous()
+
+
+WEIGHTS = {"q4_0": q4_0_weights, "tq2_0": tq2_0_weights, "q8_0": q8_0_weights, "iq4_nl": iq4_nl_weights}
+
+
 def weight_copies(fmt, n, k, gen, torch, total=COLD_BYTES):
-    make = q4_0_weights if fmt == "q4_0" else tq2_0_weights
+    make = WEIGHTS[fmt]
     wq, ws = make(n, k, gen, torch)
     per = wq.numel() + 2 * ws.numel()
     copies = max(2, math.ceil(total / per))
@@ -152,8 +182,8 @@ def dispatch_times(abi, torch, step, count):
 
 def step_bytes_fused(fmt, n, k, m):
     """Algorithmic bytes of one quantize-and-GEMV: weights, f32 activations in, f32 outputs."""
-    wb = n * k * 18 // 32 if fmt == "q4_0" else n * k * 66 // 256
-    return wb + 4 * m * k + 4 * m * n
+    blk, nbytes, _ = BLOCKS[fmt]
+    return n * k * nbytes // blk + 4 * m * k + 4 * m * n
 
 
 def headline(torch, host, abi, args):
@@ -276,7 +306,9 @@ DETAIL_SHAPES = (  # (fmt, n, k, m)
     ("q4_0", 4096, 4096, 1), ("q4_0", 6144, 4096, 1), ("q4_0", 28672, 4096, 1), ("q4_0", 4096, 14336, 1),
     ("q4_0", 4096, 14336, 3), ("q4_0", 128256, 4096, 1), ("q4_0", 28672, 8192, 1), ("tq2_0", 6912, 2560, 1),
     ("tq2_0", 2560, 6912, 1), ("tq2_0", 6912, 2560, 3), ("tq2_0", 32768, 8192, 1), ("q4_0", 4097, 4192, 1),
-    ("tq2_0", 6913, 2816, 1),
+    ("tq2_0", 6913, 2816, 1), ("q8_0", 4096, 4096, 1), ("q8_0", 14336, 4096, 1), ("q8_0", 4096, 14336, 1),
+    ("q8_0", 128256, 4096, 1), ("iq4_nl", 4096, 4096, 1), ("iq4_nl", 14336, 4096, 1), ("iq4_nl", 4096, 14336, 1),
+    ("iq4_nl", 28672, 8192, 1),
 )  # fmt: skip
 
 
@@ -300,7 +332,7 @@ def detail(torch, host, abi, args):
         reps = 4 * per_graph
         ms, _ = timed_steps(torch, call, nc, reps, per_graph)
         disp = dispatch_times(abi, torch, call, min(reps, 256))
-        kind = "q4_0_gemv" if fmt == "q4_0" else "tq2_0_gemv"
+        kind = f"{fmt}_gemv"
         d_us = disp[kind][0] * 1e3 / disp[kind][1]
         b = gemv_bytes(fmt, n, k, m)
         us = ms * 1e3 / reps
@@ -328,7 +360,7 @@ def multi_detail(torch, host, args):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed + 2)
     for name, fmt, ns, k in MULTI_CASES:
-        make = q4_0_weights if fmt == "q4_0" else tq2_0_weights
+        make = WEIGHTS[fmt]
         per = sum(gemv_bytes(fmt, n, k, 0) for n in ns)
         ncopy = max(2, math.ceil((COLD_BYTES // 2) / per))
         base = [make(n, k, gen, torch) for n in ns]
@@ -354,7 +386,7 @@ def multi_detail(torch, host, args):
         rel = max(float((a - b).abs().max() / b.abs().max()) for a, b in zip(ys, ys1))
         if rel > 1e-6:
             raise RuntimeError(f"{name}: multi-matrix and single launches differ by {rel:.2e} (relative)")
-        b = sum(n * k * (18 if fmt == "q4_0" else 66) // (32 if fmt == "q4_0" else 256) for n in ns) + 4 * k + 4 * sum(ns)
+        b = sum(n * k * BLOCKS[fmt][1] // BLOCKS[fmt][0] for n in ns) + 4 * k + 4 * sum(ns)
         us_m, us_s = ms_m * 1e3 / reps, ms_s * 1e3 / reps
         rows.append({"case": name, "fmt": fmt, "rows": list(ns), "k": k, "bytes": b, "us_multi": round(us_m, 3),
                      "us_singles": round(us_s, 3), "launches_singles": len(ns), "speedup": round(us_s / us_m, 3),
@@ -370,6 +402,8 @@ BATCH_CASES = (  # (name, fmt, N, K): decode projections, several tokens at once
     ("llama3_8b_ffn_down", "q4_0", 4096, 14336),
     ("bitnet2b_ffn_gate", "tq2_0", 6912, 2560),
     ("bitnet2b_ffn_down", "tq2_0", 2560, 6912),
+    ("llama3_8b_ffn_gate", "q8_0", 14336, 4096),
+    ("llama3_8b_ffn_gate", "iq4_nl", 14336, 4096),
 )
 BATCH_M = (4, 16, 64)
 
@@ -426,6 +460,7 @@ def batched_detail(torch, host, args):
 INGEST_CASES = (  # (name, fmt, N, K): one weight matrix's ggml block bytes, split on the device
     ("llama3_8b_ffn_gate", "q4_0", 14336, 4096),
     ("llama3_8b_lm_head", "q4_0", 128256, 4096),
+    ("llama3_8b_ffn_gate", "q8_0", 14336, 4096),
     ("bitnet2b_ffn_gate", "tq2_0", 6912, 2560),
 )
 

@@ -109,8 +109,8 @@ int device_cus() {
 }
 
 GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t k) {
-  const int bpb = fmt == FMT_Q4_0 ? 1 : 4;              // 16-byte chunks per block
-  const int64_t nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
+  const int bpb = fmt_info(fmt).qbytes / 16;            // 16-byte chunks per block
+  const int64_t nblk = k / fmt_info(fmt).block;
   const int64_t chunks = nblk * bpb;                      // 16-byte chunks per row
   if (n >= 16384) {
     if (fmt == FMT_TQ2_0) return plan_of(32, 2, 8, 16, 1);  // 16 lanes per row, 4 rows per wave, steps of 8 blocks
@@ -138,7 +138,7 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   const int64_t blocks_per_slot = lpr / bpb;
   int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
   nb = nb < 1 ? 1 : (nb > 16 ? 16 : nb);
-  if (fmt == FMT_Q4_0 && nb > 4) nb = 4;
+  if (fmt != FMT_TQ2_0 && nb > 4) nb = 4;
   int w = 8;
   const int rpw = 64 / lpr;
   while (w * rpw > 128) w >>= 1;
@@ -181,7 +181,7 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
   const double r = static_cast<double>((n + 15) / 16) * groups / device_cus();
   GemmPlan q = {8, 1, 1, cn, 2};
   if (r > 8.0)
-    q = cn == 1 ? GemmPlan{1, 8, m > 8 ? 2 : 1, 1, 2} : GemmPlan{1, 8, 1, cn, cn == 2 ? 2 : 1};
+    q = cn == 1 ? GemmPlan{1, 8, m > 8 && fmt != FMT_Q8_0 ? 2 : 1, 1, 2} : GemmPlan{1, 8, 1, cn, cn == 2 ? 2 : 1};
   else if (r > 2.0)
     q = cn == 1 ? GemmPlan{4, 2, 2, 1, 4} : GemmPlan{2, 4, 1, cn, 2};
   else if (r > 1.25 && cn > 1)
@@ -217,8 +217,9 @@ struct GemvArgs {
 
 int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t M, int64_t K, int block_n, int nb,
                int mode, int num_warps, void* stream, int route = kRouteAuto) {
-  const int blk = fmt == FMT_Q4_0 ? 32 : 256;
-  const int64_t row_bytes = fmt == FMT_Q4_0 ? K / 2 : K / 4;
+  const FmtInfo fi = fmt_info(fmt);
+  const int blk = fi.block;
+  const int64_t row_bytes = K / blk * fi.qbytes;
   if (a.count < 1 || a.count > kMaxSegs || a.mats == nullptr)
     return fail(KOMP_EINVAL, "%s: count=%d must be 1..%d", name, a.count, kMaxSegs);
   if (M < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (M=%lld K=%lld)", name, (long long)M, (long long)K);
@@ -240,8 +241,8 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
     if (!in_set(num_warps, kWarps, 4)) return fail(KOMP_EINVAL, "%s: num_warps=%d not in {1,2,4,8}", name, num_warps);
   }
-  if (fused && fmt == FMT_Q4_0 && a.xb_out != nullptr)
-    return fail(KOMP_EINVAL, "%s: XB (bsums) is a q8_K plane; pass NULL for q4_0", name);
+  if (fused && fmt != FMT_TQ2_0 && a.xb_out != nullptr)
+    return fail(KOMP_EINVAL, "%s: XB (bsums) is a q8_K plane; pass NULL for q8_0 activations", name);
   if (fused && a.xq_out == nullptr && (a.xd_out != nullptr || a.xb_out != nullptr))
     return fail(KOMP_EINVAL, "%s: XD / XB outputs need XQ as well", name);
   if (fused && a.xq_out != nullptr && a.xd_out == nullptr)
@@ -341,7 +342,9 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
 int gemv_multi_entry(int fmt, int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
                      const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X, int64_t M,
                      int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
-  const char* name = fmt == FMT_Q4_0 ? "komp_q4_0_gemv_multi" : "komp_tq2_0_gemv_multi";
+  static const char* const names[] = {"komp_q4_0_gemv_multi", "komp_tq2_0_gemv_multi", "komp_q8_0_gemv_multi",
+                                      "komp_iq4_nl_gemv_multi"};
+  const char* name = names[fmt];
   if (count < 1 || count > kMaxSegs) return fail(KOMP_EINVAL, "%s: count=%d must be 1..%d", name, count, kMaxSegs);
   if (WQ == nullptr || WS == nullptr || Y == nullptr || N == nullptr || SW == nullptr)
     return fail(KOMP_EINVAL, "%s: the WQ, WS, Y, N and SW arrays must not be NULL", name);
@@ -443,8 +446,8 @@ int komp_tq2_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, fl
 namespace {
 int split_entry(int fmt, const char* name, const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K,
                 int64_t SW, void* stream) {
-  const int blk = fmt == FMT_Q4_0 ? 32 : 256;
-  const int64_t qbytes = fmt == FMT_Q4_0 ? 16 : 64;
+  const int blk = fmt_info(fmt).block;
+  const int64_t qbytes = fmt_info(fmt).qbytes;
   if (N < 0 || K < 0) return fail(KOMP_EINVAL, "%s: negative size (N=%lld K=%lld)", name, (long long)N, (long long)K);
   if (K % blk) return fail(KOMP_EINVAL, "%s: K=%lld is not a multiple of the %d-value block", name, (long long)K, blk);
   if (K > INT32_MAX) return fail(KOMP_EINVAL, "%s: K must be < 2^31", name);
@@ -484,7 +487,7 @@ int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, cons
 
 int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
                    int* waves) {
-  if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemm_plan: fmt=%d", fmt);
+  if (fmt < FMT_Q4_0 || fmt > FMT_IQ4_NL) return fail(KOMP_EINVAL, "komp_gemm_plan: fmt=%d", fmt);
   if (M < 1 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemm_plan: bad argument");
   GemmPlan p;
   if (!gemm_plan(fmt, M < kGemmMaxCols ? M : kGemmMaxCols, N, K, SW, &p))
@@ -507,9 +510,44 @@ int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* co
   return gemv_multi_entry(FMT_TQ2_0, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);
 }
 
+// ---- Q8_0 and IQ4_NL (q8_0 activations): the same entries as Q4_0's ----
+#define KOMP_FORMAT_ENTRIES(F, FMT)                                                                                   \
+  int komp_##F##_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,  \
+                      int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,      \
+                      void* stream) {                                                                                 \
+    const GemvMat w{WQ, WS, Y, S, N, SW};                                                                             \
+    const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};                                              \
+    return gemv_entry(FMT, false, "komp_" #F "_gemv", a, M, K, block_n, nb, mode, num_warps, stream);               \
+  }                                                                                                                   \
+  int komp_##F##_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,     \
+                          float* XD, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode,      \
+                          int num_warps, void* stream) {                                                              \
+    const GemvMat w{WQ, WS, Y, S, N, SW};                                                                             \
+    const GemvArgs a{&w, 1, nullptr, nullptr, X, XQ, XD, nullptr};                                                    \
+    return gemv_entry(FMT, true, "komp_" #F "_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);            \
+  }                                                                                                                   \
+  int komp_##F##_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,           \
+                            const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,   \
+                            int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {       \
+    return gemv_multi_entry(FMT, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);   \
+  }                                                                                                                   \
+  int komp_##F##_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,  \
+                      int64_t M, int64_t N, int64_t K, int64_t SW, void* stream) {                                    \
+    const GemvMat w{WQ, WS, Y, S, N, SW};                                                                             \
+    const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};                                              \
+    return gemv_entry(FMT, false, "komp_" #F "_gemm", a, M, K, 0, 0, KOMP_MODE_DP4A, 0, stream, kRouteGemm);        \
+  }                                                                                                                   \
+  int komp_##F##_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream) {  \
+    return split_entry(FMT, "komp_" #F "_split", W, WQ, WS, N, K, SW, stream);                                        \
+  }
+
+KOMP_FORMAT_ENTRIES(q8_0, FMT_Q8_0)
+KOMP_FORMAT_ENTRIES(iq4_nl, FMT_IQ4_NL)
+#undef KOMP_FORMAT_ENTRIES
+
 int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
                           int* num_warps, int* lanes_per_row, int* passes) {
-  if (fmt != FMT_Q4_0 && fmt != FMT_TQ2_0) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
+  if (fmt < FMT_Q4_0 || fmt > FMT_IQ4_NL) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
   if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A)
     return fail(KOMP_EINVAL, "komp_gemv_auto_config: mode=%d not in {0,1,2}", mode);
   if (M < 1 || N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)

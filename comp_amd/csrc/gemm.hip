@@ -1,5 +1,5 @@
-// Batched-column GEMMs on the gfx950 matrix cores: Q4_0 x q8_0 and TQ2_0 x q8_K for any number M of activation
-// columns, with the decode GEMVs' result definition (src/komp/kernels.py:48-94 and :97-142):
+// Batched-column GEMMs on the gfx950 matrix cores: Q4_0, Q8_0 and IQ4_NL x q8_0, TQ2_0 x q8_K, for any number M of
+// activation columns, with the decode GEMVs' result definition (src/komp/kernels.py:48-94 and :97-142):
 //   Y[m][n] = sum_b d_w(n, b) * d_x(m, b) * s(m, n, b),  s = the exact int32 dot of weight block b of row n with
 //   activation block b of column m,
 // and the same optional S [M][N][K/block] of exact block dots.  The GEMVs stream the weights once per 1..3 columns;
@@ -21,6 +21,10 @@
 //          values 4g..4g+3 (low nibbles) and 16+4g..16+4g+3 (high nibbles), so A = {w & 0x0F0F0F0F, (w >> 4) &
 //          0x0F0F0F0F}.  The activations are loaded the same way (32 bytes of block 4s+g of column r in group g) and
 //          transposed into B = {x[4g..4g+3], x[16+4g..16+4g+3]}.
+//   Q8_0   a step is 2 blocks of 32 int8; group g holds half g%2 of block g/2, and the same transpose leaves dword g
+//          of each half of each block in group g: A = {w0, w1} as loaded, no offset.
+//   IQ4_NL Q4_0's byte layout; the nibbles go through ggml's 16-entry value table (two v_perm_b32 and a byte
+//          select per dword), which gives signed values: no offset.
 //   TQ2_0  group g holds bytes 16g..16g+15 of the block; crumb j of byte 16g+e is value (g/2)*128 + 32j + 16(g%2) + e
 //          (kernels.py:102), so B for crumb j is 16 contiguous activation bytes and nothing is transposed.
 // Nibbles and crumbs go in unsigned (0..15, 0..2).  Their offset (-8, resp. -1, times the block's activation sum)
@@ -96,9 +100,13 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
             float* __restrict__ Y, int32_t* __restrict__ S) {
   // ss: row stride of the f32 scale slab in LDS, nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four
   // scales of a row with one 16-byte LDS load).
-  constexpr bool Q4 = FMT == FMT_Q4_0;
+  constexpr bool NIB4 = FMT == FMT_Q4_0 || FMT == FMT_IQ4_NL;  // 16 nibble bytes per 32-value block
+  constexpr bool Q8 = FMT == FMT_Q8_0;                           // 32 int8 bytes per 32-value block
+  constexpr bool BLK32 = NIB4 || Q8;                             // the 32-value blocks (q8_0 activations)
+  constexpr bool TQ2 = FMT == FMT_TQ2_0;
+  constexpr int BPS = NIB4 ? 4 : (Q8 ? 2 : 1);                   // blocks per 64-byte K step
   constexpr int W = WK * WR;
-  constexpr int XV = Q4 ? 2 : 4;        // 16-byte activation loads per column tile per step
+  constexpr int XV = NIB4 ? 2 : (Q8 ? 1 : 4);                    // 16-byte activation loads per column tile per step
   constexpr int WGR = 16 * WN * WR;     // rows per workgroup
   constexpr int RPW = WGR / W;          // slab rows each wave stages
   static_assert(RPW >= 1 && RPW * W == WGR, "the waves split the workgroup's rows evenly");
@@ -124,33 +132,34 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
   unsigned va[WN];
 #pragma unroll
   for (int t = 0; t < WN; ++t) va[t] = static_cast<unsigned>((16 * t + r16) * SW + 16 * g);
-  // Q4_0 activations: load v of column c takes bytes 64v + 16g .. +15 of the step (64 contiguous bytes per column per
-  // load); after the dword transpose these are exactly the B halves of blocks 2v and 2v + 1 (see compute).
+  // 32-value blocks: load v of column c takes bytes 64v + 16g .. +15 of the step's activations (64 contiguous bytes
+  // per column per load); after the dword transpose these are exactly the B halves of blocks 2v and 2v + 1 (see
+  // compute).  d_x: row group g loads block BPS*s + g's (Q8_0: + g % 2).
   unsigned vx[CN], vd[CN];
 #pragma unroll
   for (int u = 0; u < CN; ++u) {
     const int c = 16 * u + r16;
-    vx[u] = static_cast<unsigned>(Q4 ? c * K + 16 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
-    vd[u] = static_cast<unsigned>(c * nblk * 4 + (Q4 ? 4 * g : 0));
+    vx[u] = static_cast<unsigned>(BLK32 ? c * K + 16 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
+    vd[u] = static_cast<unsigned>(c * nblk * 4 + (NIB4 ? 4 * g : (Q8 ? 4 * (g & 1) : 0)));
   }
 
   struct Step {
     u32x4 a[WN];
     u32x4 x[CN][XV];
-    float dx[CN];  // Q4_0: d_x of block 4s+g (row group g's own block); TQ2_0: d_x of block s
+    float dx[CN];  // 32-value blocks: d_x of row group g's block of the step; TQ2_0: d_x of block s
   };
   auto load = [&](Step& st, int s) {
     const bool sv = s < nsteps;  // wave-uniform
     const unsigned sa = sv ? 64u * s : kOob;
-    const unsigned sx = sv ? (Q4 ? 128u : 256u) * s : kOob;
-    const unsigned sd = sv ? (Q4 ? 16u : 4u) * s : kOob;
+    const unsigned sx = sv ? (32u * BPS * (TQ2 ? 8u : 1u)) * s : kOob;  // activation bytes per step
+    const unsigned sd = sv ? 4u * BPS * s : kOob;
 #pragma unroll
     for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t], sa, 2);  // nt: read once
 #pragma unroll
     for (int u = 0; u < CN; ++u) {
 #pragma unroll
       for (int v = 0; v < XV; ++v)
-        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (Q4 ? 64 * v : 32 * v), sx, 0);
+        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (BLK32 ? 64 * v : 32 * v), sx, 0);
       st.dx[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u], sd, 0));
     }
   };
@@ -210,43 +219,67 @@ gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const
   };
 
   auto compute = [&](const Step& st, int s) {
-    if constexpr (Q4) {
-      // weights: row group g holds block 4s+g; after the transpose ta[t][j] (row group g) is dword g of block 4s+j.
+    if constexpr (BLK32) {
+      // weights (Q4_0, IQ4_NL): row group g holds block 4s+g; after the transpose ta[t][j] (row group g) is dword g of
+      // block 4s+j.  Q8_0: row group g holds half g%2 of block 2s + g/2; after the transpose ta[t][2j + h] (row group
+      // g) is dword g of half h of block 2s+j.
       // activations: load v, row group g holds dwords 0..3 of half g%2 of block 2v + g/2; after the transpose
       // xt[u][v][2i + h] (row group g) is dword g of half h of block 2v + i, i.e. xt[u][j / 2][2 (j % 2) + h] holds
-      // x[4g .. 4g+3] (h = 0) and x[16 + 4g .. 16 + 4g+3] (h = 1) of block 4s+j.
-      // d_x: row group g holds block 4s+g's; dxb[u][j] is block 4s+j's in every row group (row broadcasts).
-      unsigned ta[WN][4], xt[CN][2][4];
+      // x[4g .. 4g+3] (h = 0) and x[16 + 4g .. 16 + 4g+3] (h = 1) of the step's block j.
+      // d_x: row group g holds block BPS*s + g's (Q8_0: g % 2); dxb[u][j] is block j's in every row group.
+      unsigned ta[WN][4], xt[CN][XV][4];
       float dxb[CN][4];
 #pragma unroll
       for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
 #pragma unroll
       for (int u = 0; u < CN; ++u) {
-        transpose4(st.x[u][0], xt[u][0]);
-        transpose4(st.x[u][1], xt[u][1]);
+#pragma unroll
+        for (int v = 0; v < XV; ++v) transpose4(st.x[u][v], xt[u][v]);
         bcast_rows(st.dx[u], dxb[u]);
       }
-      f32x4 dw[WN][4];  // [t][r] = d_w of row 16t + 4g + r, blocks 4s .. 4s+3
+      float dw[WN][4][BPS];  // [t][r][j] = d_w of row 16t + 4g + r, block BPS*s + j
 #pragma unroll
       for (int t = 0; t < WN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dw[t][r] = *reinterpret_cast<const f32x4*>(slab + (16 * (WN * wr + t) + 4 * g + r) * ss + 4 * s);
+        for (int r = 0; r < 4; ++r) {
+          const float* row = slab + (16 * (WN * wr + t) + 4 * g + r) * ss + BPS * s;
+          if constexpr (BPS == 4) {
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(row);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int b = 4 * s + j;
+            for (int j = 0; j < 4; ++j) dw[t][r][j] = v4[j];
+          } else {
+            const float2 v2 = *reinterpret_cast<const float2*>(row);
+            dw[t][r][0] = v2.x;
+            dw[t][r][1] = v2.y;
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < BPS; ++j) {
+        const int b = BPS * s + j;
         if (b >= nblk) break;  // wave-uniform: the step's last blocks past K
         long bj[CN];
         i32x4 corr[CN];
 #pragma unroll
         for (int u = 0; u < CN; ++u) {
           bj[u] = pack2(xt[u][j >> 1][2 * (j & 1)], xt[u][j >> 1][2 * (j & 1) + 1]);
-          corr[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(0xF8F8F8F8F8F8F8F8ull), bj[u],
-                                                          i32x4{0, 0, 0, 0}, 0, 0, 0);
+          if constexpr (FMT == FMT_Q4_0)
+            corr[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(0xF8F8F8F8F8F8F8F8ull), bj[u],
+                                                            i32x4{0, 0, 0, 0}, 0, 0, 0);
+          else
+            corr[u] = i32x4{0, 0, 0, 0};  // signed weights: no offset
         }
 #pragma unroll
         for (int t = 0; t < WN; ++t) {
-          const long aj = pack2(ta[t][j] & NIB, (ta[t][j] >> 4) & NIB);
+          long aj;
+          if constexpr (FMT == FMT_Q4_0)
+            aj = pack2(ta[t][j] & NIB, (ta[t][j] >> 4) & NIB);
+          else if constexpr (FMT == FMT_IQ4_NL) {
+            unsigned lo, hi;
+            iq4_nl_lut(ta[t][j], lo, hi);
+            aj = pack2(lo, hi);
+          }
+          else
+            aj = pack2(ta[t][2 * j], ta[t][2 * j + 1]);
 #pragma unroll
           for (int u = 0; u < CN; ++u) {
             const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(aj, bj[u], corr[u], 0, 0, 0);
@@ -345,14 +378,14 @@ namespace {
 
 template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
 hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
-  const int blk = FMT == FMT_Q4_0 ? 32 : 256;
-  const int nblk = c.k / blk;
-  const int nsteps = FMT == FMT_Q4_0 ? (nblk + 3) / 4 : nblk;
+  const int nblk = c.k / fmt_info(FMT).block;
+  const int bps = FMT == FMT_TQ2_0 ? 1 : (FMT == FMT_Q8_0 ? 2 : 4);  // blocks per 64-byte K step
+  const int nsteps = (nblk + bps - 1) / bps;
   const dim3 grid((c.n + 16 * WN * WR - 1) / (16 * WN * WR), (c.m + 16 * CN - 1) / (16 * CN));
   const dim3 block(64 * WK * WR);
   const size_t lds = gemm_lds_bytes(FMT, p, c.k);
   auto kern = gemm_impl::gemm_kernel<FMT, WK, WR, WN, CN, D, STORE_S>;
-  const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
+  const Timing tm = timing_slot(gemv_kind(FMT));
   hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, nsteps,
                         gemm_impl::slab_stride(nblk), c.sw, c.wq, c.ws, c.xq, c.xd, c.y, c.s);
   return hipGetLastError();
@@ -381,7 +414,9 @@ hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) 
   KOMP_GEMM_PLAN(2, 4, 1, 3, 2)
   KOMP_GEMM_PLAN(2, 4, 1, 4, 2)
   KOMP_GEMM_PLAN(1, 8, 1, 1, 2)
-  KOMP_GEMM_PLAN(1, 8, 2, 1, 2)
+  if constexpr (FMT != FMT_Q8_0) {  // Q8_0's two row tiles a wave need more than 256 VGPRs (the plan never asks)
+    KOMP_GEMM_PLAN(1, 8, 2, 1, 2)
+  }
   KOMP_GEMM_PLAN(1, 8, 1, 2, 2)
   KOMP_GEMM_PLAN(1, 8, 1, 3, 1)
   KOMP_GEMM_PLAN(1, 8, 1, 4, 1)
@@ -392,14 +427,20 @@ hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) 
 }  // namespace
 
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k) {
-  const int nblk = k / (fmt == FMT_Q4_0 ? 32 : 256);
+  const int nblk = k / fmt_info(fmt).block;
   const size_t slab = (static_cast<size_t>(16) * p.wn * p.wr * gemm_impl::slab_stride(nblk) + 64) * 4;  // + spill slots
   const size_t red = p.wk > 1 ? static_cast<size_t>(p.wk) * p.wr * p.wn * p.cn * 4 * 64 * 4 : 0;
   return slab > red ? slab : red;
 }
 
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
-  return c.fmt == FMT_Q4_0 ? launch_fmt<FMT_Q4_0>(c, p, stream) : launch_fmt<FMT_TQ2_0>(c, p, stream);
+  switch (c.fmt) {
+    case FMT_Q4_0: return launch_fmt<FMT_Q4_0>(c, p, stream);
+    case FMT_TQ2_0: return launch_fmt<FMT_TQ2_0>(c, p, stream);
+    case FMT_Q8_0: return launch_fmt<FMT_Q8_0>(c, p, stream);
+    case FMT_IQ4_NL: return launch_fmt<FMT_IQ4_NL>(c, p, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace komp

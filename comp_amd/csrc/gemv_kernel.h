@@ -68,6 +68,42 @@ __device__ __forceinline__ int q4_0_block_dot(u32x4 w, u32x4 xl, u32x4 xh, int c
   }
 }
 
+// IQ4_NL: exact int32 dot of one block (16 quant bytes, Q4_0's nibble order) with its 32 activations; the nibbles
+// index ggml's value table (signed values, no offset).
+template <int MODE>
+__device__ __forceinline__ int iq4_nl_block_dot(u32x4 w, u32x4 xl, u32x4 xh) {
+  int s = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    unsigned lo, hi;
+    iq4_nl_lut(w[d], lo, hi);
+    if constexpr (MODE == MODE_BYTES) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += sbyte(lo, e) * sbyte(xl[d], e) + sbyte(hi, e) * sbyte(xh[d], e);
+    } else {
+      s = dot4<MODE>(lo, xl[d], s);
+      s = dot4<MODE>(hi, xh[d], s);
+    }
+  }
+  return s;
+}
+
+// Q8_0: partial int32 dot of one 16-byte chunk (16 int8 weights) with the 16 activations of the same half block.
+template <int MODE>
+__device__ __forceinline__ int q8_0_chunk_dot(u32x4 w, u32x4 x) {
+  int s = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (MODE == MODE_BYTES) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += sbyte(w[d], e) * sbyte(x[d], e);
+    } else {
+      s = dot4<MODE>(w[d], x[d], s);
+    }
+  }
+  return s;
+}
+
 // TQ2_0: partial int32 dot of one 16-byte chunk.  Byte t of the chunk holds, at bits 2j, the value whose activation
 // is byte t of x[j].  `init` joins the x1 accumulator.
 template <int MODE>
@@ -123,7 +159,9 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   // nseg > 1: several matrices sharing the input; the workgroup takes its matrix from segs (scalar compares on the
   // argument block) and from there on works as for one matrix, on its row range within it.
   extern __shared__ __align__(16) unsigned char lds[];
-  constexpr int BB = FMT == FMT_Q4_0 ? 16 : 64;  // quant bytes per block
+  constexpr bool BLK32 = FMT != FMT_TQ2_0;  // 32-value blocks with q8_0 activations (Q4_0, Q8_0, IQ4_NL)
+  constexpr int BB = FMT == FMT_TQ2_0 ? 64 : (FMT == FMT_Q8_0 ? 32 : 16);  // quant bytes per block
+  constexpr int CPB_LOG2 = FMT == FMT_TQ2_0 ? 2 : (FMT == FMT_Q8_0 ? 1 : 0);  // log2(16-byte chunks per block)
   int N = N1;
   int64_t SW = SW1;
   const uint8_t* __restrict__ WQ = WQ1;
@@ -153,13 +191,13 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   // this wave's rows inside the workgroup's (a plan may give the waves more row slots than the workgroup has rows)
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);  // wave-uniform, may be <= 0
-  const int bpg = FMT == FMT_Q4_0 ? lpr : (lpr >> 2);  // blocks a row group covers per chunk slot
+  const int bpg = lpr >> CPB_LOG2;                       // blocks a row group covers per chunk slot
   const int bstep = bpg * NB;                            // blocks a row group covers per K step
-  const int q = gl & 3;                                  // TQ2_0: chunk of the block this lane loads
-  const int gblk = FMT == FMT_Q4_0 ? gl : (gl >> 2);     // block offset of this lane within a slot
+  const int q = gl & ((1 << CPB_LOG2) - 1);              // Q8_0, TQ2_0: chunk of the block this lane loads
+  const int gblk = gl >> CPB_LOG2;                       // block offset of this lane within a slot
   const int tiles = passes * nsteps;
   // per-lane byte offsets within a row group's tile (row grp of the group, block gblk, chunk q)
-  const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + (FMT == FMT_Q4_0 ? 0 : q * 16);
+  const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + q * 16;
   const int64_t lane_s = static_cast<int64_t>(grp) * nblk + gblk;
 
   u32x4 w[NB];
@@ -195,8 +233,8 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   // Then (sc_mode 1) the scale slab [waves * rows_per_wave][nblk] (rows past the workgroup's are never loaded nor
   // used), 16-byte aligned (the activation bytes are a multiple of 8).
   u32x4* xv = reinterpret_cast<u32x4*>(lds);
-  int2* meta = reinterpret_cast<int2*>(xv + (FMT == FMT_Q4_0 ? 2 : 16) * MC * nblk);
-  u32x4* scs16 = xv + ((MC * nblk * (FMT == FMT_Q4_0 ? 40 : 264) + 15) >> 4);
+  int2* meta = reinterpret_cast<int2*>(xv + (BLK32 ? 2 : 16) * MC * nblk);
+  u32x4* scs16 = xv + ((MC * nblk * (BLK32 ? 40 : 264) + 15) >> 4);
   const int16_t* scs = reinterpret_cast<const int16_t*>(scs16);
 
   // Then the scale slab (sc_mode 1): each wave copies 1 KB pieces of it from global memory straight into LDS
@@ -221,7 +259,7 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   // iteration for every shape that fits LDS with 256+ lanes, and extra staging registers would cut the occupancy of
   // the weight stream, so they use SU = 1.
   constexpr int SU = FUSED ? 2 : 1;
-  if constexpr (FMT == FMT_Q4_0 && !FUSED) {
+  if constexpr (BLK32 && !FUSED) {
     const int total = MC * nblk;
     for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
       u32x4 a[SU], c[SU];
@@ -246,7 +284,7 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
           xv[i] = a[u];
           xv[MC * nblk + i] = c[u];
           int sum = 0;
-          if constexpr (MODE != MODE_BYTES) {
+          if constexpr (MODE != MODE_BYTES && FMT == FMT_Q4_0) {  // the -8 offset of the Q4_0 nibbles
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
               sum = dot4<MODE>(a[u][d], ONES, sum);
@@ -257,7 +295,7 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
         }
       }
     }
-  } else if constexpr (FMT == FMT_Q4_0) {
+  } else if constexpr (BLK32) {
     // 8 consecutive lanes quantize one block (lane e holds values 4e..4e+3); groups of 8 stay aligned and whole.
     const int total = MC * nblk * 8;
     for (int i0 = tid; i0 < total; i0 += SU * nthreads) {
@@ -283,7 +321,7 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
           int qsum;
           const unsigned packed = q8_0_group8(v[u], d, qsum);
           reinterpret_cast<unsigned*>(xv + (e < 4 ? mb : MC * nblk + mb))[e & 3] = packed;
-          if (e == 0) meta[mb] = make_int2(__float_as_int(d), -8 * qsum);
+          if (e == 0) meta[mb] = make_int2(__float_as_int(d), FMT == FMT_Q4_0 ? -8 * qsum : 0);
           if (blockIdx.x == 0 && XQo != nullptr) {
             reinterpret_cast<unsigned*>(XQo + static_cast<int64_t>(m) * K + b * 32)[e] = packed;
             if (e == 0) XDo[static_cast<int64_t>(m) * nblk + b] = d;
@@ -406,10 +444,18 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
         for (int m = 0; m < MC; ++m) {
           const int2 mt = meta[m * nblk + b];
           const float dx = __int_as_float(mt.x);
-          if constexpr (FMT == FMT_Q4_0) {
-            const int s = q4_0_block_dot<MODE>(w[u], xv[m * nblk + b], xv[(MC + m) * nblk + b], mt.y);
+          if constexpr (FMT == FMT_Q4_0 || FMT == FMT_IQ4_NL) {
+            const u32x4 xl = xv[m * nblk + b], xh = xv[(MC + m) * nblk + b];
+            const int s = FMT == FMT_Q4_0 ? q4_0_block_dot<MODE>(w[u], xl, xh, mt.y)
+                                          : iq4_nl_block_dot<MODE>(w[u], xl, xh);
             if (S != nullptr && rv) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
             acc[m] += static_cast<float>(s) * dw * dx;  // kernels.py:93 order
+          } else if constexpr (FMT == FMT_Q8_0) {
+            // lane pair: chunk q holds the block's values 16q .. 16q+15, dotted with the matching staged half
+            const int s = group_sum(q8_0_chunk_dot<MODE>(w[u], xv[(q * MC + m) * nblk + b]), 2);
+            if (S != nullptr && rv && q == 0) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
+            const float f = static_cast<float>(s) * dw * dx;  // kernels.py:93 order
+            acc[m] += q == 0 ? f : 0.0f;
           } else {
             u32x4 xs[4];
 #pragma unroll
@@ -449,7 +495,7 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
-  const int nblk = c.k / (FMT == FMT_Q4_0 ? 32 : 256);
+  const int nblk = c.k / fmt_info(FMT).block;
   // the workgroup's scale slab goes to LDS when it is small (the weight stream then issues only quant loads)
   const size_t base = gemv_lds_bytes(FMT, MC, c.k);
   const size_t sc_off = (base + 15) & ~static_cast<size_t>(15);
@@ -467,8 +513,10 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     if (e != hipSuccess) return e;
     lds_attr = lds;
   }
-  const Timing tm = timing_slot(FMT == FMT_Q4_0 ? KIND_Q4_0_GEMV : KIND_TQ2_0_GEMV);
-  const int bstep = (FMT == FMT_Q4_0 ? (1 << p.lpr_log2) : (1 << p.lpr_log2) / 4) * NB;
+  const Timing tm = timing_slot(gemv_kind(FMT));
+  const int cpb = fmt_info(FMT).qbytes / 16;  // 16-byte chunks per block
+  if ((1 << p.lpr_log2) < cpb) return hipErrorInvalidConfiguration;  // a row group holds whole blocks
+  const int bstep = ((1 << p.lpr_log2) / cpb) * NB;
   const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
   const int rows_per_wave = p.rows_per_wave;
   if (tm.on) {

@@ -1,0 +1,13 @@
+// Unfused GEMV launches for the Q8_0 and IQ4_NL weight formats (q8_0 activations in); the kernel template is in
+// gemv_kernel.h.  A translation unit of their own, so the library's instantiations compile in parallel.
+#include "gemv_kernel.h"
+
+namespace komp {
+
+hipError_t launch_gemv_more(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+  if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, false>(c, p, stream);
+  if (c.fmt == FMT_IQ4_NL) return gemv_impl::by_mode<FMT_IQ4_NL, false>(c, p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace komp

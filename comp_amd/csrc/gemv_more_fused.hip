@@ -1,0 +1,13 @@
+// Fused quantize-and-GEMV launches for the Q8_0 and IQ4_NL weight formats (f32 activations in); the kernel template
+// is in gemv_kernel.h.
+#include "gemv_kernel.h"
+
+namespace komp {
+
+hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+  if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, true>(c, p, stream);
+  if (c.fmt == FMT_IQ4_NL) return gemv_impl::by_mode<FMT_IQ4_NL, true>(c, p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace komp

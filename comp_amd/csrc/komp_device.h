@@ -36,6 +36,25 @@ __device__ __forceinline__ int dot4(unsigned a, unsigned b, int c) {
   }
 }
 
+// IQ4_NL: a quant word q (4 bytes of Q4_0's nibble order) -> the int8 values of ggml's kvalues_iq4nl table that its
+// 8 nibbles index: lo byte j = table[q byte j & 15], hi byte j = table[q byte j >> 4].  Per 4 nibbles, two
+// v_perm_b32 look the low 3 index bits up in the table's low and high eight entries, and a third v_perm_b32 keeps
+// one of the two per byte by bit 3 of the index (its selector byte j is j, or j + 4 to take the high lookup).
+// 13 VALU ops per 8 values.
+__device__ __forceinline__ void iq4_nl_lut(unsigned q, unsigned& lo, unsigned& hi) {
+  constexpr unsigned T0 = 0xBFAD9881u;  // -127, -104, -83, -65 (bytes 0..3)
+  constexpr unsigned T1 = 0xF6EADDCFu;  // -49, -35, -22, -10
+  constexpr unsigned T2 = 0x26190D01u;  // 1, 13, 25, 38
+  constexpr unsigned T3 = 0x71594535u;  // 53, 69, 89, 113
+  const unsigned r = q >> 4;  // byte j: the high nibble of q byte j in its low 4 bits
+  const unsigned sl = q & 0x07070707u;
+  const unsigned sh = r & 0x07070707u;
+  const unsigned l0 = __builtin_amdgcn_perm(T1, T0, sl), l1 = __builtin_amdgcn_perm(T3, T2, sl);
+  const unsigned h0 = __builtin_amdgcn_perm(T1, T0, sh), h1 = __builtin_amdgcn_perm(T3, T2, sh);
+  lo = __builtin_amdgcn_perm(l1, l0, ((q >> 1) & 0x04040404u) | 0x03020100u);
+  hi = __builtin_amdgcn_perm(h1, h0, ((r >> 1) & 0x04040404u) | 0x03020100u);
+}
+
 // Signed byte e of a 32-bit word.
 __device__ __forceinline__ int sbyte(unsigned w, int e) { return static_cast<int>(w << (24 - 8 * e)) >> 24; }
 

@@ -1,12 +1,12 @@
 // Weight ingestion on the device: ggml block bytes -> KURN's split planes, the device counterpart of the reference's
 // host.split (src/komp/host.py:16-22).
 //
-// W holds N rows of K/blk ggml blocks, each `nbytes` long (Q4_0: f16 d then 16 quant bytes, 18 bytes; TQ2_0: 64 quant
-// bytes then f16 d, 66 bytes).  Outputs: WQ u8 [N][SW] (the quant bytes of row r at WQ + r*SW, blocks in order) and
+// W holds N rows of K/blk ggml blocks, each `nbytes` long (Q4_0 and IQ4_NL: f16 d then 16 quant bytes, 18 bytes;
+// Q8_0: f16 d then 32 int8, 34 bytes; TQ2_0: 64 quant bytes then f16 d, 66 bytes).  Outputs: WQ u8 [N][SW] (the quant bytes of row r at WQ + r*SW, blocks in order) and
 // WS i16 [N][K/blk] (the f16 bit patterns).  Pure byte movement, so the planes equal host.split's bit for bit.
 //
-// One thread per 16-byte chunk of WQ (Q4_0: one per block, TQ2_0: four).  A chunk's 16 source bytes start at an
-// address that is 2 mod 4 for every other block (18- and 66-byte blocks), so the thread loads the aligned words that
+// One thread per 16-byte chunk of WQ (Q4_0, IQ4_NL: one per block, Q8_0: two, TQ2_0: four).  A chunk's 16 source
+// bytes start at an address that is 2 mod 4 for every other block (18-, 34- and 66-byte blocks), so the thread loads the aligned words that
 // cover them and funnel-shifts them into place (v_alignbyte_b32); consecutive threads read consecutive 16-18 byte
 // windows, so each wave's loads cover contiguous memory.  The loads go through a buffer descriptor whose range ends at
 // the launch's last byte, so nothing is read past the tensor.
@@ -59,11 +59,12 @@ split_kernel(int chunks, int nblk, int cpb_log2, int nbytes, int qoff, int soff,
 // Rows are launched in batches whose ggml bytes stay below 2^31 (32-bit buffer offsets).
 hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,
                         hipStream_t stream) {
-  const int blk = fmt == FMT_Q4_0 ? 32 : 256;
-  const int nbytes = fmt == FMT_Q4_0 ? 18 : 66;
-  const int qoff = fmt == FMT_Q4_0 ? 2 : 0;
-  const int soff = fmt == FMT_Q4_0 ? 0 : 64;
-  const int cpb_log2 = fmt == FMT_Q4_0 ? 0 : 2;
+  const FmtInfo f = fmt_info(fmt);
+  const int blk = f.block;
+  const int nbytes = f.nbytes;
+  const int qoff = f.qoff;
+  const int soff = f.soff;
+  const int cpb_log2 = f.qbytes == 16 ? 0 : (f.qbytes == 32 ? 1 : 2);  // 16-byte chunks per block
   const int64_t nblk = k / blk;
   const int64_t row_bytes = nblk * nbytes;
   int64_t rows_per = row_bytes > 0 ? (int64_t{1} << 30) / row_bytes : n;

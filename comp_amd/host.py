@@ -28,10 +28,13 @@ from . import _abi
 FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale offset, activation format
     "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
     "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
+    # ggml formats beyond the reference's two (its README.md:144 lists them as next): same planes, q8_0 activations
+    "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
+    "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
 }
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
-FMT_ID = {"q4_0": 0, "tq2_0": 1}
-GEMM_MIN_M = {"q4_0": 4, "tq2_0": 4}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
+FMT_ID = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3}
+GEMM_MIN_M = {f: 4 for f in FMT_ID}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
 
 
 def split(fmt, W, n, k):
@@ -82,7 +85,7 @@ def split_into(fmt, W, wq, ws, n, k):
     for t, name in ((wq, "wq"), (ws, "ws")):
         if t.device != W.device:
             raise _abi.KompArgumentError(f"{name} is on {t.device}, W on {W.device}")
-    fn = "komp_q4_0_split" if fmt == "q4_0" else "komp_tq2_0_split"
+    fn = f"komp_{fmt}_split"
     with torch.cuda.device(W.device):
         _abi.call(fn, W.data_ptr(), wq.data_ptr(), ws.data_ptr(), n, k, wq.stride(0) if n else 16, _stream(W))
 
@@ -211,7 +214,7 @@ def _check_gemv(fmt, wq, ws, xq, xd, n, k):
 def _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps):
     if block_n is None:
         block_n, nb, num_warps = 0, 0, 0
-    fn = "komp_q4_0_gemv" if fmt == "q4_0" else "komp_tq2_0_gemv"
+    fn = f"komp_{fmt}_gemv"
     with torch.cuda.device(xq.device):
         _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
                   None if s is None else s.data_ptr(), xq.shape[0], n, k, wq.stride(0), block_n, nb, mode, num_warps,
@@ -230,7 +233,7 @@ def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store
 
 
 def _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k):
-    fn = "komp_q4_0_gemm" if fmt == "q4_0" else "komp_tq2_0_gemm"
+    fn = f"komp_{fmt}_gemm"
     with torch.cuda.device(xq.device):
         _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
                   None if s is None else s.data_ptr(), xq.shape[0], n, k, wq.stride(0), _stream(xq))  # fmt: skip
@@ -360,11 +363,14 @@ def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps
             raise _abi.KompArgumentError(f"{name} is on {t.device}, x on {x.device}")
     if block_n is None:
         block_n, nb, num_warps = 0, 0, 0
-    fn = "komp_q4_0_gemv_f32" if fmt == "q4_0" else "komp_tq2_0_gemv_f32"
+    fn = f"komp_{fmt}_gemv_f32"
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    planes = (ptr(xq), ptr(xd), ptr(xb)) if fmt in ("q4_0", "tq2_0") else (ptr(xq), ptr(xd))  # the others: no XB
+    if xb is not None and FORMATS[fmt]["act"] != "q8_K":
+        raise _abi.KompArgumentError("xb (bsums) is a q8_K plane; pass None for q8_0 activations")
     with torch.cuda.device(x.device):
-        _abi.call(fn, wq.data_ptr(), ws.data_ptr(), x.data_ptr(), y.data_ptr(), ptr(s), ptr(xq), ptr(xd), ptr(xb), m, n,
-                  k, wq.stride(0), block_n, nb, mode, num_warps, _stream(x))  # fmt: skip
+        _abi.call(fn, wq.data_ptr(), ws.data_ptr(), x.data_ptr(), y.data_ptr(), ptr(s), *planes, m, n, k, wq.stride(0),
+                  block_n, nb, mode, num_warps, _stream(x))  # fmt: skip
 
 
 def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, store_s=False, return_q=False):
@@ -433,7 +439,7 @@ def gemv_multi_into(fmt, mats, ys, k, xq=None, xd=None, x=None, block_n=None, nb
     yps = P(*(y.data_ptr() for y in ys))
     ns = I64(*(n for _, _, n in mats))
     sws = I64(*(w.stride(0) for w, _, _ in mats))
-    fn = "komp_q4_0_gemv_multi" if fmt == "q4_0" else "komp_tq2_0_gemv_multi"
+    fn = f"komp_{fmt}_gemv_multi"
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     with torch.cuda.device(ref.device):
         _abi.call(fn, cnt, wqs, wss, yps, ns, sws, ptr(xq), ptr(xd), ptr(x), m, k, block_n, nb, mode, num_warps,

@@ -99,7 +99,40 @@ int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* co
                           const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
                           int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
 
-/* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0; fused != 0 for
+/* Q8_0 and IQ4_NL weights x q8_0 activations: ggml formats beyond the reference's two (its README.md:144 lists them as
+ * next), on the same split planes and with the same entries and semantics as Q4_0:
+ *   Q8_0    WQ u8 [N][SW] (32 int8 per block of 32, SW >= K), WS i16 [N][K/32] (f16 bits)   (ggml block_q8_0)
+ *   IQ4_NL  WQ u8 [N][SW] (16 bytes per block of 32 in Q4_0's nibble order; each nibble indexes ggml's value table
+ *           kvalues_iq4nl), WS i16 [N][K/32]                                              (ggml block_iq4_nl)
+ * Y[m][n] = sum_b f16(d_w) * d_x * s(m, n, b) with s the exact int32 block dot of the decoded values.  The _f32
+ * entries take no XB (q8_0 activations have no bsums).  No reference counterpart. */
+int komp_q8_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                   void* stream);
+int komp_iq4_nl_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                     int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                     void* stream);
+int komp_q8_0_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                       float* XD, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode,
+                       int num_warps, void* stream);
+int komp_iq4_nl_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                         float* XD, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode,
+                         int num_warps, void* stream);
+int komp_q8_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                         const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                         int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+int komp_iq4_nl_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                           const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                           int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+int komp_q8_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
+int komp_iq4_nl_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                     int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
+int komp_q8_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
+int komp_iq4_nl_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
+
+/* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0, 2 = q8_0,
+ * 3 = iq4_nl; fused != 0 for
  * komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32; mode as in the GEMV entries; M the activation columns.  block_n receives
  * the rows per workgroup, nb the 16-byte weight chunks each lane loads per row per K step, num_warps the waves per
  * workgroup, and (when not NULL) lanes_per_row the lanes that share a row and passes the row groups each wave walks
@@ -125,7 +158,7 @@ int komp_q4_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const
 int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                     int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
 
-/* The matrix-core GEMM's plan for a shape on the current device (fmt 0 = q4_0, 1 = tq2_0): weight rows and activation
+/* The matrix-core GEMM's plan for a shape on the current device (fmt as komp_gemv_auto_config): weight rows and activation
  * columns per workgroup, waves per workgroup.  Returns KOMP_EINVAL when the shape is past the kernel's limits.
  * No reference counterpart. */
 int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
@@ -155,9 +188,9 @@ int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* strea
  * issued with hipExtLaunchKernel start/stop events, which the runtime stamps with the dispatch's own begin and end.
  * komp_timing_end() waits for those events and returns, per kernel kind, the summed dispatch time in milliseconds and
  * the dispatch count.  Kinds: 0 quant_q8_0, 1 quant_q8_K, 2 q4_0 GEMV / GEMM, 3 tq2_0 GEMV / GEMM, 4 probes and
- * weight splits (arrays of length 5).
+ * weight splits, 5 q8_0 GEMV / GEMM, 6 iq4_nl GEMV / GEMM (arrays of length 7).
  * max_dispatches bounds the events created. */
-#define KOMP_TIMING_KINDS 5
+#define KOMP_TIMING_KINDS 7
 int komp_timing_begin(int64_t max_dispatches);
 int komp_timing_end(double* ms, int64_t* count);
 

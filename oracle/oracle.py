@@ -17,6 +17,10 @@ How each function is pinned (tests/test_oracle_pins.py):
 
   f16_bits_to_f32        all 65536 bit patterns vs IEEE binary16 decoded from its fields with exact rationals
   q4_0_values            all 256 byte values vs the per-value formula; ggml q4_0 quantize->decode round trip
+  q8_0_values            all 256 byte values vs struct's signed-byte decode of ggml block_q8_0 bytes
+  iq4_nl_values          all 256 byte values at both nibble positions vs a per-byte loop over ggml block_iq4_nl
+                         bytes; the table itself (ggml's kvalues_iq4nl) is parity unpinned: KURN, where COMP's
+                         formats would be defined, is absent, so the table restates ggml's published constant
   tq2_0_values           all 256 byte values at every crumb position vs a per-value loop over the layout text
   dp4a                   the reference's 11 edge words + random words vs an independent struct-based byte dot
   round_half_*           vs Python's round()/Fraction on ties, negatives, huge and subnormal values
@@ -38,7 +42,13 @@ import numpy as np
 FORMATS = {
     "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
     "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
+    # ggml formats the reference lists as next (README.md:144), restated from ggml's published block layouts
+    # (ggml-common.h: block_q8_0 = f16 d + 32 int8; block_iq4_nl = f16 d + 16 bytes of 4-bit table indices)
+    "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
+    "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
 }
+# ggml's IQ4_NL value table (ggml-common.h kvalues_iq4nl): a fixed non-uniform 4-bit grid
+IQ4_NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int32)
 ACT_BLOCK = {"q8_0": 32, "q8_K": 256}
 
 
@@ -57,6 +67,18 @@ def q4_0_values(qs):
     lo = (qs & 15).astype(np.int32) - 8
     hi = (qs >> 4).astype(np.int32) - 8
     return np.concatenate([lo, hi], axis=-1)
+
+
+def q8_0_values(qs):
+    """[..., 32] q8_0 quant bytes -> [..., 32] int32: value i = byte i as a signed int8 (ggml dequantize_row_q8_0)."""
+    return np.asarray(qs, dtype=np.uint8).view(np.int8).astype(np.int32)
+
+
+def iq4_nl_values(qs):
+    """[..., 16] iq4_nl quant bytes -> [..., 32] int32: value i = table[byte i & 15], value i+16 = table[byte i >> 4]
+    (ggml dequantize_row_iq4_nl: the Q4_0 nibble order with the non-uniform table in place of nibble - 8)."""
+    qs = np.asarray(qs, dtype=np.uint8)
+    return np.concatenate([IQ4_NL_VALUES[qs & 15], IQ4_NL_VALUES[qs >> 4]], axis=-1)
 
 
 def tq2_0_values(qs):
@@ -223,6 +245,10 @@ def weight_values(fmt, wq, n, k):
     wq = np.asarray(wq, np.uint8).reshape(n, -1)
     if fmt == "q4_0":
         return q4_0_values(wq[:, : k // 2].reshape(n, k // 32, 16)).reshape(n, k)
+    if fmt == "iq4_nl":
+        return iq4_nl_values(wq[:, : k // 2].reshape(n, k // 32, 16)).reshape(n, k)
+    if fmt == "q8_0":
+        return q8_0_values(wq[:, :k]).reshape(n, k)
     return tq2_0_values(wq[:, : k // 4].reshape(n, k // 256, 64)).reshape(n, k)
 
 
@@ -239,14 +265,16 @@ def reference_dot(fmt, ws, xd, s):
 
     q4_0 adds f16(dw) * f16(dx) * s, tq2_0 adds f32(dx) * f16(dw) * s, left to right, in Python-float (f64)
     arithmetic.  Both products are exact in f64 (11+11+22 and 24+11+16 significant bits), so only the running
-    sum rounds, and the result depends on the block order alone."""
+    sum rounds, and the result depends on the block order alone.  q8_0 and iq4_nl weights take q4_0's form (ggml's
+    vec_dot_q8_0_q8_0 and vec_dot_iq4_nl_q8_0 scale the int block dot by f16(dw) * f16(dx)); their block dots stay
+    below 2**22 in magnitude, so the products are exact there too."""
     dw = f16_bits_to_f32(ws).astype(np.float64)  # [N][nb]
     dx = np.asarray(xd, np.float32).astype(np.float64)  # [M][nb]
     s = np.asarray(s, dtype=np.int64)
     m, n, nb = s.shape
     total = np.zeros((m, n), dtype=np.float64)
     for b in range(nb):
-        if fmt == "q4_0":
+        if fmt != "tq2_0":
             term = (dw[None, :, b] * dx[:, None, b]) * s[:, :, b]
         else:
             term = (dx[:, None, b] * dw[None, :, b]) * s[:, :, b]
@@ -330,6 +358,16 @@ def pack_tq2_0(crumbs, d_bits):
     return out.tobytes()
 
 
+def pack_q8_0(q, d_bits):
+    """int8 values [n][k] and f16 bit patterns [n][k/32] -> ggml q8_0 blocks (f16 d, then 32 int8)."""
+    q = np.asarray(q, np.int8)
+    n, k = q.shape
+    out = np.empty((n, k // 32, 34), dtype=np.uint8)
+    out[:, :, :2] = np.ascontiguousarray(d_bits, dtype=np.uint16).view(np.uint8).reshape(n, k // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8).reshape(n, k // 32, 32)
+    return out.tobytes()
+
+
 F16_MAX_BITS = 0x7BFF  # 65504
 F16_MIN_SUBNORMAL_BITS = 0x0001  # 2**-24
 
@@ -338,10 +376,34 @@ def weights(fmt, rng, n, k, extreme=False):
     """Seeded ggml weight blocks for an n x k matrix.
 
     random  q4_0: W ~ N(0, 0.02) quantized by ggml's q4_0 rule; tq2_0: trits from {-1, 0, +1} with p 0.3/0.4/0.3,
-            d ~ U(0.01, 0.05) rounded to f16.
+            d ~ U(0.01, 0.05) rounded to f16; q8_0: W ~ N(0, 0.02) quantized by ggml's q8_0 rule; iq4_nl: uniform
+            table indices, d ~ U(0.0005, 0.002).
     extreme per block: f16 d at 65504, at the smallest subnormal 2**-24 or random; values all at the minimum
             (nibble 0 / crumb 0), all at the maximum (nibble 15 / crumb 2), random, or (tq2_0) crumb 3."""
     nb = k // FORMATS[fmt]["block"]
+    if fmt == "q8_0":
+        if not extreme:  # ggml quantize_row_q8_0_ref of W ~ N(0, 0.02): the activation quantizer's rule
+            q, d = quant_q8_0(rng.normal(0.0, 0.02, size=(n, k)).astype(np.float32))
+            return pack_q8_0(q, d.astype(np.float16).view(np.uint16))
+        q = rng.integers(-128, 128, size=(n, nb, 32)).astype(np.int8)
+        kind = rng.integers(0, 4, size=(n, nb))
+        q[kind == 1] = -128
+        q[kind == 2] = 127
+        q[kind == 3] = -127
+        d = np.asarray(rng.uniform(-0.05, 0.05, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+        sk = rng.integers(0, 4, size=(n, nb))
+        d = np.where(sk == 1, F16_MAX_BITS, np.where(sk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
+        return pack_q8_0(q.reshape(n, k), d)
+    if fmt == "iq4_nl":  # any nibbles are valid table indices; d ~ U(0.0005, 0.002) (values up to 127 * d)
+        nib = rng.integers(0, 16, size=(n, nb, 32), dtype=np.uint8)
+        d = np.asarray(rng.uniform(0.0005, 0.002, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+        if extreme:
+            kind = rng.integers(0, 3, size=(n, nb))
+            nib[kind == 1] = 0
+            nib[kind == 2] = 15
+            sk = rng.integers(0, 4, size=(n, nb))
+            d = np.where(sk == 1, F16_MAX_BITS, np.where(sk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
+        return pack_q4_0(nib.reshape(n, k), d)  # same bytes as Q4_0: index i low nibble, index i+16 high nibble
     if fmt == "q4_0" and not extreme:
         return quantize_q4_0_weights(rng.normal(0.0, 0.02, size=(n, k)).astype(np.float32))
     if fmt == "q4_0":

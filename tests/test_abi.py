@@ -21,6 +21,8 @@ def declared():
 
 def test_header_and_binding_agree():
     assert declared() == set(_abi.SIGNATURES)
+    kinds = re.search(r"#define KOMP_TIMING_KINDS (\d+)", open(HEADER).read())
+    assert int(kinds.group(1)) == len(_abi.TIMING_KINDS)
 
 
 def test_library_exports_every_declared_symbol():
@@ -178,4 +180,7 @@ def test_gemm_rejects_bad_arguments():
     rows, cols, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.komp_gemm_plan(0, 16, 4096, 4096, 2048, ctypes.byref(rows), ctypes.byref(cols), ctypes.byref(waves)) == 0
     assert cols.value == 16 and waves.value == 8 and rows.value % 16 == 0
-    assert lib.komp_gemm_plan(2, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL
+    for fmt in (2, 3):  # q8_0, iq4_nl
+        assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 4096, None, None, None) == 0
+    for fmt in (-1, 4):
+        assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL

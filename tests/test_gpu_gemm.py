@@ -1,4 +1,4 @@
-"""Matrix-core GEMM (komp_q4_0_gemm / komp_tq2_0_gemm) vs the oracle: int32 block dots S exact, Y within 1e-5
+"""Matrix-core GEMM (komp_{q4_0,tq2_0,q8_0,iq4_nl}_gemm) vs the oracle: int32 block dots S exact, Y within 1e-5
 (norm-wise) of the f64 reference_dot, on the same seeded problems.  Shapes cover the kernel's tails: rows not a
 multiple of 16, column counts around the 16-column tiles and the 64-column workgroups, Q4_0 block counts that are not
 a multiple of the 4-block K step, scale planes that take the 2-byte staging path, padded weight rows, and the
@@ -22,6 +22,7 @@ SHAPES = {
     "tq2_0": [(16, 256, 1), (16, 256, 3), (64, 1024, 4), (37, 768, 5), (5, 1280, 17), (33, 2560, 31),
               (100, 2560, 33), (40, 6912, 64), (48, 256, 65), (300, 512, 130)],
 }
+SHAPES["q8_0"] = SHAPES["iq4_nl"] = SHAPES["q4_0"]
 
 
 def dev(a):
@@ -48,7 +49,7 @@ def check(fmt, n, k, m, seed, extreme=False, ws_offset=0, pad=0):
     return y
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 @pytest.mark.parametrize("shape", range(10))
 @pytest.mark.parametrize("extreme", [False, True])
 def test_gemm_matches_oracle(fmt, shape, extreme):
@@ -56,11 +57,11 @@ def test_gemm_matches_oracle(fmt, shape, extreme):
     check(fmt, n, k, m, 300 + shape, extreme)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 def test_gemm_unaligned_scales_and_padded_rows(fmt):
-    k = 416 if fmt == "q4_0" else 768
+    k = 416 if fmt != "tq2_0" else 768
     check(fmt, 45, k, 20, 11, ws_offset=1, pad=48)
-    check(fmt, 64, 2 * k if fmt == "q4_0" else 1024, 8, 12, ws_offset=3)
+    check(fmt, 64, 2 * k if fmt != "tq2_0" else 1024, 8, 12, ws_offset=3)
 
 
 # one shape per plan family on a 256-CU device: (n, k, m, rows per workgroup, columns per workgroup)
@@ -75,21 +76,23 @@ FAMILIES = [
 ]
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 @pytest.mark.parametrize("fam", range(len(FAMILIES)))
 def test_gemm_plan_families(fmt, fam):
     n, k, m, rows, cols = FAMILIES[fam]
     if fmt == "tq2_0":
         k = 512 if k == 256 else 1024
+    if fmt == "q8_0" and rows == 256:
+        rows = 128  # Q8_0 waves take one row tile each (two would need more than 256 VGPRs)
     plan = host.gemm_plan(fmt, m, n, k)
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert (plan["rows"], plan["cols"]) == (rows, cols), plan
     check(fmt, n, k, m, 60 + fam)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 def test_gemv_auto_routes_batches_to_gemm(fmt):
-    n, k, m = (96, 1024, 12) if fmt == "q4_0" else (96, 1536, 12)
+    n, k, m = (96, 1024, 12) if fmt != "tq2_0" else (96, 1536, 12)
     W, x = O.problem(fmt, n, k, m, 31)
     wq, ws = host.split(fmt, W, n, k)
     xq, xd, *_ = host.quantize(fmt, dev(x))
@@ -108,14 +111,14 @@ def test_gemv_auto_routes_batches_to_gemm(fmt):
     assert O.relerr(y_gemm.cpu().numpy(), r) <= TOL and O.relerr(y_gemv.cpu().numpy(), r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 def test_gemm_multi_matrix_batches(fmt):
     k = 512
     ns = (40, 24, 64)
     m = 9
     rng = np.random.default_rng(41)
     mats, refs = [], []
-    x = O.activations(rng, k, m, block=32 if fmt == "q4_0" else 256)
+    x = O.activations(rng, k, m, block=O.ACT_BLOCK[O.FORMATS[fmt]["act"]])
     rq, rd, _ = O.quantize(fmt, x)
     for n in ns:
         W = O.weights(fmt, rng, n, k)
@@ -128,7 +131,7 @@ def test_gemm_multi_matrix_batches(fmt):
         assert O.relerr(y.cpu().numpy(), r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 def test_gemm_empty_k_writes_zeros(fmt):
     n, m = 20, 5
     wq = torch.zeros((n, 16), dtype=torch.uint8, device="cuda")  # a row stride of 16 bytes, no quant bytes used
@@ -141,9 +144,9 @@ def test_gemm_empty_k_writes_zeros(fmt):
     assert torch.count_nonzero(y).item() == 0
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 def test_gemm_graph_replays(fmt):
-    n, k, m = (200, 1024, 24) if fmt == "q4_0" else (200, 1280, 24)
+    n, k, m = (200, 1024, 24) if fmt != "tq2_0" else (200, 1280, 24)
     W, x = O.problem(fmt, n, k, m, 51)
     wq, ws = host.split(fmt, W, n, k)
     wq, ws = dev(wq), dev(ws)

@@ -20,7 +20,7 @@ def dev(a):
 def problems(fmt, ns, k, m, seed):
     """Per matrix: (W bytes, split planes on the device); one shared activation x [m][k]."""
     rng = np.random.default_rng(seed)
-    x = O.activations(rng, k, m, block=32 if fmt == "q4_0" else 256, extreme=False, outliers=0.01)
+    x = O.activations(rng, k, m, block=O.ACT_BLOCK[O.FORMATS[fmt]["act"]], extreme=False, outliers=0.01)
     mats = []
     for i, n in enumerate(ns):
         W = O.weights(fmt, np.random.default_rng(seed + 1 + i), n, k, False)
@@ -30,7 +30,8 @@ def problems(fmt, ns, k, m, seed):
 
 
 CASES = [("q4_0", (4096, 1024, 1024), 4096), ("tq2_0", (6912, 6912), 2560), ("q4_0", (37, 5, 100, 64), 416),
-         ("tq2_0", (13, 300, 1), 1280), ("q4_0", (64, 0, 33), 512)]  # fmt: skip
+         ("tq2_0", (13, 300, 1), 1280), ("q4_0", (64, 0, 33), 512), ("q8_0", (4096, 1024, 1024), 4096),
+         ("iq4_nl", (37, 5, 100, 64), 416), ("q8_0", (13, 300, 1), 1280)]  # fmt: skip
 
 
 @pytest.mark.parametrize("fmt,ns,k", CASES)

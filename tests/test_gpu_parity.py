@@ -14,6 +14,8 @@ TOL = 1e-5
 # src/komp/verify.py:141-142
 PROBLEMS = {"q4_0": ((64, 512, 1), (37, 416, 3), (5, 96, 2)), "tq2_0": ((64, 1024, 1), (37, 768, 3), (5, 1280, 2))}
 CONFIGS = {"q4_0": ((32, 4, 4), (16, 2, 2), (64, 8, 4)), "tq2_0": ((32, 2, 4), (16, 1, 2), (64, 4, 4))}
+for _f in ("q8_0", "iq4_nl"):  # the ggml formats beyond the reference's two take Q4_0's problems and knob sets
+    PROBLEMS[_f], CONFIGS[_f] = PROBLEMS["q4_0"], CONFIGS["q4_0"]
 
 
 def dev(a):
@@ -130,7 +132,7 @@ def run_gemv(fmt, n, k, m, seed, extreme, block_n, nb, mode, num_warps):
     return y.cpu().numpy(), s.cpu().numpy(), r, rs, xq.cpu().numpy(), rq
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 @pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("cfg", [0, 1, 2])
 @pytest.mark.parametrize("prob", [0, 1, 2])
@@ -144,22 +146,23 @@ def test_gemv_verify_problems(fmt, mode, cfg, prob, extreme):
     assert O.relerr(y, r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
 @pytest.mark.parametrize("block_n", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("nb", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("nw", [1, 2, 4, 8])
 def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
-    n, k, m = (77, 96 * 32, 3) if fmt == "q4_0" else (77, 13 * 256, 3)
+    n, k, m = (77, 96 * 32, 3) if fmt != "tq2_0" else (77, 13 * 256, 3)
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
     assert np.array_equal(s.astype(np.int64), rs)
     assert O.relerr(y, r) <= TOL
 
 
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 16384, 8192), ("q4_0", 16400, 4192), ("tq2_0", 16384, 2816),
-                                     ("q4_0", 20000, 1024)])  # fmt: skip
+                                     ("q4_0", 20000, 1024), ("q8_0", 16400, 4192), ("iq4_nl", 16384, 8192),
+                                     ("q8_0", 20000, 1024)])  # fmt: skip
 def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
     # N >= 16384 (16400 and 20000 leave a partial last workgroup); q4_0 reads whole rows in one K step, two passes
-    assert host.auto_plan(fmt, 1, n, k)["passes"] == (2 if fmt == "q4_0" else 1)
+    assert host.auto_plan(fmt, 1, n, k)["passes"] == (2 if fmt != "tq2_0" else 1)
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, 1, 23, False, None, None, 2, None)
     assert np.array_equal(s.astype(np.int64), rs)
     assert O.relerr(y, r) <= TOL
@@ -168,7 +171,9 @@ def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 4096, 4096), ("q4_0", 4097, 4192), ("q4_0", 127, 4192),
                                      ("q4_0", 16383, 4096), ("q4_0", 300, 96), ("tq2_0", 6912, 2560),
                                      ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816), ("tq2_0", 16383, 256),
-                                     ("tq2_0", 513, 1280)])  # fmt: skip
+                                     ("tq2_0", 513, 1280), ("q8_0", 4096, 4096), ("q8_0", 4097, 4192),
+                                     ("q8_0", 300, 96), ("iq4_nl", 4096, 4096), ("iq4_nl", 127, 4192),
+                                     ("iq4_nl", 16383, 4096)])  # fmt: skip
 @pytest.mark.parametrize("m", [1, 3])
 def test_gemv_auto_config_shapes(fmt, n, k, m):
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 21, False, None, None, 2, None)
@@ -205,7 +210,8 @@ def test_decode_probes():
 
 
 @pytest.mark.parametrize("fmt,n,k,knobs", [("q4_0", 300, 4096, (16, 4, 4)), ("q4_0", 4096, 4096, None),
-                                           ("tq2_0", 300, 8192, (32, 2, 8)), ("tq2_0", 2560, 8192, None)])  # fmt: skip
+                                           ("tq2_0", 300, 8192, (32, 2, 8)), ("tq2_0", 2560, 8192, None),
+                                           ("q8_0", 300, 4096, (16, 4, 4)), ("iq4_nl", 4096, 4096, None)])  # fmt: skip
 def test_scale_slab_and_per_tile_scales_agree(fmt, n, k, knobs):
     # a 16-byte aligned WS is staged in LDS per workgroup; a WS view at a 2-byte offset takes the per-tile scale loads
     W, x = O.problem(fmt, n, k, 1, 31)
@@ -228,7 +234,8 @@ def test_scale_slab_and_per_tile_scales_agree(fmt, n, k, knobs):
 @pytest.mark.parametrize("fmt,n,k,fused", [("tq2_0", 6912, 2560, True), ("tq2_0", 6913, 2816, False),
                                            ("q4_0", 4097, 4096, True), ("tq2_0", 4097, 2048, False),
                                            ("tq2_0", 300, 1280, False), ("q4_0", 6144, 4096, True),
-                                           ("q4_0", 4096, 14336, True), ("tq2_0", 2560, 6912, True)])  # fmt: skip
+                                           ("q4_0", 4096, 14336, True), ("tq2_0", 2560, 6912, True),
+                                           ("q8_0", 4097, 4096, True), ("iq4_nl", 6144, 4096, True)])  # fmt: skip
 def test_one_workgroup_per_cu_plans(fmt, n, k, fused):
     # small single-column GEMVs plan one workgroup of ceil(N / CUs) rows per CU; the first five shapes give the waves
     # more row slots than rows (clipped per wave), q4_0 4097x4096 and tq2_0 4097x2048 with the scale slab in LDS

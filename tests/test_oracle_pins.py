@@ -49,6 +49,47 @@ def test_q4_0_every_byte_every_position():
         assert (v[:, others] == -8).all()
 
 
+def test_q8_0_every_byte_every_position():
+    for pos in (0, 13, 31):
+        qs = np.zeros((256, 32), np.uint8)
+        qs[:, pos] = np.arange(256)
+        v = O.q8_0_values(qs)
+        for b in range(256):
+            assert v[b, pos] == struct.unpack("<b", bytes([b]))[0]
+        assert (np.delete(v, pos, axis=1) == 0).all()
+
+
+def test_iq4_nl_every_byte_every_position():
+    # value i = table[low nibble of byte i], value i+16 = table[high nibble of byte i]; decoded here through the table
+    # held in a dict keyed by nibble, one byte at a time
+    table = dict(enumerate(int(t) for t in O.IQ4_NL_VALUES))
+    for pos in (0, 7, 15):
+        qs = np.full((256, 16), 0x88, np.uint8)  # nibble 8 -> table[8] elsewhere
+        qs[:, pos] = np.arange(256)
+        v = O.iq4_nl_values(qs)
+        for b in range(256):
+            assert v[b, pos] == table[b & 15] and v[b, pos + 16] == table[b >> 4]
+        others = [i for i in range(32) if i not in (pos, pos + 16)]
+        assert (v[:, others] == table[8]).all()
+    # the table is a non-uniform 4-bit grid inside int8: 16 strictly increasing entries spanning -127 .. 113
+    t = O.IQ4_NL_VALUES
+    assert t.size == 16 and (np.diff(t) > 0).all() and t[0] == -127 and t[-1] == 113 and len(set(t.tolist())) == 16
+
+
+def test_new_format_blocks_from_ggml_bytes():
+    # block_q8_0 / block_iq4_nl bytes built with struct, decoded value by value
+    rng = np.random.default_rng(21)
+    d = struct.pack("<e", 0.25)
+    q = [int(v) for v in rng.integers(-128, 128, size=32)]
+    blk = d + struct.pack("<32b", *q)
+    wq, ws = O.split("q8_0", blk, 1, 32)
+    assert ws[0, 0].tobytes() == d and O.weight_values("q8_0", wq, 1, 32).tolist() == [q]
+    idx = [int(v) for v in rng.integers(0, 16, size=32)]
+    blk = d + bytes((idx[i] | (idx[i + 16] << 4)) for i in range(16))
+    wq, ws = O.split("iq4_nl", blk, 1, 32)
+    assert O.weight_values("iq4_nl", wq, 1, 32).tolist() == [[int(O.IQ4_NL_VALUES[i]) for i in idx]]
+
+
 def test_tq2_0_every_byte_every_position():
     # ggml dequantize_row_tq2_0 order: for j in (0, 32): for l in 0..3: for m in 0..31: y = crumb(qs[j+m], l) - 1
     rng = np.random.default_rng(0)
@@ -258,7 +299,7 @@ def test_act_block_layouts():
 # GEMV references (verify.py:94-120)
 
 
-@pytest.mark.parametrize("fmt,k", [("q4_0", 96), ("tq2_0", 512)])
+@pytest.mark.parametrize("fmt,k", [("q4_0", 96), ("tq2_0", 512), ("q8_0", 96), ("iq4_nl", 96)])
 def test_block_dots_brute_force(fmt, k):
     rng = np.random.default_rng(8)
     n, m = 5, 2
@@ -273,6 +314,10 @@ def test_block_dots_brute_force(fmt, k):
             raw = W[(r * (k // blk) + b) * O.FORMATS[fmt]["nbytes"] :][: O.FORMATS[fmt]["nbytes"]]
             if fmt == "q4_0":
                 vals = [(raw[2 + i % 16] >> (4 * (i // 16))) % 16 - 8 for i in range(32)]
+            elif fmt == "q8_0":
+                vals = list(struct.unpack("<32b", bytes(raw[2:34])))
+            elif fmt == "iq4_nl":
+                vals = [int(O.IQ4_NL_VALUES[(raw[2 + i % 16] >> (4 * (i // 16))) % 16]) for i in range(32)]
             else:
                 vals = [(raw[(v // 128) * 32 + v % 32] >> (2 * ((v % 128) // 32))) % 4 - 1 for v in range(256)]
             for i in range(m):
