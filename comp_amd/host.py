@@ -28,7 +28,7 @@ from . import _abi
 FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale offset, activation format
     "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
     "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
-    # ggml formats beyond the reference's two (its README.md:144 lists them as next): same planes, q8_0 activations
+    # ggml formats beyond the reference's two (its README.md:143 lists them as next): same planes, q8_0 activations
     "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
     "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
 }

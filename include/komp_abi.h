@@ -99,7 +99,7 @@ int komp_tq2_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* co
                           const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
                           int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
 
-/* Q8_0 and IQ4_NL weights x q8_0 activations: ggml formats beyond the reference's two (its README.md:144 lists them as
+/* Q8_0 and IQ4_NL weights x q8_0 activations: ggml formats beyond the reference's two (its README.md:143 lists them as
  * next), on the same split planes and with the same entries and semantics as Q4_0:
  *   Q8_0    WQ u8 [N][SW] (32 int8 per block of 32, SW >= K), WS i16 [N][K/32] (f16 bits)   (ggml block_q8_0)
  *   IQ4_NL  WQ u8 [N][SW] (16 bytes per block of 32 in Q4_0's nibble order; each nibble indexes ggml's value table

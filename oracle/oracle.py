@@ -42,7 +42,7 @@ import numpy as np
 FORMATS = {
     "q4_0": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
     "tq2_0": dict(block=256, nbytes=66, qoff=0, qbytes=64, soff=64, act="q8_K"),
-    # ggml formats the reference lists as next (README.md:144), restated from ggml's published block layouts
+    # ggml formats the reference lists as next (README.md:143), restated from ggml's published block layouts
     # (ggml-common.h: block_q8_0 = f16 d + 32 int8; block_iq4_nl = f16 d + 16 bytes of 4-bit table indices)
     "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
     "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
