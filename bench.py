@@ -45,7 +45,8 @@ TRAFFIC_FUSED_BITNET_M1 = 4882640
 
 
 # (values per weight block, weight bytes per block, values per activation block) of each weight format
-BLOCKS = {"q4_0": (32, 18, 32), "tq2_0": (256, 66, 256), "q8_0": (32, 34, 32), "iq4_nl": (32, 18, 32)}
+BLOCKS = {"q4_0": (32, 18, 32), "tq2_0": (256, 66, 256), "q8_0": (32, 34, 32), "iq4_nl": (32, 18, 32),
+          "q4_k": (256, 144, 256)}
 
 
 def gemv_bytes(fmt, n, k, m):
@@ -116,7 +117,19 @@ def iq4_nl_weights(n, k, gen, torch):
     return wq, d[:, :, 0].half().view(torch.int16).contiguous()
 
 
-WEIGHTS = {"q4_0": q4_0_weights, "tq2_0": tq2_0_weights, "q8_0": q8_0_weights, "iq4_nl": iq4_nl_weights}
+def q4_k_weights(n, k, gen, torch):
+    """Split planes of Q4_K weights: uniform nibbles and 6-bit scale / min bytes, d and dmin ~ U(0.0002, 0.001)
+    (the scale plane holds each block's d, dmin and 12 scale bytes: int16 [n][8 * blocks])."""
+    nb = k // 256
+    wq = torch.randint(0, 256, (n, nb * 128), dtype=torch.uint8, device="cuda", generator=gen)
+    meta = torch.randint(0, 256, (n, nb, 16), dtype=torch.uint8, device="cuda", generator=gen)
+    dd = (torch.rand((n, nb, 2), generator=gen, device="cuda") * 0.0008 + 0.0002).half()
+    meta[:, :, :4] = dd.view(torch.uint8).reshape(n, nb, 4)
+    return wq, meta.view(torch.int16).reshape(n, nb * 8).contiguous()
+
+
+WEIGHTS = {"q4_0": q4_0_weights, "tq2_0": tq2_0_weights, "q8_0": q8_0_weights, "iq4_nl": iq4_nl_weights,
+           "q4_k": q4_k_weights}
 
 
 def weight_copies(fmt, n, k, gen, torch, total=COLD_BYTES):
@@ -308,7 +321,8 @@ DETAIL_SHAPES = (  # (fmt, n, k, m)
     ("tq2_0", 2560, 6912, 1), ("tq2_0", 6912, 2560, 3), ("tq2_0", 32768, 8192, 1), ("q4_0", 4097, 4192, 1),
     ("tq2_0", 6913, 2816, 1), ("q8_0", 4096, 4096, 1), ("q8_0", 14336, 4096, 1), ("q8_0", 4096, 14336, 1),
     ("q8_0", 128256, 4096, 1), ("iq4_nl", 4096, 4096, 1), ("iq4_nl", 14336, 4096, 1), ("iq4_nl", 4096, 14336, 1),
-    ("iq4_nl", 28672, 8192, 1),
+    ("iq4_nl", 28672, 8192, 1), ("q4_k", 4096, 4096, 1), ("q4_k", 14336, 4096, 1), ("q4_k", 4096, 14336, 1),
+    ("q4_k", 128256, 4096, 1), ("q4_k", 14336, 4096, 3),
 )  # fmt: skip
 
 
@@ -461,6 +475,7 @@ INGEST_CASES = (  # (name, fmt, N, K): one weight matrix's ggml block bytes, spl
     ("llama3_8b_ffn_gate", "q4_0", 14336, 4096),
     ("llama3_8b_lm_head", "q4_0", 128256, 4096),
     ("llama3_8b_ffn_gate", "q8_0", 14336, 4096),
+    ("llama3_8b_ffn_gate", "q4_k", 14336, 4096),
     ("bitnet2b_ffn_gate", "tq2_0", 6912, 2560),
 )
 
@@ -478,7 +493,7 @@ def ingest_detail(torch, host, args):
         ncopy = max(2, math.ceil((COLD_BYTES // 2) / size))
         blocks = [torch.randint(0, 256, (size,), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(ncopy)]
         wq = torch.empty((n, nb * f["qbytes"]), dtype=torch.uint8, device="cuda")
-        ws = torch.empty((n, nb), dtype=torch.int16, device="cuda")
+        ws = torch.empty((n, nb * f["sbytes"] // 2), dtype=torch.int16, device="cuda")
 
         def call(i, blocks=blocks, wq=wq, ws=ws, fmt=fmt, n=n, k=k):
             host.split_into(fmt, blocks[i % len(blocks)], wq, ws, n, k)
@@ -486,7 +501,7 @@ def ingest_detail(torch, host, args):
         per_graph = ncopy * math.ceil(16 / ncopy)
         reps = 2 * per_graph
         ms, _ = timed_steps(torch, call, ncopy, reps, per_graph)
-        b = size + n * nb * (f["qbytes"] + 2)
+        b = size + n * nb * (f["qbytes"] + f["sbytes"])
         us = ms * 1e3 / reps
         rows.append({"case": name, "fmt": fmt, "n": n, "k": k, "bytes": b, "us": round(us, 3),
                      "gbs": round(b / us / 1e3, 1), "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1),

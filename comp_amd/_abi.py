@@ -17,7 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkomp_hip.so")
 
 KOMP_OK, KOMP_EINVAL, KOMP_EHIP = 0, 1, 2
-TIMING_KINDS = ("quant_q8_0", "quant_q8_K", "q4_0_gemv", "tq2_0_gemv", "probe", "q8_0_gemv", "iq4_nl_gemv")
+TIMING_KINDS = ("quant_q8_0", "quant_q8_K", "q4_0_gemv", "tq2_0_gemv", "probe", "q8_0_gemv", "iq4_nl_gemv",
+                "q4_k_gemv")
 
 
 class KompError(RuntimeError):
@@ -53,6 +54,10 @@ SIGNATURES = {
        for f in ("q8_0", "iq4_nl")},
     **{f"komp_{f}_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]) for f in ("q8_0", "iq4_nl")},
     **{f"komp_{f}_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]) for f in ("q8_0", "iq4_nl")},
+    "komp_q4_k_gemv": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_q4_k_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_q4_k_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
+    "komp_q4_k_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "komp_q4_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_tq2_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_gemm_plan": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _P]),

@@ -122,19 +122,22 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   if (m == 1 && mode == KOMP_MODE_DP4A && (fused || fmt == FMT_TQ2_0)) {
     const int cus = device_cus();
     const int64_t rows = n < 1 ? 1 : (n + cus - 1) / cus;
+    const int lpr_min = bpb > 4 ? bpb : 4;  // a row group holds whole blocks
     int lpr = 64;
-    while (lpr > 4 && ((rows + 64 / lpr - 1) / (64 / lpr) > 16 || 2 * chunks < 3 * lpr)) lpr >>= 1;
+    while (lpr > lpr_min && ((rows + 64 / lpr - 1) / (64 / lpr) > 16 || 2 * chunks < 3 * lpr)) lpr >>= 1;
     const int rpp = 64 / lpr;
     const int64_t waves = (rows + rpp - 1) / rpp;
     if (waves <= 16) {
       const int64_t blocks_per_slot = lpr / bpb;
+      const int nb_max = fmt == FMT_Q4_K ? 4 : 8;  // the 16-wave instantiations (Q4_K: 4 VGPRs of scales per slot)
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
-      nb = nb < 1 ? 1 : (nb > 8 ? 8 : nb);
+      nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
       return plan_of(static_cast<int>(rows), nb, static_cast<int>(waves), lpr, 1);
     }
   }
   int lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
   lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
+  if (lpr < bpb) lpr = bpb;  // a row group holds whole blocks (Q4_K: 8 chunks)
   const int64_t blocks_per_slot = lpr / bpb;
   int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
   nb = nb < 1 ? 1 : (nb > 16 ? 16 : nb);
@@ -174,6 +177,7 @@ constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (
 // (4096x4096, 14336x4096, 4096x14336, 128256x4096) and BitNet-2B shapes, 1..64 columns.  False when the shape is past
 // the kernel's 32-bit buffer offsets (64 * K and 32 * SW below 2^31) or its scale slab does not fit in LDS.
 bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p) {
+  if (fmt == FMT_Q4_K) return false;  // no matrix-core path for Q4_K: its batches run on the GEMV
   if (64 * k > INT32_MAX || 32 * sw > INT32_MAX) return false;
   const int64_t c16 = (m + 15) / 16;
   const int64_t groups = (c16 + 3) / 4;
@@ -240,8 +244,11 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     if (!in_set(block_n, kBlockN, 5)) return fail(KOMP_EINVAL, "%s: block_n=%d not in {8,16,32,64,128}", name, block_n);
     if (!in_set(nb, kNb, 5)) return fail(KOMP_EINVAL, "%s: nb=%d not in {1,2,4,8,16}", name, nb);
     if (!in_set(num_warps, kWarps, 4)) return fail(KOMP_EINVAL, "%s: num_warps=%d not in {1,2,4,8}", name, num_warps);
+    if (fmt == FMT_Q4_K && block_n / num_warps > 8)  // a row group of 64 / rows-per-wave lanes holds 8-chunk blocks
+      return fail(KOMP_EINVAL, "%s: block_n / num_warps = %d rows per wave; q4_k takes at most 8", name,
+                  block_n / num_warps);
   }
-  if (fused && fmt != FMT_TQ2_0 && a.xb_out != nullptr)
+  if (fused && blk != 256 && a.xb_out != nullptr)
     return fail(KOMP_EINVAL, "%s: XB (bsums) is a q8_K plane; pass NULL for q8_0 activations", name);
   if (fused && a.xq_out == nullptr && (a.xd_out != nullptr || a.xb_out != nullptr))
     return fail(KOMP_EINVAL, "%s: XD / XB outputs need XQ as well", name);
@@ -264,6 +271,8 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     if (!aligned(w.wq, 16)) return fail(KOMP_EINVAL, "%s: WQ must be 16-byte aligned", name);
     if (!aligned(w.ws, 2) || !aligned(w.y, 4) || !aligned(w.s, 4))
       return fail(KOMP_EINVAL, "%s: WS, Y and S must be aligned to their element size", name);
+    if (fmt == FMT_Q4_K && !aligned(w.ws, 16))  // its 16-byte scale-plane entries are read whole
+      return fail(KOMP_EINVAL, "%s: WS must be 16-byte aligned for q4_k", name);
     mats[count++] = w;
   }
   const int64_t nblk = K / blk;
@@ -319,7 +328,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     c.xd_out = a.xd_out != nullptr ? a.xd_out + m0 * nblk : nullptr;
     c.xb_out = a.xb_out != nullptr ? a.xb_out + m0 * (K / 16) : nullptr;
     c.y = mats[0].y + m0 * mats[0].n;
-    c.s = mats[0].s != nullptr ? mats[0].s + m0 * mats[0].n * nblk : nullptr;
+    c.s = mats[0].s != nullptr ? mats[0].s + m0 * mats[0].n * nblk * s_per_block(fmt) : nullptr;
     c.m = static_cast<int>(M - m0 < mc ? M - m0 : mc);
     c.n = static_cast<int>(mats[0].n);
     c.k = static_cast<int>(K);
@@ -343,7 +352,7 @@ int gemv_multi_entry(int fmt, int count, const uint8_t* const* WQ, const int16_t
                      const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X, int64_t M,
                      int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
   static const char* const names[] = {"komp_q4_0_gemv_multi", "komp_tq2_0_gemv_multi", "komp_q8_0_gemv_multi",
-                                      "komp_iq4_nl_gemv_multi"};
+                                      "komp_iq4_nl_gemv_multi", "komp_q4_k_gemv_multi"};
   const char* name = names[fmt];
   if (count < 1 || count > kMaxSegs) return fail(KOMP_EINVAL, "%s: count=%d must be 1..%d", name, count, kMaxSegs);
   if (WQ == nullptr || WS == nullptr || Y == nullptr || N == nullptr || SW == nullptr)
@@ -457,8 +466,9 @@ int split_entry(int fmt, const char* name, const uint8_t* W, uint8_t* WQ, int16_
                 (long long)SW, (long long)row_bytes);
   if (N == 0 || K == 0) return KOMP_OK;
   if (W == nullptr || WQ == nullptr || WS == nullptr) return fail(KOMP_EINVAL, "%s: NULL pointer", name);
-  if (!aligned(W, 4) || !aligned(WQ, 16) || !aligned(WS, 2))
-    return fail(KOMP_EINVAL, "%s: W must be 4-byte aligned, WQ 16-byte aligned, WS 2-byte aligned", name);
+  if (!aligned(W, 4) || !aligned(WQ, 16) || !aligned(WS, fmt == FMT_Q4_K ? 16 : 2))
+    return fail(KOMP_EINVAL, "%s: W must be 4-byte aligned, WQ 16-byte aligned, WS %d-byte aligned", name,
+                fmt == FMT_Q4_K ? 16 : 2);
   return hip_status(launch_split(fmt, W, WQ, WS, N, K, SW, static_cast<hipStream_t>(stream)), name);
 }
 }  // namespace
@@ -487,7 +497,7 @@ int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, cons
 
 int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
                    int* waves) {
-  if (fmt < FMT_Q4_0 || fmt > FMT_IQ4_NL) return fail(KOMP_EINVAL, "komp_gemm_plan: fmt=%d", fmt);
+  if (fmt < FMT_Q4_0 || fmt > FMT_Q4_K) return fail(KOMP_EINVAL, "komp_gemm_plan: fmt=%d", fmt);
   if (M < 1 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemm_plan: bad argument");
   GemmPlan p;
   if (!gemm_plan(fmt, M < kGemmMaxCols ? M : kGemmMaxCols, N, K, SW, &p))
@@ -545,9 +555,36 @@ KOMP_FORMAT_ENTRIES(q8_0, FMT_Q8_0)
 KOMP_FORMAT_ENTRIES(iq4_nl, FMT_IQ4_NL)
 #undef KOMP_FORMAT_ENTRIES
 
+// ---- Q4_K (q8_K activations): TQ2_0's entries, S with two int32 per block ----
+int komp_q4_k_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                   void* stream) {
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_Q4_K, false, "komp_q4_k_gemv", a, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_k_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                       float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                       int mode, int num_warps, void* stream) {
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, nullptr, nullptr, X, XQ, XD, XB};
+  return gemv_entry(FMT_Q4_K, true, "komp_q4_k_gemv_f32", a, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_k_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                         const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                         int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
+  return gemv_multi_entry(FMT_Q4_K, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_k_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream) {
+  return split_entry(FMT_Q4_K, "komp_q4_k_split", W, WQ, WS, N, K, SW, stream);
+}
+
 int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
                           int* num_warps, int* lanes_per_row, int* passes) {
-  if (fmt < FMT_Q4_0 || fmt > FMT_IQ4_NL) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
+  if (fmt < FMT_Q4_0 || fmt > FMT_Q4_K) return fail(KOMP_EINVAL, "komp_gemv_auto_config: fmt=%d", fmt);
   if (mode < KOMP_MODE_BYTES || mode > KOMP_MODE_DP4A)
     return fail(KOMP_EINVAL, "komp_gemv_auto_config: mode=%d not in {0,1,2}", mode);
   if (M < 1 || N < 0 || K < 0 || block_n == nullptr || nb == nullptr || num_warps == nullptr)

@@ -30,6 +30,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "komp_device.h"
 #include "komp_internal.h"
 
@@ -104,6 +106,44 @@ __device__ __forceinline__ int q8_0_chunk_dot(u32x4 w, u32x4 x) {
   return s;
 }
 
+// Q4_K: the two int32 dots of one 16-byte chunk, whose low nibbles are 16 values of one 32-value sub-block
+// (activations xl) and whose high nibbles the matching 16 values of the next (xh); the nibbles are unsigned, the
+// sub-block's min enters through its own term.
+template <int MODE>
+__device__ __forceinline__ int2 q4_k_chunk_dots(u32x4 w, u32x4 xl, u32x4 xh) {
+  int lo = 0, hi = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (MODE == MODE_BYTES) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo += static_cast<int>((w[d] >> (8 * e)) & 15u) * sbyte(xl[d], e);
+        hi += static_cast<int>((w[d] >> (8 * e + 4)) & 15u) * sbyte(xh[d], e);
+      }
+    } else {
+      lo = dot4<MODE>(w[d] & NIB, xl[d], lo);
+      hi = dot4<MODE>((w[d] >> 4) & NIB, xh[d], hi);
+    }
+  }
+  return make_int2(lo, hi);
+}
+
+// Q4_K: the 6-bit scales and mins of sub-blocks 2j and 2j+1 from a block's 16 scale-plane bytes (dword 0: f16 d and
+// dmin; dwords 1..3: the 12 packed bytes), as {scale 2j, scale 2j+1, min 2j, min 2j+1} in bytes 0..3.  Sub-blocks
+// 0..3 keep their scale and min in the low 6 bits of bytes 0..3 and 4..7; sub-blocks 4..7 in the low and high nibble
+// of bytes 8..11, with the top two bits of bytes 0..3 (scales) and 4..7 (mins) above them (ggml get_scale_min_k4).
+// hi: all ones for j >= 2; sel: the v_perm selector that takes bytes 2(j&1), 2(j&1)+1 of the scales, then of the
+// mins.  Both are constants of the lane; the two forms are blended bit-wise (v_bfi_b32), so the wave never branches.
+__device__ __forceinline__ unsigned q4_k_scale_pair(u32x4 meta, unsigned hi, unsigned sel) {
+  const unsigned u0 = meta[1], u1 = meta[2], u2 = meta[3];
+  const unsigned sc_lo = u0 & 0x3F3F3F3Fu, mn_lo = u1 & 0x3F3F3F3Fu;
+  const unsigned sc_hi = (u2 & 0x0F0F0F0Fu) | ((u0 >> 2) & 0x30303030u);
+  const unsigned mn_hi = ((u2 >> 4) & 0x0F0F0F0Fu) | ((u1 >> 2) & 0x30303030u);
+  const unsigned sc = (sc_hi & hi) | (sc_lo & ~hi);
+  const unsigned mn = (mn_hi & hi) | (mn_lo & ~hi);
+  return __builtin_amdgcn_perm(mn, sc, sel);
+}
+
 // TQ2_0: partial int32 dot of one 16-byte chunk.  Byte t of the chunk holds, at bits 2j, the value whose activation
 // is byte t of x[j].  `init` joins the x1 accumulator.
 template <int MODE>
@@ -133,11 +173,12 @@ __device__ __forceinline__ int tq2_0_chunk_dot(u32x4 w, const u32x4 (&x)[4], int
   }
 }
 
-// Largest workgroup an instantiation is built for.  One activation column in dp4a mode with nb <= 8 fits 16 waves
-// (at most 128 VGPRs per wave), which the one-workgroup-per-CU plans of small GEMVs use; the others stay at 8.
+// Largest workgroup an instantiation is built for.  One activation column in dp4a mode with nb <= 8 (Q4_K, whose
+// 16-byte scale entries take 4 VGPRs per chunk slot: nb <= 4) fits 16 waves (at most 128 VGPRs per wave), which the
+// one-workgroup-per-CU plans of small GEMVs use; the others stay at 8.
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 constexpr int max_threads() {
-  return (MC == 1 && MODE == MODE_DP4A && NB <= 8) ? 1024 : 512;
+  return (MC == 1 && MODE == MODE_DP4A && NB <= (FMT == FMT_Q4_K ? 4 : 8)) ? 1024 : 512;
 }
 
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
@@ -159,9 +200,12 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   // nseg > 1: several matrices sharing the input; the workgroup takes its matrix from segs (scalar compares on the
   // argument block) and from there on works as for one matrix, on its row range within it.
   extern __shared__ __align__(16) unsigned char lds[];
-  constexpr bool BLK32 = FMT != FMT_TQ2_0;  // 32-value blocks with q8_0 activations (Q4_0, Q8_0, IQ4_NL)
-  constexpr int BB = FMT == FMT_TQ2_0 ? 64 : (FMT == FMT_Q8_0 ? 32 : 16);  // quant bytes per block
-  constexpr int CPB_LOG2 = FMT == FMT_TQ2_0 ? 2 : (FMT == FMT_Q8_0 ? 1 : 0);  // log2(16-byte chunks per block)
+  constexpr bool QK = FMT == FMT_Q4_K;
+  constexpr bool BLK32 = FMT != FMT_TQ2_0 && !QK;  // 32-value blocks with q8_0 activations (Q4_0, Q8_0, IQ4_NL)
+  constexpr int BB = FMT == FMT_TQ2_0 ? 64 : QK ? 128 : (FMT == FMT_Q8_0 ? 32 : 16);  // quant bytes per block
+  constexpr int CPB_LOG2 = FMT == FMT_TQ2_0 ? 2 : QK ? 3 : (FMT == FMT_Q8_0 ? 1 : 0);  // log2(16-byte chunks/block)
+  constexpr int SCW = QK ? 8 : 1;  // int16 of the scale plane per block (Q4_K: d, dmin and 12 scale bytes)
+  constexpr int SPB = QK ? 2 : 1;  // int32 of S per block (Q4_K: the scaled dot and the mins dot)
   int N = N1;
   int64_t SW = SW1;
   const uint8_t* __restrict__ WQ = WQ1;
@@ -193,15 +237,16 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);  // wave-uniform, may be <= 0
   const int bpg = lpr >> CPB_LOG2;                       // blocks a row group covers per chunk slot
   const int bstep = bpg * NB;                            // blocks a row group covers per K step
-  const int q = gl & ((1 << CPB_LOG2) - 1);              // Q8_0, TQ2_0: chunk of the block this lane loads
+  const int q = gl & ((1 << CPB_LOG2) - 1);              // Q8_0, TQ2_0, Q4_K: chunk of the block this lane loads
   const int gblk = gl >> CPB_LOG2;                       // block offset of this lane within a slot
   const int tiles = passes * nsteps;
   // per-lane byte offsets within a row group's tile (row grp of the group, block gblk, chunk q)
   const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + q * 16;
-  const int64_t lane_s = static_cast<int64_t>(grp) * nblk + gblk;
+  const int64_t lane_s = (static_cast<int64_t>(grp) * nblk + gblk) * SCW;
 
+  using ScT = std::conditional_t<QK, u32x4, int16_t>;  // one block's scale-plane entry
   u32x4 w[NB];
-  int16_t sc[NB];
+  ScT sc[NB];
   const bool sc_global = sc_mode == 0;
   auto load_tile = [&](int t) {
     const int p = t / nsteps;
@@ -210,16 +255,19 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
     const bool rv = rl < wave_rows && row_base + rl < N;
     const int64_t row0 = static_cast<int64_t>(row_base) + p * rows_per_pass;  // wave-uniform
     const uint8_t* wt = WQ + row0 * SW + static_cast<int64_t>(st) * bstep * BB + lane_w;
-    const int16_t* stp = WS + row0 * nblk + st * bstep + lane_s;
+    const int16_t* stp = WS + (row0 * nblk + st * bstep) * SCW + lane_s;
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int b = st * bstep + u * bpg + gblk;
       if (rv && b < nblk) {
         w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + static_cast<int64_t>(u) * bpg * BB));
-        sc[u] = sc_global ? stp[u * bpg] : static_cast<int16_t>(0);
+        if constexpr (QK)
+          sc[u] = sc_global ? *reinterpret_cast<const u32x4*>(stp + u * bpg * SCW) : u32x4{0u, 0u, 0u, 0u};
+        else
+          sc[u] = sc_global ? stp[u * bpg] : static_cast<int16_t>(0);
       } else {
         w[u] = u32x4{0u, 0u, 0u, 0u};
-        sc[u] = 0;
+        sc[u] = ScT{};
       }
     }
   };
@@ -232,9 +280,12 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   // TQ2_0: x4[m][j][b][q] = the 16 activations that pair with crumb j of chunk q; meta[m][b] = {d_x bits, -sum(x)}.
   // Then (sc_mode 1) the scale slab [waves * rows_per_wave][nblk] (rows past the workgroup's are never loaded nor
   // used), 16-byte aligned (the activation bytes are a multiple of 8).
+  // Q4_K: xk[m][p][b] = activation piece p (bytes 16p..16p+15) of block b, meta[m][b] = {d_x bits, 0}, then
+  // bs[m][b][p] = the int32 sum of piece p (the q8_K bsums).
   u32x4* xv = reinterpret_cast<u32x4*>(lds);
   int2* meta = reinterpret_cast<int2*>(xv + (BLK32 ? 2 : 16) * MC * nblk);
-  u32x4* scs16 = xv + ((MC * nblk * (BLK32 ? 40 : 264) + 15) >> 4);
+  int* bs = reinterpret_cast<int*>(meta + MC * nblk);  // Q4_K only
+  u32x4* scs16 = xv + ((MC * nblk * (BLK32 ? 40 : QK ? 328 : 264) + 15) >> 4);
   const int16_t* scs = reinterpret_cast<const int16_t*>(scs16);
 
   // Then the scale slab (sc_mode 1): each wave copies 1 KB pieces of it from global memory straight into LDS
@@ -243,8 +294,8 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
   if (sc_mode == 1) {
     const int wg_row0 = wg * rows_per_wg;
     const int sc_rows = min(rows_per_wg, N - wg_row0);
-    const int pieces = (sc_rows * nblk) >> 3;  // 16-byte pieces
-    const u32x4* src = reinterpret_cast<const u32x4*>(WS + static_cast<int64_t>(wg_row0) * nblk);
+    const int pieces = (sc_rows * nblk * SCW) >> 3;  // 16-byte pieces
+    const u32x4* src = reinterpret_cast<const u32x4*>(WS + static_cast<int64_t>(wg_row0) * nblk * SCW);
     for (int c = wave * 64; c < pieces; c += nthreads) {  // wave-uniform
       if (c + lane < pieces)
         __builtin_amdgcn_global_load_lds(src + c + lane, reinterpret_cast<__attribute__((address_space(3))) void*>(
@@ -354,16 +405,32 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
           const int mb = i >> 4;
           const int m = mb / nblk;
           const int b = mb - m * nblk;
-          const int j = (p >> 1) & 3;
-          const int qq = ((p >> 3) << 1) | (p & 1);
-          xv[((m * 4 + j) * nblk + b) * 4 + qq] = a[u];
-          int sum = 0;
-          if constexpr (MODE != MODE_BYTES) {
+          if constexpr (QK) {
+            xv[(m * 16 + p) * nblk + b] = a[u];
+            int sum = 0;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) sum = dot4<MODE>(a[u][d], ONES, sum);
-            sum = group_sum(sum, 16);
+            for (int d = 0; d < 4; ++d) {
+              if constexpr (MODE == MODE_BYTES) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += sbyte(a[u][d], e);
+              } else {
+                sum = dot4<MODE>(a[u][d], ONES, sum);
+              }
+            }
+            bs[mb * 16 + p] = sum;
+            if (p == 0) meta[mb] = make_int2(__float_as_int(dxs[u]), 0);
+          } else {
+            const int j = (p >> 1) & 3;
+            const int qq = ((p >> 3) << 1) | (p & 1);
+            xv[((m * 4 + j) * nblk + b) * 4 + qq] = a[u];
+            int sum = 0;
+            if constexpr (MODE != MODE_BYTES) {
+#pragma unroll
+              for (int d = 0; d < 4; ++d) sum = dot4<MODE>(a[u][d], ONES, sum);
+              sum = group_sum(sum, 16);
+            }
+            if (p == 0) meta[mb] = make_int2(__float_as_int(dxs[u]), -sum);
           }
-          if (p == 0) meta[mb] = make_int2(__float_as_int(dxs[u]), -sum);
         }
       }
     }
@@ -397,10 +464,16 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
           float d;
           int qsum;
           const int bsum = q8_K_row16(v[u], r, qv, d, qsum);
-          const int j = (r & 7) >> 1;
-          const int qq = ((r >> 3) << 1) | (r & 1);
-          xv[((m * 4 + j) * nblk + b) * 4 + qq] = qv;
-          if (r == 0) meta[mb] = make_int2(__float_as_int(d), -qsum);
+          if constexpr (QK) {
+            xv[(m * 16 + r) * nblk + b] = qv;
+            bs[mb * 16 + r] = bsum;
+            if (r == 0) meta[mb] = make_int2(__float_as_int(d), 0);
+          } else {
+            const int j = (r & 7) >> 1;
+            const int qq = ((r >> 3) << 1) | (r & 1);
+            xv[((m * 4 + j) * nblk + b) * 4 + qq] = qv;
+            if (r == 0) meta[mb] = make_int2(__float_as_int(d), -qsum);
+          }
           if (blockIdx.x == 0 && XQo != nullptr) {
             reinterpret_cast<u32x4*>(XQo + static_cast<int64_t>(m) * K + b * 256)[r] = qv;
             if (r == 0) XDo[static_cast<int64_t>(m) * nblk + b] = d;
@@ -428,18 +501,30 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
     if (!sc_global) {
       // this tile's scales from the LDS slab (a lane of an idle row reads a slab row that was not loaded; its results
       // are never stored)
-      const int16_t* scr = scs + (wave * rows_per_wave + rl) * nblk;
+      const int16_t* scr = scs + (wave * rows_per_wave + rl) * nblk * SCW;
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const int b = st * bstep + u * bpg + gblk;
-        sc[u] = b < nblk ? scr[b] : static_cast<int16_t>(0);
+        if constexpr (QK)
+          sc[u] = b < nblk ? *reinterpret_cast<const u32x4*>(scr + b * SCW) : u32x4{0u, 0u, 0u, 0u};
+        else
+          sc[u] = b < nblk ? scr[b] : static_cast<int16_t>(0);
       }
     }
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int b = st * bstep + u * bpg + gblk;
       if (b < nblk) {
-        const float dw = f16_bits_to_f32(sc[u]);
+        float dw, dmin = 0.0f;
+        unsigned scm = 0;
+        if constexpr (QK) {
+          dw = f16_bits_to_f32(static_cast<int16_t>(sc[u][0] & 0xFFFFu));
+          dmin = f16_bits_to_f32(static_cast<int16_t>(sc[u][0] >> 16));
+          const unsigned jb = 2u * ((q >> 1) & 1);  // byte of sub-block 2j within its dword
+          scm = q4_k_scale_pair(sc[u], (q >> 1) >= 2 ? ~0u : 0u, jb | ((jb + 1) << 8) | ((jb + 4) << 16) | ((jb + 5) << 24));
+        } else {
+          dw = f16_bits_to_f32(sc[u]);
+        }
 #pragma unroll
         for (int m = 0; m < MC; ++m) {
           const int2 mt = meta[m * nblk + b];
@@ -450,6 +535,29 @@ gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_
                                           : iq4_nl_block_dot<MODE>(w[u], xl, xh);
             if (S != nullptr && rv) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
             acc[m] += static_cast<float>(s) * dw * dx;  // kernels.py:93 order
+          } else if constexpr (QK) {
+            // lane octet: chunk q = 2j + h holds values 64j + 16h + e (sub-block 2j, low nibbles) and 64j + 32 + 16h
+            // + e (sub-block 2j + 1, high nibbles), e < 16: activation pieces 4j + h and 4j + 2 + h
+            const int j = q >> 1, h = q & 1;
+            const int2 dd = q4_k_chunk_dots<MODE>(w[u], xv[(m * 16 + 4 * j + h) * nblk + b],
+                                                  xv[(m * 16 + 4 * j + 2 + h) * nblk + b]);
+            const int* bsr = bs + (m * nblk + b) * 16;
+            // 24-bit multiplies (full rate): |dots| < 2^15, |bsums| < 2^12, scales and mins < 64
+            const int sd = __mul24(static_cast<int>(scm & 0xFFu), dd.x) + __mul24(static_cast<int>((scm >> 8) & 0xFFu), dd.y);
+            const int sm = __mul24(static_cast<int>((scm >> 16) & 0xFFu), bsr[4 * j + h]) +
+                           __mul24(static_cast<int>(scm >> 24), bsr[4 * j + 2 + h]);
+            if (S != nullptr) {  // the block's exact (sd, sm): the octet's partial sums added
+              const int sdb = group_sum(sd, 8), smb = group_sum(sm, 8);
+              if (rv && q == 0) {
+                int32_t* sp = S + ((static_cast<int64_t>(m) * N + row) * nblk + b) * SPB;
+                sp[0] = sdb;
+                sp[1] = smb;
+              }
+            }
+            // y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K), each lane adding its chunk's part (the
+            // lane sums meet in the row reduction), so Y does not depend on whether S is stored
+            acc[m] = __builtin_fmaf(static_cast<float>(sd), dw * dx, acc[m]);
+            acc[m] = __builtin_fmaf(-static_cast<float>(sm), dmin * dx, acc[m]);
           } else if constexpr (FMT == FMT_Q8_0) {
             // lane pair: chunk q holds the block's values 16q .. 16q+15, dotted with the matching staged half
             const int s = group_sum(q8_0_chunk_dot<MODE>(w[u], xv[(q * MC + m) * nblk + b]), 2);
@@ -499,11 +607,12 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   // the workgroup's scale slab goes to LDS when it is small (the weight stream then issues only quant loads)
   const size_t base = gemv_lds_bytes(FMT, MC, c.k);
   const size_t sc_off = (base + 15) & ~static_cast<size_t>(15);
-  const size_t sc_bytes = static_cast<size_t>(p.waves) * p.rows_per_wave * nblk * 2;  // every wave's row slots
+  const int scw = fmt_info(FMT).sbytes / 2;  // int16 of the scale plane per block
+  const size_t sc_bytes = static_cast<size_t>(p.waves) * p.rows_per_wave * nblk * 2 * scw;  // every wave's row slots
   int sc_mode = 0;
   bool ws_aligned = reinterpret_cast<uintptr_t>(c.ws) % 16 == 0;
   for (int i = 0; c.nseg > 1 && i < c.nseg; ++i) ws_aligned = ws_aligned && reinterpret_cast<uintptr_t>(segs.ws[i]) % 16 == 0;
-  if (nblk > 0 && nblk % 8 == 0 && ws_aligned && sc_bytes <= kScaleSlabMax && sc_off + sc_bytes <= kLdsLimit)
+  if (nblk > 0 && (nblk * scw) % 8 == 0 && ws_aligned && sc_bytes <= kScaleSlabMax && sc_off + sc_bytes <= kLdsLimit)
     sc_mode = 1;
   const unsigned lds = static_cast<unsigned>(sc_mode != 0 ? sc_off + sc_bytes : base);
   static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel

@@ -1,4 +1,4 @@
-// Unfused GEMV launches for the Q8_0 and IQ4_NL weight formats (q8_0 activations in); the kernel template is in
+// Unfused GEMV launches for the Q8_0 and IQ4_NL weight formats (Q4_K: gemv_q4_k.hip) (q8_0 activations in); the kernel template is in
 // gemv_kernel.h.  A translation unit of their own, so the library's instantiations compile in parallel.
 #include "gemv_kernel.h"
 
@@ -7,6 +7,7 @@ namespace komp {
 hipError_t launch_gemv_more(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, false>(c, p, stream);
   if (c.fmt == FMT_IQ4_NL) return gemv_impl::by_mode<FMT_IQ4_NL, false>(c, p, stream);
+  if (c.fmt == FMT_Q4_K) return launch_gemv_q4_k(c, p, stream);
   return hipErrorInvalidValue;
 }
 

@@ -6,23 +6,28 @@
 
 namespace komp {
 
-enum Fmt { FMT_Q4_0 = 0, FMT_TQ2_0 = 1, FMT_Q8_0 = 2, FMT_IQ4_NL = 3 };
+enum Fmt { FMT_Q4_0 = 0, FMT_TQ2_0 = 1, FMT_Q8_0 = 2, FMT_IQ4_NL = 3, FMT_Q4_K = 4 };
 
-// Per-format constants: values per block, ggml block bytes, quant bytes per block and their offset, scale offset.
+// Per-format constants: values per block, ggml block bytes, quant bytes per block and their offset, scale offset,
+// scale-plane bytes per block (the f16 scale; Q4_K: d, dmin and the 12 bytes of 6-bit sub-block scales and mins).
 struct FmtInfo {
   int block;
   int nbytes;
   int qbytes;
   int qoff;
   int soff;
+  int sbytes;
 };
 inline FmtInfo fmt_info(int fmt) {
   switch (fmt) {
-    case FMT_TQ2_0: return FmtInfo{256, 66, 64, 0, 64};
-    case FMT_Q8_0: return FmtInfo{32, 34, 32, 2, 0};
-    default: return FmtInfo{32, 18, 16, 2, 0};  // Q4_0, IQ4_NL
+    case FMT_TQ2_0: return FmtInfo{256, 66, 64, 0, 64, 2};
+    case FMT_Q8_0: return FmtInfo{32, 34, 32, 2, 0, 2};
+    case FMT_Q4_K: return FmtInfo{256, 144, 128, 16, 0, 16};
+    default: return FmtInfo{32, 18, 16, 2, 0, 2};  // Q4_0, IQ4_NL
   }
 }
+// int32 of S per block: the exact block dot, or (Q4_K) the scaled dot and the mins dot
+inline int s_per_block(int fmt) { return fmt == FMT_Q4_K ? 2 : 1; }
 
 // Kernel kinds, for the per-dispatch timing of the tuning harness.
 enum Kind {
@@ -33,12 +38,14 @@ enum Kind {
   KIND_PROBE = 4,
   KIND_Q8_0_GEMV = 5,
   KIND_IQ4_NL_GEMV = 6,
-  KIND_COUNT = 7
+  KIND_Q4_K_GEMV = 7,
+  KIND_COUNT = 8
 };
 // the timing kind of a weight format's GEMV / GEMM launches
 constexpr int gemv_kind(int fmt) {
   return fmt == FMT_TQ2_0 ? KIND_TQ2_0_GEMV : fmt == FMT_Q8_0 ? KIND_Q8_0_GEMV
-                                           : fmt == FMT_IQ4_NL ? KIND_IQ4_NL_GEMV : KIND_Q4_0_GEMV;
+                                           : fmt == FMT_IQ4_NL ? KIND_IQ4_NL_GEMV
+                                           : fmt == FMT_Q4_K  ? KIND_Q4_K_GEMV : KIND_Q4_0_GEMV;
 }
 
 // Work decomposition of one GEMV launch (gemv_kernel.h describes the mapping of block_n / nb / num_warps).
@@ -121,6 +128,8 @@ hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream)
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_more(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_q4_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_q4_k_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
 hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,

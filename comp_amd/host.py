@@ -31,22 +31,39 @@ FORMATS = {  # weights: block values, block bytes, quant offset/bytes, scale off
     # ggml formats beyond the reference's two (its README.md:143 lists them as next): same planes, q8_0 activations
     "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
     "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
+    # ggml block_q4_K (d, dmin, 12 bytes of 6-bit sub-block scales and mins, 128 quant bytes) with q8_K activations;
+    # its scale plane keeps each block's first 16 bytes: WS int16 [N][8 * K/256], and S holds (sd, sm) per block
+    "q4_k": dict(block=256, nbytes=144, qoff=16, qbytes=128, soff=0, sbytes=16, act="q8_K"),
 }
+for _f in FORMATS.values():
+    _f.setdefault("sbytes", 2)  # scale-plane bytes per block
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
-FMT_ID = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3}
+FMT_ID = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}
+_XB_F32 = ("q4_0", "tq2_0", "q4_k")  # formats whose gemv_f32 entry takes the XB (bsums) output
 GEMM_MIN_M = {f: 4 for f in FMT_ID}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
 
 
 def split(fmt, W, n, k):
     """ggml blocks (bytes, n rows) -> (WQ uint8 [n][quant bytes per row], WS int16 [n][blocks]): KURN's split planes.
 
-    src/komp/host.py:16-22."""
+    src/komp/host.py:16-22.  q4_k: WS int16 [n][8 * blocks] (each block's d, dmin and 12 scale bytes)."""
     f = FORMATS[fmt]
     nb = k // f["block"]
+    sb = f["sbytes"]
     blocks = np.frombuffer(W, dtype=np.uint8).reshape(n, nb, f["nbytes"])
     wq = blocks[:, :, f["qoff"] : f["qoff"] + f["qbytes"]].reshape(n, nb * f["qbytes"]).copy()
-    ws = blocks[:, :, f["soff"] : f["soff"] + 2].copy().view(np.int16).reshape(n, nb)
+    ws = blocks[:, :, f["soff"] : f["soff"] + sb].copy().view(np.int16).reshape(n, nb * sb // 2)
     return wq, ws
+
+
+def _ws_cols(fmt, nblk):
+    """int16 columns of the scale plane for nblk blocks."""
+    return nblk * FORMATS[fmt]["sbytes"] // 2
+
+
+def _s_shape(fmt, m, n, nblk):
+    """Shape of S: int32 [M][N][blocks], q4_k [M][N][blocks][2] (the scaled dot sd and the mins dot sm)."""
+    return (m, n, nblk, 2) if fmt == "q4_k" else (m, n, nblk)
 
 
 def split_device(fmt, W, n, k, sw=None):
@@ -63,7 +80,7 @@ def split_device(fmt, W, n, k, sw=None):
     row = nb * f["qbytes"]
     sw = (row + 15) // 16 * 16 if sw is None else sw
     wq = torch.empty((n, sw), dtype=torch.uint8, device=W.device)
-    ws = torch.empty((n, nb), dtype=torch.int16, device=W.device)
+    ws = torch.empty((n, _ws_cols(fmt, nb)), dtype=torch.int16, device=W.device)
     split_into(fmt, W, wq, ws, n, k)
     return wq[:, :row], ws
 
@@ -76,8 +93,8 @@ def split_into(fmt, W, wq, ws, n, k):
     _need(wq, "wq", torch.uint8, 2)
     _need(ws, "ws", torch.int16, 2)
     nb = k // f["block"]
-    if tuple(ws.shape) != (n, nb) or not ws.is_contiguous():
-        raise _abi.KompArgumentError(f"split_into: ws must be a contiguous [{n}][{nb}] plane")
+    if tuple(ws.shape) != (n, _ws_cols(fmt, nb)) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"split_into: ws must be a contiguous [{n}][{_ws_cols(fmt, nb)}] plane")
     if wq.shape[0] != n or wq.shape[1] < nb * f["qbytes"] or (wq.numel() and wq.stride(1) != 1):
         raise _abi.KompArgumentError(f"split_into: wq must be [{n}][>= {nb * f['qbytes']}] with contiguous rows")
     if W.numel() != n * nb * f["nbytes"] or not W.is_contiguous():
@@ -196,8 +213,8 @@ def _check_gemv(fmt, wq, ws, xq, xd, n, k):
     if wq.numel() and wq.stride(1) != 1:
         raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
     nblk = k // f["block"]
-    if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
-        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{nblk}] plane, got {tuple(ws.shape)}")
+    if tuple(ws.shape) != (n, _ws_cols(fmt, nblk)) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{_ws_cols(fmt, nblk)}] plane, got {tuple(ws.shape)}")
     if wq.shape[0] != n or wq.shape[1] < nblk * f["qbytes"]:
         raise _abi.KompArgumentError(f"wq must be [{n}][>= {nblk * f['qbytes']}], got {tuple(wq.shape)}")
     m = xq.shape[0]
@@ -227,12 +244,14 @@ def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store
     src/komp/host.py:76-85.  block_n=None lets the library choose block_n, nb and num_warps for the shape."""
     m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
     y = torch.empty((m, n), dtype=torch.float32, device=xq.device)
-    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
+    s = torch.zeros(_s_shape(fmt, m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
     _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
     return y, s
 
 
 def _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k):
+    if fmt == "q4_k":
+        raise _abi.KompArgumentError("gemm: q4_k has no matrix-core GEMM; gemv runs its batches")
     fn = f"komp_{fmt}_gemm"
     with torch.cuda.device(xq.device):
         _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
@@ -314,9 +333,10 @@ def gemv_into(fmt, wq, ws, xq, xd, y, n, k, block_n=None, nb=4, mode=2, num_warp
     if tuple(y.shape) != (m, n) or not y.is_contiguous():
         raise _abi.KompArgumentError(f"gemv_into: y must be a contiguous [{m}][{n}] tensor")
     if s is not None:
-        _need(s, "s", torch.int32, 3)
-        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
-            raise _abi.KompArgumentError(f"gemv_into: s must be a contiguous [{m}][{n}][{nblk}] tensor")
+        shape = _s_shape(fmt, m, n, nblk)
+        _need(s, "s", torch.int32, len(shape))
+        if tuple(s.shape) != shape or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"gemv_into: s must be a contiguous {list(shape)} tensor")
     _launch_gemv(fmt, wq, ws, xq, xd, y, s, n, k, block_n, nb, mode, num_warps)
 
 
@@ -327,8 +347,8 @@ def _check_weights(fmt, wq, ws, n, k):
     if wq.numel() and wq.stride(1) != 1:
         raise _abi.KompArgumentError("wq rows must be contiguous (stride(1) == 1)")
     nblk = k // f["block"]
-    if tuple(ws.shape) != (n, nblk) or not ws.is_contiguous():
-        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{nblk}] plane, got {tuple(ws.shape)}")
+    if tuple(ws.shape) != (n, _ws_cols(fmt, nblk)) or not ws.is_contiguous():
+        raise _abi.KompArgumentError(f"ws must be a contiguous [{n}][{_ws_cols(fmt, nblk)}] plane, got {tuple(ws.shape)}")
     if wq.shape[0] != n or wq.shape[1] < nblk * f["qbytes"]:
         raise _abi.KompArgumentError(f"wq must be [{n}][>= {nblk * f['qbytes']}], got {tuple(wq.shape)}")
     return nblk
@@ -348,9 +368,10 @@ def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps
     if tuple(y.shape) != (m, n) or not y.is_contiguous():
         raise _abi.KompArgumentError(f"y must be a contiguous [{m}][{n}] tensor")
     if s is not None:
-        _need(s, "s", torch.int32, 3)
-        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
-            raise _abi.KompArgumentError(f"s must be a contiguous [{m}][{n}][{nblk}] tensor")
+        shape = _s_shape(fmt, m, n, nblk)
+        _need(s, "s", torch.int32, len(shape))
+        if tuple(s.shape) != shape or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"s must be a contiguous {list(shape)} tensor")
     ablk = FORMATS[fmt]["block"]
     for t, name, dt, shape in ((xq, "xq", torch.int8, (m, k)), (xd, "xd", torch.float32, (m, k // ablk)),
                                (xb, "xb", torch.int16, (m, k // 16))):  # fmt: skip
@@ -365,7 +386,7 @@ def gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n=None, nb=4, mode=2, num_warps
         block_n, nb, num_warps = 0, 0, 0
     fn = f"komp_{fmt}_gemv_f32"
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    planes = (ptr(xq), ptr(xd), ptr(xb)) if fmt in ("q4_0", "tq2_0") else (ptr(xq), ptr(xd))  # the others: no XB
+    planes = (ptr(xq), ptr(xd), ptr(xb)) if fmt in _XB_F32 else (ptr(xq), ptr(xd))  # the others: no XB
     if xb is not None and FORMATS[fmt]["act"] != "q8_K":
         raise _abi.KompArgumentError("xb (bsums) is a q8_K plane; pass None for q8_0 activations")
     with torch.cuda.device(x.device):
@@ -387,12 +408,12 @@ def gemv_f32(fmt, wq, ws, x, n, k, block_n=None, nb=4, mode=2, num_warps=4, stor
     if k % blk:
         raise _abi.KompArgumentError(f"{fmt}: K={k} is not a multiple of {blk}")
     y = torch.empty((m, n), dtype=torch.float32, device=x.device)
-    s = torch.zeros((m, n, k // blk), dtype=torch.int32, device=x.device) if store_s else None
+    s = torch.zeros(_s_shape(fmt, m, n, k // blk), dtype=torch.int32, device=x.device) if store_s else None
     q = None
     if return_q:
         q = (torch.empty((m, k), dtype=torch.int8, device=x.device),
              torch.empty((m, k // blk), dtype=torch.float32, device=x.device))  # fmt: skip
-        if fmt == "tq2_0":
+        if FORMATS[fmt]["act"] == "q8_K":
             q = q + (torch.empty((m, k // 16), dtype=torch.int16, device=x.device),)
     gemv_f32_into(fmt, wq, ws, x, y, n, k, block_n, nb, mode, num_warps, s, *(q or ()))
     return (y, s, q) if return_q else (y, s)

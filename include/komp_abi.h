@@ -131,8 +131,29 @@ int komp_iq4_nl_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, con
 int komp_q8_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
 int komp_iq4_nl_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
 
+/* Q4_K weights x q8_K activations: ggml's block_q4_K (README.md:143 lists it as a next format; no reference
+ * counterpart), with TQ2_0's entries and activation planes.
+ *   WQ u8 [N][SW] (128 quant bytes per 256-value block: byte 32j + l holds value 64j + l in its low nibble and
+ *      64j + 32 + l in its high nibble, SW >= K/2), WS i16 [N][8 K/256], 16-byte aligned (each block's first 16
+ *      bytes: f16 d, f16 dmin, 12 bytes of 6-bit sub-block scales and mins)                      (ggml block_q4_K)
+ *   S i32 [M][N][K/256][2] = (sd, sm): sd = sum_i sc_i * (dot of sub-block i), sm = sum_i m_i * (sum of the
+ *      activations of sub-block i), over the 8 sub-blocks of 32 values
+ *   Y[m][n] = sum_b f16(d) * d_x * sd - f16(dmin) * d_x * sm                        (ggml vec_dot_q4_K_q8_K)
+ * Explicit knobs need block_n / num_warps <= 8 (a row group holds whole 8-chunk blocks).  No matrix-core GEMM: with
+ * block_n == 0 every column count runs on the GEMV. */
+int komp_q4_k_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
+                   void* stream);
+int komp_q4_k_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, float* Y, int32_t* S, int8_t* XQ,
+                       float* XD, int16_t* XB, int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb,
+                       int mode, int num_warps, void* stream);
+int komp_q4_k_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
+                         const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
+                         int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+int komp_q4_k_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
+
 /* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0, 2 = q8_0,
- * 3 = iq4_nl; fused != 0 for
+ * 3 = iq4_nl, 4 = q4_k; fused != 0 for
  * komp_q4_0_gemv_f32 / komp_tq2_0_gemv_f32; mode as in the GEMV entries; M the activation columns.  block_n receives
  * the rows per workgroup, nb the 16-byte weight chunks each lane loads per row per K step, num_warps the waves per
  * workgroup, and (when not NULL) lanes_per_row the lanes that share a row and passes the row groups each wave walks
@@ -188,9 +209,9 @@ int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* strea
  * issued with hipExtLaunchKernel start/stop events, which the runtime stamps with the dispatch's own begin and end.
  * komp_timing_end() waits for those events and returns, per kernel kind, the summed dispatch time in milliseconds and
  * the dispatch count.  Kinds: 0 quant_q8_0, 1 quant_q8_K, 2 q4_0 GEMV / GEMM, 3 tq2_0 GEMV / GEMM, 4 probes and
- * weight splits, 5 q8_0 GEMV / GEMM, 6 iq4_nl GEMV / GEMM (arrays of length 7).
+ * weight splits, 5 q8_0 GEMV / GEMM, 6 iq4_nl GEMV / GEMM, 7 q4_k GEMV (arrays of length 8).
  * max_dispatches bounds the events created. */
-#define KOMP_TIMING_KINDS 7
+#define KOMP_TIMING_KINDS 8
 int komp_timing_begin(int64_t max_dispatches);
 int komp_timing_end(double* ms, int64_t* count);
 

@@ -22,6 +22,11 @@ How each function is pinned (tests/test_oracle_pins.py):
                          bytes; the table itself (ggml's kvalues_iq4nl) is parity unpinned: KURN, where COMP's
                          formats would be defined, is absent, so the table restates ggml's published constant
   tq2_0_values           all 256 byte values at every crumb position vs a per-value loop over the layout text
+  q4_k_values            all 256 byte values at 5 positions vs the dequantizer's loop order; random blocks
+  q4_k_scales            all 256 values of each of the 12 bytes vs two independent formulations (bit fields of the
+                         96-bit integer; ggml vec_dot's dword masks)
+  q4_k_block_dots        (sd, sm) vs brute-force loops over struct-built block_q4_K bytes, and d*dx*sd - dmin*dx*sm
+                         equal, in exact rationals, to the dot of the dequantized weights; a known-answer block
   dp4a                   the reference's 11 edge words + random words vs an independent struct-based byte dot
   round_half_*           vs Python's round()/Fraction on ties, negatives, huge and subnormal values
   quant_q8_0 / q8_K      vs an exact-rational (fractions.Fraction) implementation with explicit IEEE f32 rounding,
@@ -46,7 +51,12 @@ FORMATS = {
     # (ggml-common.h: block_q8_0 = f16 d + 32 int8; block_iq4_nl = f16 d + 16 bytes of 4-bit table indices)
     "q8_0": dict(block=32, nbytes=34, qoff=2, qbytes=32, soff=0, act="q8_0"),
     "iq4_nl": dict(block=32, nbytes=18, qoff=2, qbytes=16, soff=0, act="q8_0"),
+    # block_q4_K = f16 d, f16 dmin, 12 bytes of 6-bit sub-block scales and mins, 128 quant bytes; its split keeps the
+    # first 16 bytes (d, dmin, scales) as the scale plane: WS int16 [n][8 * blocks]
+    "q4_k": dict(block=256, nbytes=144, qoff=16, qbytes=128, soff=0, sbytes=16, act="q8_K"),
 }
+for _f in FORMATS.values():
+    _f.setdefault("sbytes", 2)  # scale-plane bytes per block
 # ggml's IQ4_NL value table (ggml-common.h kvalues_iq4nl): a fixed non-uniform 4-bit grid
 IQ4_NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int32)
 ACT_BLOCK = {"q8_0": 32, "q8_K": 256}
@@ -79,6 +89,33 @@ def iq4_nl_values(qs):
     (ggml dequantize_row_iq4_nl: the Q4_0 nibble order with the non-uniform table in place of nibble - 8)."""
     qs = np.asarray(qs, dtype=np.uint8)
     return np.concatenate([IQ4_NL_VALUES[qs & 15], IQ4_NL_VALUES[qs >> 4]], axis=-1)
+
+
+def q4_k_values(qs):
+    """[..., 128] q4_k quant bytes -> [..., 256] int32 in 0..15: byte 32j + l holds value 64j + l in its low nibble
+    and value 64j + 32 + l in its high nibble (ggml dequantize_row_q4_K)."""
+    qs = np.asarray(qs, dtype=np.uint8)
+    g = qs.reshape(*qs.shape[:-1], 4, 32)
+    v = np.stack([g & 15, g >> 4], axis=-2)  # [.., j, half, l] -> value 64j + 32 half + l
+    return v.reshape(*qs.shape[:-1], 256).astype(np.int32)
+
+
+def q4_k_scales(sc12):
+    """[..., 12] packed scale bytes of block_q4_K -> (scales [..., 8], mins [..., 8]) int32 in 0..63, ggml's
+    get_scale_min_k4: sub-block i < 4 takes the low 6 bits of byte i (scale) and byte i + 4 (min); i >= 4 takes the
+    low (scale) / high (min) nibble of byte i + 4 and, as bits 4..5, the top two bits of byte i - 4 (scale) / byte i
+    (min)."""
+    q = np.asarray(sc12, dtype=np.uint8).astype(np.int32)
+    sc = np.empty(q.shape[:-1] + (8,), dtype=np.int32)
+    mn = np.empty_like(sc)
+    for i in range(8):
+        if i < 4:
+            sc[..., i] = q[..., i] & 63
+            mn[..., i] = q[..., i + 4] & 63
+        else:
+            sc[..., i] = (q[..., i + 4] & 0xF) | ((q[..., i - 4] >> 6) << 4)
+            mn[..., i] = (q[..., i + 4] >> 4) | ((q[..., i] >> 6) << 4)
+    return sc, mn
 
 
 def tq2_0_values(qs):
@@ -192,17 +229,20 @@ def split(fmt, W, n, k):
     nb = k // f["block"]
     blocks = np.frombuffer(bytes(W), dtype=np.uint8).reshape(n, nb, f["nbytes"])
     wq = np.ascontiguousarray(blocks[:, :, f["qoff"] : f["qoff"] + f["qbytes"]]).reshape(n, nb * f["qbytes"])
-    ws = np.ascontiguousarray(blocks[:, :, f["soff"] : f["soff"] + 2]).view(np.int16).reshape(n, nb)
+    sb = f["sbytes"]
+    ws = np.ascontiguousarray(blocks[:, :, f["soff"] : f["soff"] + sb]).view(np.int16).reshape(n, nb * sb // 2)
     return wq, ws
 
 
 def join(fmt, wq, ws):
     """Inverse of split: split planes -> ggml block bytes."""
     f = FORMATS[fmt]
-    n, nb = ws.shape
+    sb = f["sbytes"]
+    n = ws.shape[0]
+    nb = ws.shape[1] * 2 // sb
     out = np.zeros((n, nb, f["nbytes"]), dtype=np.uint8)
     out[:, :, f["qoff"] : f["qoff"] + f["qbytes"]] = np.asarray(wq, np.uint8).reshape(n, nb, f["qbytes"])
-    out[:, :, f["soff"] : f["soff"] + 2] = np.ascontiguousarray(ws, dtype=np.int16).view(np.uint8).reshape(n, nb, 2)
+    out[:, :, f["soff"] : f["soff"] + sb] = np.ascontiguousarray(ws, dtype=np.int16).view(np.uint8).reshape(n, nb, sb)
     return out.tobytes()
 
 
@@ -249,11 +289,32 @@ def weight_values(fmt, wq, n, k):
         return iq4_nl_values(wq[:, : k // 2].reshape(n, k // 32, 16)).reshape(n, k)
     if fmt == "q8_0":
         return q8_0_values(wq[:, :k]).reshape(n, k)
+    if fmt == "q4_k":
+        return q4_k_values(wq[:, : k // 2].reshape(n, k // 256, 128)).reshape(n, k)
     return tq2_0_values(wq[:, : k // 4].reshape(n, k // 256, 64)).reshape(n, k)
 
 
-def block_dots(fmt, wq, xq, n, k):
-    """Exact int64 block dots S[m][n][b] = sum_i w(n, b*blk + i) * q(m, b*blk + i) (verify.py:94-100)."""
+def q4_k_block_dots(wq, ws, xq, n, k):
+    """Exact int64 Q4_K block dots S[m][n][b] = (sd, sm): sd = sum_i sc_i * (sum over sub-block i of q * x), sm =
+    sum_i m_i * (sum over sub-block i of x), with q the 4-bit values, x the q8_K activations and (sc_i, m_i) the
+    6-bit scale and min of the 32-value sub-block i (ggml vec_dot_q4_K_q8_K's integer sums; its mins term uses the
+    q8_K bsums, whose pairs are these sub-block sums)."""
+    nb = k // 256
+    v = weight_values("q4_k", wq, n, k).reshape(n, nb, 8, 32).astype(np.int64)
+    q = np.asarray(xq, np.int8).reshape(-1, nb, 8, 32).astype(np.int64)
+    meta = np.ascontiguousarray(ws, dtype=np.int16).view(np.uint8).reshape(n, nb, 16)
+    sc, mn = q4_k_scales(meta[:, :, 4:])
+    dots = np.einsum("nbil,mbil->mnbi", v, q)
+    sd = np.einsum("mnbi,nbi->mnb", dots, sc.astype(np.int64))
+    sm = np.einsum("mbi,nbi->mnb", q.sum(-1), mn.astype(np.int64))
+    return np.stack([sd, sm], axis=-1)
+
+
+def block_dots(fmt, wq, xq, n, k, ws=None):
+    """Exact int64 block dots S[m][n][b] = sum_i w(n, b*blk + i) * q(m, b*blk + i) (verify.py:94-100); q4_k (whose
+    sums need the scale plane ws): S[m][n][b] = (sd, sm) of q4_k_block_dots."""
+    if fmt == "q4_k":
+        return q4_k_block_dots(wq, ws, xq, n, k)
     blk = FORMATS[fmt]["block"]
     v = weight_values(fmt, wq, n, k).reshape(n, k // blk, blk).astype(np.int64)
     q = np.asarray(xq, np.int8).reshape(-1, k // blk, blk).astype(np.int64)
@@ -268,9 +329,21 @@ def reference_dot(fmt, ws, xd, s):
     sum rounds, and the result depends on the block order alone.  q8_0 and iq4_nl weights take q4_0's form (ggml's
     vec_dot_q8_0_q8_0 and vec_dot_iq4_nl_q8_0 scale the int block dot by f16(dw) * f16(dx)); their block dots stay
     below 2**22 in magnitude, so the products are exact there too."""
-    dw = f16_bits_to_f32(ws).astype(np.float64)  # [N][nb]
     dx = np.asarray(xd, np.float32).astype(np.float64)  # [M][nb]
     s = np.asarray(s, dtype=np.int64)
+    if fmt == "q4_k":
+        # y = sum_b f16(d) * dx * sd - f16(dmin) * dx * sm (ggml vec_dot_q4_K_q8_K), each term in f64: the products
+        # are not all exact there (sd reaches 2**24), which the 1e-5 tolerance of the comparisons covers
+        meta = np.ascontiguousarray(ws, dtype=np.int16).reshape(ws.shape[0], -1, 8)
+        d = f16_bits_to_f32(meta[:, :, 0]).astype(np.float64)
+        dmin = f16_bits_to_f32(meta[:, :, 1]).astype(np.float64)
+        m, n, nb, _ = s.shape
+        total = np.zeros((m, n), dtype=np.float64)
+        for b in range(nb):
+            total = total + ((d[None, :, b] * dx[:, None, b]) * s[:, :, b, 0]
+                             - (dmin[None, :, b] * dx[:, None, b]) * s[:, :, b, 1])  # fmt: skip
+        return total
+    dw = f16_bits_to_f32(ws).astype(np.float64)  # [N][nb]
     m, n, nb = s.shape
     total = np.zeros((m, n), dtype=np.float64)
     for b in range(nb):
@@ -283,8 +356,9 @@ def reference_dot(fmt, ws, xd, s):
 
 
 def gemv(fmt, wq, ws, xq, xd, n, k):
-    """(Y f64 reference [M][N], S int64 [M][N][blocks]) for split planes and q8 activations."""
-    s = block_dots(fmt, wq, xq, n, k)
+    """(Y f64 reference [M][N], S int64 [M][N][blocks] ([M][N][blocks][2] for q4_k)) for split planes and q8
+    activations."""
+    s = block_dots(fmt, wq, xq, n, k, ws)
     return reference_dot(fmt, ws, xd, s), s
 
 
@@ -368,6 +442,22 @@ def pack_q8_0(q, d_bits):
     return out.tobytes()
 
 
+def pack_q4_k(nibbles, d_bits, dmin_bits, sc12):
+    """nibbles uint8 [n][k] in 0..15, f16 bit patterns of d and dmin [n][k/256] and packed scale bytes
+    [n][k/256][12] -> ggml q4_K blocks (d, dmin, scales, then value 64j + l / 64j + 32 + l in the low / high nibble
+    of byte 32j + l)."""
+    nib = np.asarray(nibbles, np.uint8)
+    n, k = nib.shape
+    nb = k // 256
+    g = nib.reshape(n, nb, 4, 2, 32)
+    out = np.empty((n, nb, 144), dtype=np.uint8)
+    out[:, :, 0:2] = np.ascontiguousarray(d_bits, dtype=np.uint16).view(np.uint8).reshape(n, nb, 2)
+    out[:, :, 2:4] = np.ascontiguousarray(dmin_bits, dtype=np.uint16).view(np.uint8).reshape(n, nb, 2)
+    out[:, :, 4:16] = np.asarray(sc12, np.uint8).reshape(n, nb, 12)
+    out[:, :, 16:] = ((g[:, :, :, 0] & 15) | ((g[:, :, :, 1] & 15) << 4)).reshape(n, nb, 128)
+    return out.tobytes()
+
+
 F16_MAX_BITS = 0x7BFF  # 65504
 F16_MIN_SUBNORMAL_BITS = 0x0001  # 2**-24
 
@@ -404,6 +494,24 @@ def weights(fmt, rng, n, k, extreme=False):
             sk = rng.integers(0, 4, size=(n, nb))
             d = np.where(sk == 1, F16_MAX_BITS, np.where(sk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
         return pack_q4_0(nib.reshape(n, k), d)  # same bytes as Q4_0: index i low nibble, index i+16 high nibble
+    if fmt == "q4_k":  # any 12 scale bytes are valid 6-bit scales and mins; d, dmin ~ U(0.0002, 0.001)
+        nib = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+        sc12 = rng.integers(0, 256, size=(n, nb, 12), dtype=np.uint8)
+        d = np.asarray(rng.uniform(0.0002, 0.001, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+        dm = np.asarray(rng.uniform(0.0002, 0.001, size=(n, nb)), np.float32).astype(np.float16).view(np.uint16)
+        if extreme:
+            nb4 = nib.reshape(n, nb, 256)
+            kind = rng.integers(0, 3, size=(n, nb))
+            nb4[kind == 1] = 0
+            nb4[kind == 2] = 15
+            sk = rng.integers(0, 4, size=(n, nb))
+            sc12[sk == 1] = 0xFF  # every scale and min 63
+            sc12[sk == 2] = 0
+            dk = rng.integers(0, 4, size=(n, nb))
+            d = np.where(dk == 1, F16_MAX_BITS, np.where(dk == 2, F16_MIN_SUBNORMAL_BITS, d)).astype(np.uint16)
+            mk = rng.integers(0, 4, size=(n, nb))
+            dm = np.where(mk == 1, F16_MAX_BITS, np.where(mk == 2, F16_MIN_SUBNORMAL_BITS, dm)).astype(np.uint16)
+        return pack_q4_k(nib, d, dm, sc12)
     if fmt == "q4_0" and not extreme:
         return quantize_q4_0_weights(rng.normal(0.0, 0.02, size=(n, k)).astype(np.float32))
     if fmt == "q4_0":

@@ -55,6 +55,20 @@ def test_gemv_rejects_bad_arguments(kw, needle):
     assert needle in _abi.last_error()
 
 
+def test_q4_k_rejects_bad_arguments():
+    lib = _abi.lib()
+    p16, p8 = ctypes.c_void_p(16), ctypes.c_void_p(8)
+    q4k = dict(name="komp_q4_k_gemv", K=256, SW=128)
+    assert _gemv(**q4k, bn=128, nw=8) == _abi.KOMP_EINVAL and "at most 8" in _abi.last_error()  # 16 rows per wave
+    assert _gemv(name="komp_q4_k_gemv", K=288, SW=144) == _abi.KOMP_EINVAL
+    assert "multiple of the 256" in _abi.last_error()
+    st = lib.komp_q4_k_gemv(p16, p8, p16, p16, p16, None, 1, 4, 256, 128, 32, 4, 2, 4, None)  # WS 8-byte aligned
+    assert st == _abi.KOMP_EINVAL and "16-byte aligned" in _abi.last_error()
+    st = lib.komp_q4_k_split(p16, p16, p8, 4, 256, 128, None)
+    assert st == _abi.KOMP_EINVAL and "WS 16-byte aligned" in _abi.last_error()
+    assert lib.komp_gemm_plan(4, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL  # no q4_k GEMM
+
+
 def test_empty_shapes_are_no_ops():
     assert _gemv(M=0) == 0 and _gemv(N=0) == 0
     lib = _abi.lib()
@@ -182,5 +196,5 @@ def test_gemm_rejects_bad_arguments():
     assert cols.value == 16 and waves.value == 8 and rows.value % 16 == 0
     for fmt in (2, 3):  # q8_0, iq4_nl
         assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 4096, None, None, None) == 0
-    for fmt in (-1, 4):
+    for fmt in (-1, 5):
         assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL

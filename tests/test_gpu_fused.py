@@ -18,7 +18,8 @@ def dev(a):
 
 CASES = [("q4_0", 37, 416, 3), ("q4_0", 4097, 4192, 1), ("q4_0", 64, 512, 4), ("tq2_0", 37, 768, 3),
          ("tq2_0", 6913, 2816, 2), ("tq2_0", 5, 1280, 1), ("q8_0", 37, 416, 3), ("q8_0", 4097, 4192, 1),
-         ("iq4_nl", 37, 416, 3), ("iq4_nl", 4097, 4192, 1), ("iq4_nl", 64, 512, 4)]  # fmt: skip
+         ("iq4_nl", 37, 416, 3), ("iq4_nl", 4097, 4192, 1), ("iq4_nl", 64, 512, 4), ("q4_k", 37, 768, 3),
+         ("q4_k", 4097, 4352, 1), ("q4_k", 64, 1024, 4)]  # fmt: skip
 
 
 @pytest.mark.parametrize("fmt,n,k,m", CASES)
@@ -31,7 +32,7 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
     wq, ws, xg = dev(wq), dev(ws), dev(x)
     bn, nb, nw = knobs if knobs else (None, 0, 0)
     y1, s1, q = host.gemv_f32(fmt, wq, ws, xg, n, k, bn, nb, mode, nw, store_s=True, return_q=True)
-    qq = host.quantize(fmt, xg, bsums=(fmt == "tq2_0"))
+    qq = host.quantize(fmt, xg, bsums=(O.FORMATS[fmt]["act"] == "q8_K"))
     y2, s2 = host.gemv(fmt, wq, ws, qq[0], qq[1], n, k, bn, nb, mode, nw, store_s=True)
     torch.cuda.synchronize()
     assert torch.equal(s1, s2)

@@ -31,7 +31,8 @@ def problems(fmt, ns, k, m, seed):
 
 CASES = [("q4_0", (4096, 1024, 1024), 4096), ("tq2_0", (6912, 6912), 2560), ("q4_0", (37, 5, 100, 64), 416),
          ("tq2_0", (13, 300, 1), 1280), ("q4_0", (64, 0, 33), 512), ("q8_0", (4096, 1024, 1024), 4096),
-         ("iq4_nl", (37, 5, 100, 64), 416), ("q8_0", (13, 300, 1), 1280)]  # fmt: skip
+         ("iq4_nl", (37, 5, 100, 64), 416), ("q8_0", (13, 300, 1), 1280), ("q4_k", (37, 5, 100, 64), 768),
+         ("q4_k", (6912, 6912), 2560)]  # fmt: skip
 
 
 @pytest.mark.parametrize("fmt,ns,k", CASES)

@@ -16,6 +16,8 @@ PROBLEMS = {"q4_0": ((64, 512, 1), (37, 416, 3), (5, 96, 2)), "tq2_0": ((64, 102
 CONFIGS = {"q4_0": ((32, 4, 4), (16, 2, 2), (64, 8, 4)), "tq2_0": ((32, 2, 4), (16, 1, 2), (64, 4, 4))}
 for _f in ("q8_0", "iq4_nl"):  # the ggml formats beyond the reference's two take Q4_0's problems and knob sets
     PROBLEMS[_f], CONFIGS[_f] = PROBLEMS["q4_0"], CONFIGS["q4_0"]
+PROBLEMS["q4_k"] = PROBLEMS["tq2_0"]  # 256-value blocks; knob sets with at most 8 rows per wave
+CONFIGS["q4_k"] = ((32, 4, 4), (16, 2, 2), (64, 8, 8))
 
 
 def dev(a):
@@ -132,7 +134,7 @@ def run_gemv(fmt, n, k, m, seed, extreme, block_n, nb, mode, num_warps):
     return y.cpu().numpy(), s.cpu().numpy(), r, rs, xq.cpu().numpy(), rq
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 @pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("cfg", [0, 1, 2])
 @pytest.mark.parametrize("prob", [0, 1, 2])
@@ -146,12 +148,16 @@ def test_gemv_verify_problems(fmt, mode, cfg, prob, extreme):
     assert O.relerr(y, r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 @pytest.mark.parametrize("block_n", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("nb", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("nw", [1, 2, 4, 8])
 def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
-    n, k, m = (77, 96 * 32, 3) if fmt != "tq2_0" else (77, 13 * 256, 3)
+    n, k, m = (77, 96 * 32, 3) if O.FORMATS[fmt]["block"] == 32 else (77, 13 * 256, 3)
+    if fmt == "q4_k" and block_n // nw > 8:  # q4_k: a row group of 64 / rows-per-wave lanes must hold 8 chunks
+        with pytest.raises(host._abi.KompArgumentError, match="at most 8"):
+            run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
+        return
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
     assert np.array_equal(s.astype(np.int64), rs)
     assert O.relerr(y, r) <= TOL
@@ -159,7 +165,7 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
 
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 16384, 8192), ("q4_0", 16400, 4192), ("tq2_0", 16384, 2816),
                                      ("q4_0", 20000, 1024), ("q8_0", 16400, 4192), ("iq4_nl", 16384, 8192),
-                                     ("q8_0", 20000, 1024)])  # fmt: skip
+                                     ("q8_0", 20000, 1024), ("q4_k", 16400, 4352)])  # fmt: skip
 def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
     # N >= 16384 (16400 and 20000 leave a partial last workgroup); q4_0 reads whole rows in one K step, two passes
     assert host.auto_plan(fmt, 1, n, k)["passes"] == (2 if fmt != "tq2_0" else 1)
@@ -173,7 +179,8 @@ def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
                                      ("tq2_0", 2560, 6912), ("tq2_0", 6913, 2816), ("tq2_0", 16383, 256),
                                      ("tq2_0", 513, 1280), ("q8_0", 4096, 4096), ("q8_0", 4097, 4192),
                                      ("q8_0", 300, 96), ("iq4_nl", 4096, 4096), ("iq4_nl", 127, 4192),
-                                     ("iq4_nl", 16383, 4096)])  # fmt: skip
+                                     ("iq4_nl", 16383, 4096), ("q4_k", 4096, 4096), ("q4_k", 4097, 4352),
+                                     ("q4_k", 6912, 2560), ("q4_k", 300, 256), ("q4_k", 2560, 6912)])  # fmt: skip
 @pytest.mark.parametrize("m", [1, 3])
 def test_gemv_auto_config_shapes(fmt, n, k, m):
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 21, False, None, None, 2, None)
@@ -235,7 +242,8 @@ def test_scale_slab_and_per_tile_scales_agree(fmt, n, k, knobs):
                                            ("q4_0", 4097, 4096, True), ("tq2_0", 4097, 2048, False),
                                            ("tq2_0", 300, 1280, False), ("q4_0", 6144, 4096, True),
                                            ("q4_0", 4096, 14336, True), ("tq2_0", 2560, 6912, True),
-                                           ("q8_0", 4097, 4096, True), ("iq4_nl", 6144, 4096, True)])  # fmt: skip
+                                           ("q8_0", 4097, 4096, True), ("iq4_nl", 6144, 4096, True),
+                                           ("q4_k", 4096, 4096, True), ("q4_k", 4096, 14336, True)])  # fmt: skip
 def test_one_workgroup_per_cu_plans(fmt, n, k, fused):
     # small single-column GEMVs plan one workgroup of ceil(N / CUs) rows per CU; the first five shapes give the waves
     # more row slots than rows (clipped per wave), q4_0 4097x4096 and tq2_0 4097x2048 with the scale slab in LDS
@@ -252,3 +260,22 @@ def test_one_workgroup_per_cu_plans(fmt, n, k, fused):
     torch.cuda.synchronize()
     r, rs = O.gemv(fmt, wq, ws, *O.quantize(fmt, x)[:2], n, k)
     assert np.array_equal(s.cpu().numpy().astype(np.int64), rs) and O.relerr(y.cpu().numpy(), r) <= TOL
+
+
+@pytest.mark.parametrize("knobs", [(64, 4, 8), (16, 4, 2), None])
+def test_q4_k_scale_slab_and_global_scales(knobs):
+    # q4_k's 16-byte scale entries: (64, 4, 8) needs 8 x 8 rows x 32 blocks x 16 B = 32 KB of slab, past the 16 KB
+    # limit, so its lanes load their entries from global memory; (16, 4, 2) stages an 8 KB slab in LDS
+    n, k = 300, 8192
+    bn, nb, nw = knobs or (None, None, None)
+    y, s, r, rs, _, _ = run_gemv("q4_k", n, k, 2, 41, False, bn, nb, 2, nw)
+    assert np.array_equal(s.astype(np.int64), rs)
+    assert O.relerr(y, r) <= TOL
+
+
+def test_q4_k_extreme_scales_every_mode():
+    # every scale and min at 63 or 0, d / dmin at 65504 or the smallest subnormal, nibbles all 0 or 15
+    for mode in (0, 1, 2):
+        y, s, r, rs, _, _ = run_gemv("q4_k", 45, 2304, 3, 43, True, 16, 4, mode, 2)
+        assert np.array_equal(s.astype(np.int64), rs)
+        assert O.relerr(y, r) <= TOL

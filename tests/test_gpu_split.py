@@ -1,4 +1,4 @@
-"""Weight ingestion on the device (komp_{q4_0,tq2_0,q8_0,iq4_nl}_split) vs the oracle's split of the same ggml block
+"""Weight ingestion on the device (komp_{q4_0,tq2_0,q8_0,iq4_nl,q4_k}_split) vs the oracle's split of the same ggml block
 bytes: WQ and WS bit-identical, row padding left untouched, and a GEMV over the device-split planes equal to one over
 the host-split planes.  Everything goes through the C ABI."""
 
@@ -12,7 +12,8 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 # block values, block bytes, quant bytes
-NBYTES = {"q4_0": (32, 18, 16), "tq2_0": (256, 66, 64), "q8_0": (32, 34, 32), "iq4_nl": (32, 18, 16)}
+NBYTES = {"q4_0": (32, 18, 16), "tq2_0": (256, 66, 64), "q8_0": (32, 34, 32), "iq4_nl": (32, 18, 16),
+          "q4_k": (256, 144, 128)}
 SHAPES = [(1, 1), (5, 3), (37, 13), (64, 128), (300, 27), (1023, 7)]  # (rows, blocks per row)
 
 
@@ -20,7 +21,7 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 @pytest.mark.parametrize("shape", range(len(SHAPES)))
 def test_split_matches_oracle(fmt, shape):
     n, nb = SHAPES[shape]
@@ -35,7 +36,7 @@ def test_split_matches_oracle(fmt, shape):
     assert np.array_equal(wq.cpu().numpy(), rq) and np.array_equal(ws.cpu().numpy(), rs)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_split_padded_rows_and_offset_input(fmt):
     n, nb = 29, 11
     blk, nbytes, qbytes = NBYTES[fmt]
@@ -48,7 +49,7 @@ def test_split_padded_rows_and_offset_input(fmt):
     w_in = base[4 : 4 + W.size]
     sw = (nb * qbytes + 15) // 16 * 16 + 48
     wq = torch.full((n, sw), 0xA5, dtype=torch.uint8, device="cuda")
-    ws = torch.zeros((n, nb), dtype=torch.int16, device="cuda")
+    ws = torch.zeros((n, nb * O.FORMATS[fmt]["sbytes"] // 2), dtype=torch.int16, device="cuda")
     host.split_into(fmt, w_in, wq, ws, n, k)
     torch.cuda.synchronize()
     got = wq.cpu().numpy()
@@ -56,7 +57,7 @@ def test_split_padded_rows_and_offset_input(fmt):
     assert (got[:, nb * qbytes :] == 0xA5).all()  # padding untouched
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemv_over_device_split(fmt):
     n, k, m = (96, 1024, 3) if fmt != "tq2_0" else (96, 1536, 3)
     W, x = O.problem(fmt, n, k, m, 81)

@@ -53,7 +53,7 @@ def test_cpu_tensors_fail_loudly():
     with pytest.raises(_abi.KompArgumentError, match="HIP device"):
         host.gemv("iq4_nl", wq, ws, xq, xd, 4, 64)
     with pytest.raises(KeyError):
-        host.gemv("q4_k", wq, ws, xq, xd, 4, 64)
+        host.gemv("q5_k", wq, ws, xq, xd, 4, 64)
     with pytest.raises(_abi.KompArgumentError, match="HIP device"):
         host.gemv_multi("q4_0", [(wq, ws, 4), (wq, ws, 4)], 64, xq=xq, xd=xd)
     with pytest.raises(_abi.KompArgumentError, match="either"):

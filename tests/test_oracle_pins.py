@@ -90,6 +90,106 @@ def test_new_format_blocks_from_ggml_bytes():
     assert O.weight_values("iq4_nl", wq, 1, 32).tolist() == [[int(O.IQ4_NL_VALUES[i]) for i in idx]]
 
 
+def test_q4_k_every_byte_every_position():
+    # ggml dequantize_row_q4_K order: for each 32-byte group j: 32 low nibbles (values 64j..64j+31), then the 32 high
+    # nibbles of the same bytes (values 64j+32..64j+63)
+    for pos in (0, 31, 32, 77, 127):
+        qs = np.full((256, 128), 0x53, np.uint8)
+        qs[:, pos] = np.arange(256)
+        v = O.q4_k_values(qs)
+        j, l = divmod(pos, 32)
+        for b in range(256):
+            assert v[b, 64 * j + l] == b & 15 and v[b, 64 * j + 32 + l] == b >> 4
+        others = [i for i in range(256) if i not in (64 * j + l, 64 * j + 32 + l)]
+        assert ((v[:, others] == 3) | (v[:, others] == 5)).all()
+    rng = np.random.default_rng(4)
+    qs = rng.integers(0, 256, size=(3, 128), dtype=np.uint8)
+    want = []
+    for row in qs:  # the loop of the dequantizer, value by value
+        out = []
+        for j in range(4):
+            out += [int(row[32 * j + l]) & 15 for l in range(32)] + [int(row[32 * j + l]) >> 4 for l in range(32)]
+        want.append(out)
+    assert O.q4_k_values(qs).tolist() == want
+
+
+def _q4_k_scales_bits(sc12):
+    """The 6-bit fields read out of the 96-bit little-endian integer of the 12 bytes: sub-block i < 4 at bits 8i
+    (scale) and 32 + 8i (min); i >= 4: bits 64 + 8(i-4) (low 4 scale bits), 68 + 8(i-4) (low 4 min bits), and the
+    two top bits of bytes i-4 (scale) and i (min) as bits 4..5."""
+    v = int.from_bytes(bytes(sc12), "little")
+    bits = lambda at, w: (v >> at) & ((1 << w) - 1)  # noqa: E731
+    sc = [bits(8 * i, 6) for i in range(4)] + [bits(64 + 8 * i, 4) | (bits(8 * i + 6, 2) << 4) for i in range(4)]
+    mn = [bits(32 + 8 * i, 6) for i in range(4)] + [bits(68 + 8 * i, 4) | (bits(32 + 8 * i + 6, 2) << 4) for i in range(4)]
+    return sc, mn
+
+
+def _q4_k_scales_words(sc12):
+    """The same fields as ggml's vec_dot unpacks them: three little-endian dwords u0..u2 rearranged with byte masks
+    into the 8 scales (bytes of two dwords) and the 8 mins."""
+    u0, u1, u2 = struct.unpack("<3I", bytes(sc12))
+    s_lo = u0 & 0x3F3F3F3F
+    s_hi = (u2 & 0x0F0F0F0F) | (((u0 >> 6) & 0x03030303) << 4)
+    m_lo = u1 & 0x3F3F3F3F
+    m_hi = ((u2 >> 4) & 0x0F0F0F0F) | (((u1 >> 6) & 0x03030303) << 4)
+    return list(struct.pack("<2I", s_lo, s_hi)), list(struct.pack("<2I", m_lo, m_hi))
+
+
+def test_q4_k_scales_every_byte_every_position():
+    rng = np.random.default_rng(5)
+    for pos in range(12):
+        base = rng.integers(0, 256, size=12, dtype=np.uint8)
+        sc12 = np.tile(base, (256, 1))
+        sc12[:, pos] = np.arange(256)
+        sc, mn = O.q4_k_scales(sc12)
+        for b in range(256):
+            want = _q4_k_scales_bits(sc12[b])
+            assert (sc[b].tolist(), mn[b].tolist()) == want
+            assert want == _q4_k_scales_words(sc12[b])
+    assert O.q4_k_scales(np.full(12, 0xFF, np.uint8))[0].tolist() == [63] * 8  # every field at its maximum
+
+
+def test_q4_k_block_dots_are_the_dequantized_dot():
+    # ggml dequantizes value l of sub-block i to d * sc_i * q_l - dmin * m_i; the oracle's (sd, sm) must give exactly
+    # sum_l (that value) * (dx * x_l), checked here with exact rationals on blocks built with struct
+    from fractions import Fraction
+
+    rng = np.random.default_rng(6)
+    n, k, m = 3, 512, 2
+    W = O.weights("q4_k", rng, n, k, extreme=True)
+    wq, ws = O.split("q4_k", W, n, k)
+    xq = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    xd = rng.uniform(0.001, 0.1, size=(m, k // 256)).astype(np.float32)
+    s = O.block_dots("q4_k", wq, xq, n, k, ws)
+    assert s.shape == (m, n, k // 256, 2)
+    for r in range(n):
+        for b in range(k // 256):
+            raw = W[(r * (k // 256) + b) * 144 :][:144]
+            d, dmin = (Fraction(float(v)) for v in struct.unpack_from("<2e", raw, 0))
+            sc, mn = _q4_k_scales_bits(raw[4:16])
+            q = [raw[16 + 32 * (v // 64) + v % 32] >> (4 * ((v % 64) // 32)) & 15 for v in range(256)]
+            for i in range(m):
+                xs = [int(t) for t in xq[i, 256 * b : 256 * (b + 1)]]
+                sd = sum(sc[v // 32] * q[v] * xs[v] for v in range(256))
+                sm = sum(mn[v // 32] * xs[v] for v in range(256))
+                assert tuple(s[i, r, b]) == (sd, sm)
+                dx = Fraction(float(xd[i, b]))
+                deq = sum((d * sc[v // 32] * q[v] - dmin * mn[v // 32]) * dx * xs[v] for v in range(256))
+                assert deq == d * dx * sd - dmin * dx * sm
+
+
+def test_q4_k_known_answer():
+    # one block: d = 0.5, dmin = 0.25, every scale 2 and every min 1, quant nibbles all 3; x = 1 everywhere, dx = 1:
+    # each value dequantizes to 0.5 * 2 * 3 - 0.25 * 1 = 2.75.  Scales 0..3 sit in bytes 0..3, mins 0..3 in bytes
+    # 4..7, sub-blocks 4..7 in bytes 8..11 (scale in the low nibble, min in the high nibble; top bits 0)
+    sc12 = bytes([2, 2, 2, 2, 1, 1, 1, 1, 0x12, 0x12, 0x12, 0x12])
+    blk = struct.pack("<2e", 0.5, 0.25) + sc12 + bytes([0x33] * 128)
+    wq, ws = O.split("q4_k", blk, 1, 256)
+    xq = np.ones((1, 256), np.int8)
+    y, s = O.gemv("q4_k", wq, ws, xq, np.ones((1, 1), np.float32), 1, 256)
+    assert tuple(s[0, 0, 0]) == (2 * 3 * 256, 256) and y[0, 0] == 2.75 * 256
+
+
 def test_tq2_0_every_byte_every_position():
     # ggml dequantize_row_tq2_0 order: for j in (0, 32): for l in 0..3: for m in 0..31: y = crumb(qs[j+m], l) - 1
     rng = np.random.default_rng(0)
@@ -299,7 +399,7 @@ def test_act_block_layouts():
 # GEMV references (verify.py:94-120)
 
 
-@pytest.mark.parametrize("fmt,k", [("q4_0", 96), ("tq2_0", 512), ("q8_0", 96), ("iq4_nl", 96)])
+@pytest.mark.parametrize("fmt,k", [("q4_0", 96), ("tq2_0", 512), ("q8_0", 96), ("iq4_nl", 96)])  # q4_k: above
 def test_block_dots_brute_force(fmt, k):
     rng = np.random.default_rng(8)
     n, m = 5, 2
