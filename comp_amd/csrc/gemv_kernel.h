@@ -183,14 +183,15 @@ constexpr int max_threads() {
 
 template <int FMT, int MODE, int MC, int NB, bool FUSED>
 __global__ void __launch_bounds__((max_threads<FMT, MODE, MC, NB, FUSED>()))
-gemv_kernel(int N1, int K, int64_t SW1, int nblk, int rows_per_wg, int rows_per_wave, int lpr_log2, int passes,
-            int nsteps, int sc_mode, int nseg, const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
+gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, int lpr_log2, int sc_mode, int nseg,
+            int passes, const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1, int K, int nsteps,
             const int8_t* __restrict__ XQ, const float* __restrict__ XD, const float* __restrict__ X,
             int8_t* __restrict__ XQo, float* __restrict__ XDo, int16_t* __restrict__ XBo, float* __restrict__ Y1,
             int32_t* __restrict__ S, const GemvSegs segs) {
-  // The scalars come first and the host precomputes every quotient (nblk = K / block, rows per wave, K steps), so
-  // with the first 16 argument dwords preloaded into SGPRs the first weight load needs no memory round trip for its
-  // address and the prologue no integer division.
+  // The host precomputes every quotient (nblk = K / block, rows per wave, K steps), and what the first weight and
+  // scale loads need comes first: gfx950 preloads the first 14 argument dwords into SGPRs (16 user SGPRs, 2 of them
+  // the argument pointer), so those loads are issued without waiting for an argument fetch from memory and the
+  // prologue does no integer division.
   //
   // sc_mode 1: the workgroup's weight scales WS[row0 .. row0 + rows_per_wg) (one contiguous slab, 16-byte aligned, a
   // multiple of 8 scales) are staged in LDS with the activations, and the weight stream issues only quant loads.
@@ -629,12 +630,12 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
   const int rows_per_wave = p.rows_per_wave;
   if (tm.on) {
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.k, c.sw, nblk, p.block_n,
-                          rows_per_wave, p.lpr_log2, p.passes, nsteps, sc_mode, c.nseg, c.wq, c.ws, c.xq, c.xd, c.x,
-                          c.xq_out, c.xd_out, c.xb_out, c.y, c.s, segs);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, c.sw, p.block_n,
+                          rows_per_wave, p.lpr_log2, sc_mode, c.nseg, p.passes, c.wq, c.ws, c.k, nsteps, c.xq, c.xd,
+                          c.x, c.xq_out, c.xd_out, c.xb_out, c.y, c.s, segs);
   } else {
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, c.k, c.sw, nblk, p.block_n, rows_per_wave, p.lpr_log2,
-                       p.passes, nsteps, sc_mode, c.nseg, c.wq, c.ws, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y,
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, c.sw, p.block_n, rows_per_wave, p.lpr_log2, sc_mode,
+                       c.nseg, p.passes, c.wq, c.ws, c.k, nsteps, c.xq, c.xd, c.x, c.xq_out, c.xd_out, c.xb_out, c.y,
                        c.s, segs);
   }
   return hipGetLastError();
