@@ -95,16 +95,21 @@ __device__ __forceinline__ long pack2(unsigned lo, unsigned hi) {
 // instantiation, so the plain kernel's step loop has no branch between an MFMA and the scaling of its result).
 template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
 __global__ void __launch_bounds__(64 * WK * WR)
-gemm_kernel(int N, int M, int K, int nblk, int nsteps, int ss, int64_t SW, const uint8_t* __restrict__ WQ,
-            const int16_t* __restrict__ WS, const int8_t* __restrict__ XQ, const float* __restrict__ XD,
-            float* __restrict__ Y, int32_t* __restrict__ S) {
-  // ss: row stride of the f32 scale slab in LDS, nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four
-  // scales of a row with one 16-byte LDS load).
+gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS,
+            const int8_t* __restrict__ XQ, const float* __restrict__ XD, float* __restrict__ Y,
+            int32_t* __restrict__ S) {
+  // The arguments every first load needs fill exactly the 14 argument dwords gfx950 preloads into SGPRs (16 user
+  // SGPRs, 2 of them the argument pointer), so no load waits for an argument fetch; the step count and the slab
+  // stride are shifts of nblk.
   constexpr bool NIB4 = FMT == FMT_Q4_0 || FMT == FMT_IQ4_NL;  // 16 nibble bytes per 32-value block
   constexpr bool Q8 = FMT == FMT_Q8_0;                           // 32 int8 bytes per 32-value block
   constexpr bool BLK32 = NIB4 || Q8;                             // the 32-value blocks (q8_0 activations)
   constexpr bool TQ2 = FMT == FMT_TQ2_0;
   constexpr int BPS = NIB4 ? 4 : (Q8 ? 2 : 1);                   // blocks per 64-byte K step
+  const int nsteps = (nblk + BPS - 1) / BPS;                     // K steps
+  // row stride of the f32 scale slab in LDS: nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four scales
+  // of a row with one 16-byte LDS load)
+  const int ss = slab_stride(nblk);
   constexpr int W = WK * WR;
   constexpr int XV = NIB4 ? 2 : (Q8 ? 1 : 4);                    // 16-byte activation loads per column tile per step
   constexpr int WGR = 16 * WN * WR;     // rows per workgroup
@@ -379,15 +384,13 @@ namespace {
 template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
 hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
   const int nblk = c.k / fmt_info(FMT).block;
-  const int bps = FMT == FMT_TQ2_0 ? 1 : (FMT == FMT_Q8_0 ? 2 : 4);  // blocks per 64-byte K step
-  const int nsteps = (nblk + bps - 1) / bps;
   const dim3 grid((c.n + 16 * WN * WR - 1) / (16 * WN * WR), (c.m + 16 * CN - 1) / (16 * CN));
   const dim3 block(64 * WK * WR);
   const size_t lds = gemm_lds_bytes(FMT, p, c.k);
   auto kern = gemm_impl::gemm_kernel<FMT, WK, WR, WN, CN, D, STORE_S>;
   const Timing tm = timing_slot(gemv_kind(FMT));
-  hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, nsteps,
-                        gemm_impl::slab_stride(nblk), c.sw, c.wq, c.ws, c.xq, c.xd, c.y, c.s);
+  hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, c.sw, c.wq, c.ws,
+                        c.xq, c.xd, c.y, c.s);
   return hipGetLastError();
 }
 
