@@ -4,7 +4,7 @@
 namespace komp {
 
 size_t gemv_lds_bytes(int fmt, int m, int k) {
-  if (fmt == FMT_Q4_K) return static_cast<size_t>(m) * (k / 256) * (256 + 8 + 64);  // + 16 int32 bsums
+  if (fmt == FMT_Q4_K) return static_cast<size_t>(m) * (k / 256) * (256 + 8 + 32);  // + 8 int32 sub-block sums
   if (fmt != FMT_TQ2_0) return static_cast<size_t>(m) * (k / 32) * (32 + 8);
   return static_cast<size_t>(m) * (k / 256) * (256 + 8);
 }

@@ -106,23 +106,27 @@ __device__ __forceinline__ int q8_0_chunk_dot(u32x4 w, u32x4 x) {
   return s;
 }
 
-// Q4_K: the two int32 dots of one 16-byte chunk, whose low nibbles are 16 values of one 32-value sub-block
-// (activations xl) and whose high nibbles the matching 16 values of the next (xh); the nibbles are unsigned, the
-// sub-block's min enters through its own term.
+// Q4_K: the two int32 dots of one 32-byte group of a block (16-byte halves wa, wb), whose low nibbles are the 32
+// values of one sub-block (activation pieces xa, xb) and whose high nibbles the 32 values of the next (xc, xd); the
+// nibbles are unsigned, the sub-blocks' mins enter through their own term.
 template <int MODE>
-__device__ __forceinline__ int2 q4_k_chunk_dots(u32x4 w, u32x4 xl, u32x4 xh) {
+__device__ __forceinline__ int2 q4_k_group_dots(u32x4 wa, u32x4 wb, u32x4 xa, u32x4 xb, u32x4 xc, u32x4 xd) {
   int lo = 0, hi = 0;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     if constexpr (MODE == MODE_BYTES) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        lo += static_cast<int>((w[d] >> (8 * e)) & 15u) * sbyte(xl[d], e);
-        hi += static_cast<int>((w[d] >> (8 * e + 4)) & 15u) * sbyte(xh[d], e);
+        lo += static_cast<int>((wa[d] >> (8 * e)) & 15u) * sbyte(xa[d], e) +
+              static_cast<int>((wb[d] >> (8 * e)) & 15u) * sbyte(xb[d], e);
+        hi += static_cast<int>((wa[d] >> (8 * e + 4)) & 15u) * sbyte(xc[d], e) +
+              static_cast<int>((wb[d] >> (8 * e + 4)) & 15u) * sbyte(xd[d], e);
       }
     } else {
-      lo = dot4<MODE>(w[d] & NIB, xl[d], lo);
-      hi = dot4<MODE>((w[d] >> 4) & NIB, xh[d], hi);
+      lo = dot4<MODE>(wa[d] & NIB, xa[d], lo);
+      lo = dot4<MODE>(wb[d] & NIB, xb[d], lo);
+      hi = dot4<MODE>((wa[d] >> 4) & NIB, xc[d], hi);
+      hi = dot4<MODE>((wb[d] >> 4) & NIB, xd[d], hi);
     }
   }
   return make_int2(lo, hi);
@@ -204,7 +208,9 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
   constexpr bool QK = FMT == FMT_Q4_K;
   constexpr bool BLK32 = FMT != FMT_TQ2_0 && !QK;  // 32-value blocks with q8_0 activations (Q4_0, Q8_0, IQ4_NL)
   constexpr int BB = FMT == FMT_TQ2_0 ? 64 : QK ? 128 : (FMT == FMT_Q8_0 ? 32 : 16);  // quant bytes per block
-  constexpr int CPB_LOG2 = FMT == FMT_TQ2_0 ? 2 : QK ? 3 : (FMT == FMT_Q8_0 ? 1 : 0);  // log2(16-byte chunks/block)
+  // log2(lane slots per block): a slot is 16 bytes of the block, or (Q4_K) a 32-byte group loaded as two halves
+  constexpr int CPB_LOG2 = FMT == FMT_TQ2_0 ? 2 : QK ? 2 : (FMT == FMT_Q8_0 ? 1 : 0);
+  constexpr int LB = QK ? 32 : 16;  // bytes of a lane slot
   constexpr int SCW = QK ? 8 : 1;  // int16 of the scale plane per block (Q4_K: d, dmin and 12 scale bytes)
   constexpr int SPB = QK ? 2 : 1;  // int32 of S per block (Q4_K: the scaled dot and the mins dot)
   int N = N1;
@@ -242,11 +248,12 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
   const int gblk = gl >> CPB_LOG2;                       // block offset of this lane within a slot
   const int tiles = passes * nsteps;
   // per-lane byte offsets within a row group's tile (row grp of the group, block gblk, chunk q)
-  const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + q * 16;
+  const int64_t lane_w = static_cast<int64_t>(grp) * SW + gblk * BB + q * LB;
   const int64_t lane_s = (static_cast<int64_t>(grp) * nblk + gblk) * SCW;
 
   using ScT = std::conditional_t<QK, u32x4, int16_t>;  // one block's scale-plane entry
   u32x4 w[NB];
+  u32x4 w2[QK ? NB : 1];  // Q4_K: the second 16-byte half of each slot
   ScT sc[NB];
   const bool sc_global = sc_mode == 0;
   auto load_tile = [&](int t) {
@@ -262,12 +269,15 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
       const int b = st * bstep + u * bpg + gblk;
       if (rv && b < nblk) {
         w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + static_cast<int64_t>(u) * bpg * BB));
-        if constexpr (QK)
+        if constexpr (QK) {
+          w2[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + static_cast<int64_t>(u) * bpg * BB + 16));
           sc[u] = sc_global ? *reinterpret_cast<const u32x4*>(stp + u * bpg * SCW) : u32x4{0u, 0u, 0u, 0u};
-        else
+        } else {
           sc[u] = sc_global ? stp[u * bpg] : static_cast<int16_t>(0);
+        }
       } else {
         w[u] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (QK) w2[u] = u32x4{0u, 0u, 0u, 0u};
         sc[u] = ScT{};
       }
     }
@@ -282,11 +292,11 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
   // Then (sc_mode 1) the scale slab [waves * rows_per_wave][nblk] (rows past the workgroup's are never loaded nor
   // used), 16-byte aligned (the activation bytes are a multiple of 8).
   // Q4_K: xk[m][p][b] = activation piece p (bytes 16p..16p+15) of block b, meta[m][b] = {d_x bits, 0}, then
-  // bs[m][b][p] = the int32 sum of piece p (the q8_K bsums).
+  // bs[m][b][i] = the int32 sum of sub-block i's 32 activations (two q8_K bsums).
   u32x4* xv = reinterpret_cast<u32x4*>(lds);
   int2* meta = reinterpret_cast<int2*>(xv + (BLK32 ? 2 : 16) * MC * nblk);
   int* bs = reinterpret_cast<int*>(meta + MC * nblk);  // Q4_K only
-  u32x4* scs16 = xv + ((MC * nblk * (BLK32 ? 40 : QK ? 328 : 264) + 15) >> 4);
+  u32x4* scs16 = xv + ((MC * nblk * (BLK32 ? 40 : QK ? 296 : 264) + 15) >> 4);
   const int16_t* scs = reinterpret_cast<const int16_t*>(scs16);
 
   // Then the scale slab (sc_mode 1): each wave copies 1 KB pieces of it from global memory straight into LDS
@@ -418,7 +428,8 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
                 sum = dot4<MODE>(a[u][d], ONES, sum);
               }
             }
-            bs[mb * 16 + p] = sum;
+            sum = group_sum(sum, 2);  // lanes p, p ^ 1 hold the two halves of sub-block p / 2
+            if ((p & 1) == 0) bs[mb * 8 + (p >> 1)] = sum;
             if (p == 0) meta[mb] = make_int2(__float_as_int(dxs[u]), 0);
           } else {
             const int j = (p >> 1) & 3;
@@ -467,7 +478,8 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
           const int bsum = q8_K_row16(v[u], r, qv, d, qsum);
           if constexpr (QK) {
             xv[(m * 16 + r) * nblk + b] = qv;
-            bs[mb * 16 + r] = bsum;
+            const int s32 = group_sum(bsum, 2);  // lanes r, r ^ 1 hold the two halves of sub-block r / 2
+            if ((r & 1) == 0) bs[mb * 8 + (r >> 1)] = s32;
             if (r == 0) meta[mb] = make_int2(__float_as_int(d), 0);
           } else {
             const int j = (r & 7) >> 1;
@@ -521,8 +533,8 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
         if constexpr (QK) {
           dw = f16_bits_to_f32(static_cast<int16_t>(sc[u][0] & 0xFFFFu));
           dmin = f16_bits_to_f32(static_cast<int16_t>(sc[u][0] >> 16));
-          const unsigned jb = 2u * ((q >> 1) & 1);  // byte of sub-block 2j within its dword
-          scm = q4_k_scale_pair(sc[u], (q >> 1) >= 2 ? ~0u : 0u, jb | ((jb + 1) << 8) | ((jb + 4) << 16) | ((jb + 5) << 24));
+          const unsigned jb = 2u * (q & 1);  // byte of sub-block 2q within its dword
+          scm = q4_k_scale_pair(sc[u], q >= 2 ? ~0u : 0u, jb | ((jb + 1) << 8) | ((jb + 4) << 16) | ((jb + 5) << 24));
         } else {
           dw = f16_bits_to_f32(sc[u]);
         }
@@ -537,25 +549,23 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
             if (S != nullptr && rv) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
             acc[m] += static_cast<float>(s) * dw * dx;  // kernels.py:93 order
           } else if constexpr (QK) {
-            // lane octet: chunk q = 2j + h holds values 64j + 16h + e (sub-block 2j, low nibbles) and 64j + 32 + 16h
-            // + e (sub-block 2j + 1, high nibbles), e < 16: activation pieces 4j + h and 4j + 2 + h
-            const int j = q >> 1, h = q & 1;
-            const int2 dd = q4_k_chunk_dots<MODE>(w[u], xv[(m * 16 + 4 * j + h) * nblk + b],
-                                                  xv[(m * 16 + 4 * j + 2 + h) * nblk + b]);
-            const int* bsr = bs + (m * nblk + b) * 16;
-            // 24-bit multiplies (full rate): |dots| < 2^15, |bsums| < 2^12, scales and mins < 64
+            // lane quad: slot q is the block's 32-byte group q: values 64q + e (sub-block 2q, low nibbles, activation
+            // pieces 4q and 4q + 1) and 64q + 32 + e (sub-block 2q + 1, high nibbles, pieces 4q + 2 and 4q + 3)
+            const u32x4* xq4 = xv + (m * 16 + 4 * q) * nblk + b;
+            const int2 dd = q4_k_group_dots<MODE>(w[u], w2[u], xq4[0], xq4[nblk], xq4[2 * nblk], xq4[3 * nblk]);
+            const int2 xs = *reinterpret_cast<const int2*>(bs + (m * nblk + b) * 8 + 2 * q);  // sub-block sums
+            // 24-bit multiplies (full rate): |dots| < 2^16, |sums| < 2^13, scales and mins < 64
             const int sd = __mul24(static_cast<int>(scm & 0xFFu), dd.x) + __mul24(static_cast<int>((scm >> 8) & 0xFFu), dd.y);
-            const int sm = __mul24(static_cast<int>((scm >> 16) & 0xFFu), bsr[4 * j + h]) +
-                           __mul24(static_cast<int>(scm >> 24), bsr[4 * j + 2 + h]);
-            if (S != nullptr) {  // the block's exact (sd, sm): the octet's partial sums added
-              const int sdb = group_sum(sd, 8), smb = group_sum(sm, 8);
+            const int sm = __mul24(static_cast<int>((scm >> 16) & 0xFFu), xs.x) + __mul24(static_cast<int>(scm >> 24), xs.y);
+            if (S != nullptr) {  // the block's exact (sd, sm): the quad's partial sums added
+              const int sdb = group_sum(sd, 4), smb = group_sum(sm, 4);
               if (rv && q == 0) {
                 int32_t* sp = S + ((static_cast<int64_t>(m) * N + row) * nblk + b) * SPB;
                 sp[0] = sdb;
                 sp[1] = smb;
               }
             }
-            // y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K), each lane adding its chunk's part (the
+            // y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K), each lane adding its group's part (the
             // lane sums meet in the row reduction), so Y does not depend on whether S is stored
             acc[m] = __builtin_fmaf(static_cast<float>(sd), dw * dx, acc[m]);
             acc[m] = __builtin_fmaf(-static_cast<float>(sm), dmin * dx, acc[m]);
@@ -624,7 +634,7 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     lds_attr = lds;
   }
   const Timing tm = timing_slot(gemv_kind(FMT));
-  const int cpb = fmt_info(FMT).qbytes / 16;  // 16-byte chunks per block
+  const int cpb = fmt_info(FMT).qbytes / (FMT == FMT_Q4_K ? 32 : 16);  // lane slots per block
   if ((1 << p.lpr_log2) < cpb) return hipErrorInvalidConfiguration;  // a row group holds whole blocks
   const int bstep = ((1 << p.lpr_log2) / cpb) * NB;
   const int nsteps = nblk > 0 ? (nblk + bstep - 1) / bstep : 1;
@@ -648,7 +658,9 @@ hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
     case 2: return launch_t<FMT, MODE, MC, 2, FUSED>(c, p, s);
     case 4: return launch_t<FMT, MODE, MC, 4, FUSED>(c, p, s);
     case 8: return launch_t<FMT, MODE, MC, 8, FUSED>(c, p, s);
-    case 16: return launch_t<FMT, MODE, MC, 16, FUSED>(c, p, s);
+    case 16:  // Q4_K slots are 32 bytes: nb 16 would hold 192 VGPRs of weights and scales per lane
+      if constexpr (FMT == FMT_Q4_K) return hipErrorInvalidValue;
+      else return launch_t<FMT, MODE, MC, 16, FUSED>(c, p, s);
   }
   return hipErrorInvalidValue;
 }

@@ -139,7 +139,7 @@ int komp_iq4_nl_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int
  *   S i32 [M][N][K/256][2] = (sd, sm): sd = sum_i sc_i * (dot of sub-block i), sm = sum_i m_i * (sum of the
  *      activations of sub-block i), over the 8 sub-blocks of 32 values
  *   Y[m][n] = sum_b f16(d) * d_x * sd - f16(dmin) * d_x * sm                        (ggml vec_dot_q4_K_q8_K)
- * Explicit knobs need block_n / num_warps <= 8 (a row group holds whole 8-chunk blocks).  No matrix-core GEMM: with
+ * A lane loads a 32-byte group of a block per slot, so explicit knobs take nb <= 8.  No matrix-core GEMM: with
  * block_n == 0 every column count runs on the GEMV. */
 int komp_q4_k_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,

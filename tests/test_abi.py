@@ -59,7 +59,7 @@ def test_q4_k_rejects_bad_arguments():
     lib = _abi.lib()
     p16, p8 = ctypes.c_void_p(16), ctypes.c_void_p(8)
     q4k = dict(name="komp_q4_k_gemv", K=256, SW=128)
-    assert _gemv(**q4k, bn=128, nw=8) == _abi.KOMP_EINVAL and "at most 8" in _abi.last_error()  # 16 rows per wave
+    assert _gemv(**q4k, nb=16) == _abi.KOMP_EINVAL and "nb <= 8" in _abi.last_error()  # 32-byte lane slots
     assert _gemv(name="komp_q4_k_gemv", K=288, SW=144) == _abi.KOMP_EINVAL
     assert "multiple of the 256" in _abi.last_error()
     st = lib.komp_q4_k_gemv(p16, p8, p16, p16, p16, None, 1, 4, 256, 128, 32, 4, 2, 4, None)  # WS 8-byte aligned

@@ -16,8 +16,8 @@ PROBLEMS = {"q4_0": ((64, 512, 1), (37, 416, 3), (5, 96, 2)), "tq2_0": ((64, 102
 CONFIGS = {"q4_0": ((32, 4, 4), (16, 2, 2), (64, 8, 4)), "tq2_0": ((32, 2, 4), (16, 1, 2), (64, 4, 4))}
 for _f in ("q8_0", "iq4_nl"):  # the ggml formats beyond the reference's two take Q4_0's problems and knob sets
     PROBLEMS[_f], CONFIGS[_f] = PROBLEMS["q4_0"], CONFIGS["q4_0"]
-PROBLEMS["q4_k"] = PROBLEMS["tq2_0"]  # 256-value blocks; knob sets with at most 8 rows per wave
-CONFIGS["q4_k"] = ((32, 4, 4), (16, 2, 2), (64, 8, 8))
+PROBLEMS["q4_k"] = PROBLEMS["tq2_0"]  # 256-value blocks
+CONFIGS["q4_k"] = ((32, 4, 4), (16, 2, 2), (128, 8, 8))
 
 
 def dev(a):
@@ -154,8 +154,8 @@ def test_gemv_verify_problems(fmt, mode, cfg, prob, extreme):
 @pytest.mark.parametrize("nw", [1, 2, 4, 8])
 def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
     n, k, m = (77, 96 * 32, 3) if O.FORMATS[fmt]["block"] == 32 else (77, 13 * 256, 3)
-    if fmt == "q4_k" and block_n // nw > 8:  # q4_k: a row group of 64 / rows-per-wave lanes must hold 8 chunks
-        with pytest.raises(host._abi.KompArgumentError, match="at most 8"):
+    if fmt == "q4_k" and nb > 8:  # q4_k: a lane slot is a 32-byte group; nb 16 is out of range
+        with pytest.raises(host._abi.KompArgumentError, match="nb <= 8"):
             run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
         return
     y, s, r, rs, _, _ = run_gemv(fmt, n, k, m, 11, False, block_n, nb, 2, nw)
