@@ -316,7 +316,8 @@ def cpu_baseline(args, step_bytes_m, seconds=10.0):
 
 
 DETAIL_SHAPES = (  # (fmt, n, k, m)
-    ("q4_0", 4096, 4096, 1), ("q4_0", 6144, 4096, 1), ("q4_0", 28672, 4096, 1), ("q4_0", 4096, 14336, 1),
+    ("q4_0", 4096, 4096, 1), ("q4_0", 6144, 4096, 1), ("q4_0", 14336, 4096, 1), ("q4_0", 28672, 4096, 1),
+    ("q4_0", 4096, 14336, 1),
     ("q4_0", 4096, 14336, 3), ("q4_0", 128256, 4096, 1), ("q4_0", 28672, 8192, 1), ("tq2_0", 6912, 2560, 1),
     ("tq2_0", 2560, 6912, 1), ("tq2_0", 6912, 2560, 3), ("tq2_0", 32768, 8192, 1), ("q4_0", 4097, 4192, 1),
     ("tq2_0", 6913, 2816, 1), ("q8_0", 4096, 4096, 1), ("q8_0", 14336, 4096, 1), ("q8_0", 4096, 14336, 1),

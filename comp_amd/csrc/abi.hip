@@ -147,6 +147,10 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     const int wq = 8 / rpw < 4 ? 4 : 8 / rpw;
     return plan_of(wq * rpw, nbq, wq, lq, 1);
   }
+  if (!fused && fmt != FMT_TQ2_0 && n >= 12288 && chunks <= 256)
+    // many rows per CU with short rows (Llama-3-8B's gate and up projections, 14336 x 4096): 4-wave workgroups of 8
+    // rows, two rows per wave with 32 lanes each, nb 2 (2-4 K steps); 10-15% faster than one K step of 64 lanes
+    return plan_of(8, 2, 4, 32, 1);
   int lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
   lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
   if (lpr < bpb) lpr = bpb;  // a row group holds whole blocks
