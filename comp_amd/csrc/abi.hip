@@ -62,8 +62,9 @@ TimingState g_timing;
 //   row x nb x 16 bytes covers it) and each wave walks two rows in sequence, nb 4 (8 past 256 chunks), lanes per row
 //   = chunks / nb within 16..64, 4 waves.  Reading whole rows keeps the DRAM accesses of the grid in long runs: with
 //   every workgroup resident, plans that read each row in 1 KB pieces over several steps ran 5-17% slower at
-//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): 16 lanes per row, nb 2, 8 waves, K in
-//   steps of 8 blocks; whole-row and larger-nb plans measured 2-18% slower.
+//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): nb 4, 8 waves, 16 lanes per row, or 8
+//   (8 rows per wave, K in steps of 8 blocks) from 128 chunks per row: 8% faster than nb 2 at 32768 x 8192 and
+//   16384 x 2816.
 //   Latency regime (fewer rows: every wave of the grid is resident at once), one column in dp4a mode, fused launches
 //   and TQ2_0: one workgroup per CU with ceil(N / CUs) rows, one row group per wave, one K step.  A grid of at most
 //   one workgroup per CU is spread one to a CU, so no CU stages (and, fused, quantizes) the activations twice or runs
@@ -113,7 +114,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   const int64_t nblk = k / fmt_info(fmt).block;
   const int64_t chunks = nblk * bpb;                      // lane slots per row (16-byte chunks; Q4_K 32-byte groups)
   if (n >= 16384) {
-    if (fmt == FMT_TQ2_0) return plan_of(32, 2, 8, 16, 1);  // 16 lanes per row, 4 rows per wave, steps of 8 blocks
+    if (fmt == FMT_TQ2_0)  // nb 4; 8 lanes per row (8 rows per wave) from 128 chunks per row, else 16
+      return chunks >= 128 ? plan_of(64, 4, 8, 8, 1) : plan_of(32, 4, 8, 16, 1);
     const int nb = chunks > 256 ? 8 : 4;
     int lpr = pow2_ceil((chunks + nb - 1) / nb);
     lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);

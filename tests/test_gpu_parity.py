@@ -165,7 +165,7 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
 
 @pytest.mark.parametrize("fmt,n,k", [("q4_0", 16384, 8192), ("q4_0", 16400, 4192), ("tq2_0", 16384, 2816),
                                      ("q4_0", 20000, 1024), ("q8_0", 16400, 4192), ("iq4_nl", 16384, 8192),
-                                     ("q8_0", 20000, 1024), ("q4_k", 16400, 4352)])  # fmt: skip
+                                     ("q8_0", 20000, 1024), ("q4_k", 16400, 4352), ("tq2_0", 16400, 8192)])  # fmt: skip
 def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
     # N >= 16384 (16400 and 20000 leave a partial last workgroup); q4_0 reads whole rows in one K step, two passes
     assert host.auto_plan(fmt, 1, n, k)["passes"] == (2 if fmt != "tq2_0" else 1)
