@@ -419,6 +419,7 @@ BATCH_CASES = (  # (name, fmt, N, K): decode projections, several tokens at once
     ("bitnet2b_ffn_down", "tq2_0", 2560, 6912),
     ("llama3_8b_ffn_gate", "q8_0", 14336, 4096),
     ("llama3_8b_ffn_gate", "iq4_nl", 14336, 4096),
+    ("llama3_8b_ffn_gate", "q4_k", 14336, 4096),
 )
 BATCH_M = (4, 16, 64)
 

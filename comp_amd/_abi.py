@@ -58,6 +58,7 @@ SIGNATURES = {
     "komp_q4_k_gemv_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_q4_k_gemv_multi": (_INT, [_INT, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _INT, _P]),
     "komp_q4_k_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
+    "komp_q4_k_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_q4_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_tq2_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_gemm_plan": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _P]),

@@ -195,8 +195,25 @@ constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (
 // (4096x4096, 14336x4096, 4096x14336, 128256x4096) and BitNet-2B shapes, 1..64 columns.  False when the shape is past
 // the kernel's 32-bit buffer offsets (64 * K and 32 * SW below 2^31) or its scale slab does not fit in LDS.
 bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p) {
-  if (fmt == FMT_Q4_K) return false;  // no matrix-core path for Q4_K: its batches run on the GEMV
   if (64 * k > INT32_MAX || 32 * sw > INT32_MAX) return false;
+  if (fmt == FMT_Q4_K) {
+    // Q4_K: the same families with one row tile per wave and at most 2 column tiles (each output also holds the
+    // block's integer sums); long rows move down the family list until the unpacked scale slab fits in LDS
+    const int64_t c16 = (m + 15) / 16;
+    const int64_t groups = (c16 + 1) / 2;
+    const int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
+    const double r = static_cast<double>((n + 15) / 16) * groups / device_cus();
+    static const int kFam[4][2] = {{1, 8}, {2, 4}, {4, 2}, {8, 1}};  // (wk, wr)
+    int f = r > 8.0 ? 0 : (r > 2.0 ? 1 : (r > 1.25 && cn > 1 ? 2 : 3));
+    for (;; ++f) {
+      if (f == 2 && cn == 1) continue;  // (4, 2) only with 2 column tiles
+      const GemmPlan q = {kFam[f][0], kFam[f][1], 1, cn, 2};
+      if (gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax || f == 3) {
+        *p = q;
+        return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;
+      }
+    }
+  }
   const int64_t c16 = (m + 15) / 16;
   const int64_t groups = (c16 + 3) / 4;
   const int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
@@ -310,7 +327,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
           c.xq = a.xq != nullptr ? a.xq + m0 * K : nullptr;
           c.xd = a.xd != nullptr ? a.xd + m0 * nblk : nullptr;
           c.y = mats[i].y + m0 * mats[i].n;
-          c.s = mats[i].s != nullptr ? mats[i].s + m0 * mats[i].n * nblk : nullptr;
+          c.s = mats[i].s != nullptr ? mats[i].s + m0 * mats[i].n * nblk * s_per_block(fmt) : nullptr;
           c.m = static_cast<int>(mc);
           c.n = static_cast<int>(mats[i].n);
           c.k = static_cast<int>(K);
@@ -593,6 +610,13 @@ int komp_q4_k_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* con
                          const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
                          int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream) {
   return gemv_multi_entry(FMT_Q4_K, count, WQ, WS, Y, N, SW, XQ, XD, X, M, K, block_n, nb, mode, num_warps, stream);
+}
+
+int komp_q4_k_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, void* stream) {
+  const GemvMat w{WQ, WS, Y, S, N, SW};
+  const GemvArgs a{&w, 1, XQ, XD, nullptr, nullptr, nullptr, nullptr};
+  return gemv_entry(FMT_Q4_K, false, "komp_q4_k_gemm", a, M, K, 0, 0, KOMP_MODE_DP4A, 0, stream, kRouteGemm);
 }
 
 int komp_q4_k_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream) {

@@ -105,13 +105,14 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   constexpr bool Q8 = FMT == FMT_Q8_0;                           // 32 int8 bytes per 32-value block
   constexpr bool BLK32 = NIB4 || Q8;                             // the 32-value blocks (q8_0 activations)
   constexpr bool TQ2 = FMT == FMT_TQ2_0;
-  constexpr int BPS = NIB4 ? 4 : (Q8 ? 2 : 1);                   // blocks per 64-byte K step
-  const int nsteps = (nblk + BPS - 1) / BPS;                     // K steps
+  constexpr bool QK = FMT == FMT_Q4_K;                           // 256-value blocks, 4 sub-blocks per 64-byte step
+  constexpr int BPS = NIB4 ? 4 : (Q8 ? 2 : 1);                   // blocks per 64-byte K step (Q4_K: half a block)
+  const int nsteps = QK ? 2 * nblk : (nblk + BPS - 1) / BPS;     // K steps
   // row stride of the f32 scale slab in LDS: nblk rounded up to a multiple of 4 (so Q4_0 reads a step's four scales
   // of a row with one 16-byte LDS load)
   const int ss = slab_stride(nblk);
   constexpr int W = WK * WR;
-  constexpr int XV = NIB4 ? 2 : (Q8 ? 1 : 4);                    // 16-byte activation loads per column tile per step
+  constexpr int XV = (NIB4 || QK) ? 2 : (Q8 ? 1 : 4);            // 16-byte activation loads per column tile per step
   constexpr int WGR = 16 * WN * WR;     // rows per workgroup
   constexpr int RPW = WGR / W;          // slab rows each wave stages
   static_assert(RPW >= 1 && RPW * W == WGR, "the waves split the workgroup's rows evenly");
@@ -144,27 +145,27 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
 #pragma unroll
   for (int u = 0; u < CN; ++u) {
     const int c = 16 * u + r16;
-    vx[u] = static_cast<unsigned>(BLK32 ? c * K + 16 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
+    vx[u] = static_cast<unsigned>((BLK32 || QK) ? c * K + 16 * g : c * K + (g >> 1) * 128 + (g & 1) * 16);
     vd[u] = static_cast<unsigned>(c * nblk * 4 + (NIB4 ? 4 * g : (Q8 ? 4 * (g & 1) : 0)));
   }
 
   struct Step {
     u32x4 a[WN];
     u32x4 x[CN][XV];
-    float dx[CN];  // 32-value blocks: d_x of row group g's block of the step; TQ2_0: d_x of block s
+    float dx[CN];  // 32-value blocks: d_x of row group g's block of the step; TQ2_0: d_x of block s; Q4_K: s / 2
   };
   auto load = [&](Step& st, int s) {
     const bool sv = s < nsteps;  // wave-uniform
     const unsigned sa = sv ? 64u * s : kOob;
-    const unsigned sx = sv ? (32u * BPS * (TQ2 ? 8u : 1u)) * s : kOob;  // activation bytes per step
-    const unsigned sd = sv ? 4u * BPS * s : kOob;
+    const unsigned sx = sv ? (QK ? 128u : 32u * BPS * (TQ2 ? 8u : 1u)) * s : kOob;  // activation bytes per step
+    const unsigned sd = sv ? (QK ? 4u * (s >> 1) : 4u * BPS * s) : kOob;
 #pragma unroll
     for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t], sa, 2);  // nt: read once
 #pragma unroll
     for (int u = 0; u < CN; ++u) {
 #pragma unroll
       for (int v = 0; v < XV; ++v)
-        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + (BLK32 ? 64 * v : 32 * v), sx, 0);
+        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + ((BLK32 || QK) ? 64 * v : 32 * v), sx, 0);
       st.dx[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u], sd, 0));
     }
   };
@@ -172,7 +173,37 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   // ---- the scale slab: f32 d_w of the workgroup's rows, row stride ss, zero past row N and past block nblk ----
   // Its first batch of loads is issued before the step loads, so converting it waits for nothing else.
   float* slab = reinterpret_cast<float*>(lds);
-  const auto ws = rsrc(WS + static_cast<int64_t>(n0) * nblk, static_cast<int64_t>(max(0, min(WGR, N - n0))) * nblk * 2);
+  constexpr int SCW = QK ? 8 : 1;  // int16 of WS per block (Q4_K: d, dmin and the 12 packed scale bytes)
+  const auto ws = rsrc(WS + static_cast<int64_t>(n0) * nblk * SCW,
+                       static_cast<int64_t>(max(0, min(WGR, N - n0))) * nblk * 2 * SCW);
+  // Q4_K slab: per (row, block) 6 dwords {f32 d, f32 dmin, scales of sub-blocks 0-3, 4-7, mins 0-3, 4-7 (bytes)},
+  // unpacked once from the 16 scale-plane bytes (ggml get_scale_min_k4's layout) by one lane
+  unsigned* qslab = reinterpret_cast<unsigned*>(lds);
+  u32x4 qraw[QK ? RPW : 1];
+  auto qk_slab_load = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < (QK ? RPW : 0); ++i) {
+      const int col = c0 + lane;
+      qraw[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          ws, col < nblk ? static_cast<unsigned>(((wave * RPW + i) * nblk + col) * 16) : kOob, 0, 0);
+    }
+  };
+  auto qk_slab_store = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < (QK ? RPW : 0); ++i) {
+      const int col = c0 + lane;
+      if (col < nblk) {
+        const u32x4 r = qraw[i];
+        unsigned* e = qslab + ((wave * RPW + i) * nblk + col) * 6;
+        e[0] = __float_as_uint(f16_bits_to_f32(static_cast<int16_t>(r[0] & 0xFFFFu)));
+        e[1] = __float_as_uint(f16_bits_to_f32(static_cast<int16_t>(r[0] >> 16)));
+        e[2] = r[1] & 0x3F3F3F3Fu;
+        e[3] = (r[3] & 0x0F0F0F0Fu) | ((r[1] >> 2) & 0x30303030u);
+        e[4] = r[2] & 0x3F3F3F3Fu;
+        e[5] = ((r[3] >> 4) & 0x0F0F0F0Fu) | ((r[2] >> 2) & 0x30303030u);
+      }
+    }
+  };
   constexpr int kBatch = 4;  // 64-block column chunks per slab row per batch
   unsigned short h[RPW][kBatch];
   auto slab_load = [&](int c0) {
@@ -194,25 +225,44 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
         slab[col < ss ? (wave * RPW + i) * ss + col : WGR * ss + lane] = f16_bits_to_f32(static_cast<int16_t>(h[i][b]));
       }
   };
-  slab_load(0);
+  if constexpr (QK) qk_slab_load(0); else slab_load(0);
 
-  const int my = nsteps > wk ? (nsteps - wk + WK - 1) / WK : 0;  // this wave's steps (wave-uniform)
+  // Wave wk takes steps wk, wk + WK, ...; Q4_K: both halves of blocks wk, wk + WK, ... (its integer sums then stay
+  // within the wave), i.e. steps 2(wk + WK j) and 2(wk + WK j) + 1.
+  auto step_of = [&](int i) { return QK ? 2 * (wk + WK * (i >> 1)) + (i & 1) : wk + WK * i; };
+  const int my = QK ? 2 * (nblk > wk ? (nblk - wk + WK - 1) / WK : 0)
+                    : (nsteps > wk ? (nsteps - wk + WK - 1) / WK : 0);  // this wave's steps (wave-uniform)
   Step ring[D];
 #pragma unroll
-  for (int d = 0; d < D; ++d) load(ring[d], wk + WK * d);
+  for (int d = 0; d < D; ++d) load(ring[d], step_of(d));  // past the wave's steps: zeros
 
-  slab_store(0);
-  for (int c0 = 64 * kBatch; c0 < ss; c0 += 64 * kBatch) {  // rows of more than 64 * kBatch blocks
-    slab_load(c0);
-    slab_store(c0);
+  if constexpr (QK) {
+    qk_slab_store(0);
+    for (int c0 = 64; c0 < nblk; c0 += 64) {  // rows of more than 64 blocks
+      qk_slab_load(c0);
+      qk_slab_store(c0);
+    }
+  } else {
+    slab_store(0);
+    for (int c0 = 64 * kBatch; c0 < ss; c0 += 64 * kBatch) {  // rows of more than 64 * kBatch blocks
+      slab_load(c0);
+      slab_store(c0);
+    }
   }
   __syncthreads();
 
   f32x4 acc[WN][CN];
+  i32x4 qsd[QK ? WN : 1][QK ? CN : 1], qsm[QK ? WN : 1][QK ? CN : 1];  // Q4_K: a block's (sd, sm) so far
 #pragma unroll
   for (int t = 0; t < WN; ++t)
 #pragma unroll
     for (int u = 0; u < CN; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (QK) {
+#pragma unroll
+    for (int t = 0; t < WN; ++t)
+#pragma unroll
+      for (int u = 0; u < CN; ++u) qsd[t][u] = qsm[t][u] = i32x4{0, 0, 0, 0};
+  }
 
   auto store_s = [&](const i32x4& cc, int t, int u, int b) {
     const int col = m0 + 16 * u + r16;
@@ -224,7 +274,77 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   };
 
   auto compute = [&](const Step& st, int s) {
-    if constexpr (BLK32) {
+    if constexpr (QK) {
+      // Q4_K step s = half s % 2 of block s / 2: 64 quant bytes = 32-byte groups j = 2 (s % 2) + {0, 1}, each the
+      // low nibbles of sub-block 2j and the high nibbles of sub-block 2j + 1.  After the transpose ta[t][p] (row
+      // group g) is dword g of the step's 16-byte piece p (group p / 2, half p % 2), so sub-block i of the step (the
+      // block's 4 (s % 2) + i) is {nib(piece 2 (i / 2)), nib(piece 2 (i / 2) + 1)}, low nibbles for even i, high for
+      // odd: the slots of Q4_0's block i, whose B operand the activation loads give unchanged.
+      unsigned ta[WN][4], xt[CN][XV][4];
+#pragma unroll
+      for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
+#pragma unroll
+      for (int u = 0; u < CN; ++u)
+#pragma unroll
+        for (int v = 0; v < XV; ++v) transpose4(st.x[u][v], xt[u][v]);
+      const int hb = s & 1;
+      const int b = s >> 1;
+      long bi[CN][4];
+#pragma unroll
+      for (int u = 0; u < CN; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bi[u][i] = pack2(xt[u][i >> 1][2 * (i & 1)], xt[u][i >> 1][2 * (i & 1) + 1]);
+#pragma unroll
+      for (int t = 0; t < WN; ++t) {
+        const int row_a = 16 * (WN * wr + t) + r16;  // the A operand's row (mins)
+        unsigned scw[4];                             // scales of the C rows 4g + r, this half's 4 sub-blocks
+#pragma unroll
+        for (int r = 0; r < 4; ++r) scw[r] = qslab[((16 * (WN * wr + t) + 4 * g + r) * nblk + b) * 6 + 2 + hb];
+        const unsigned mw = qslab[(row_a * nblk + b) * 6 + 4 + hb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const unsigned p0 = ta[t][2 * (i >> 1)], p1 = ta[t][2 * (i >> 1) + 1];
+          const long ai = (i & 1) ? pack2((p0 >> 4) & NIB, (p1 >> 4) & NIB) : pack2(p0 & NIB, p1 & NIB);
+          const unsigned mb = ((mw >> (8 * i)) & 0xFFu) * 0x01010101u;  // the row's min in every k slot
+#pragma unroll
+          for (int u = 0; u < CN; ++u) {
+            const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(ai, bi[u][i], i32x4{0, 0, 0, 0}, 0, 0, 0);
+            qsm[t][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(pack2(mb, mb), bi[u][i], qsm[t][u], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)  // |cc| < 2^16, scales < 64: a 24-bit multiply-add
+              qsd[t][u][r] += __mul24(static_cast<int>((scw[r] >> (8 * i)) & 0xFFu), cc[r]);
+          }
+        }
+        if (hb == 1) {  // the block is complete: y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float2 dd =
+                *reinterpret_cast<const float2*>(qslab + ((16 * (WN * wr + t) + 4 * g + r) * nblk + b) * 6);
+#pragma unroll
+            for (int u = 0; u < CN; ++u) {
+              acc[t][u][r] = __builtin_fmaf(static_cast<float>(qsd[t][u][r]), dd.x * st.dx[u], acc[t][u][r]);
+              acc[t][u][r] = __builtin_fmaf(-static_cast<float>(qsm[t][u][r]), dd.y * st.dx[u], acc[t][u][r]);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < CN; ++u) {
+            if constexpr (STORE_S) {
+              const int col = m0 + 16 * u + r16;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int row = nw + 16 * t + 4 * g + r;
+                if (col < M && row < N) {
+                  int32_t* sp = S + ((static_cast<int64_t>(col) * N + row) * nblk + b) * 2;
+                  sp[0] = qsd[t][u][r];
+                  sp[1] = qsm[t][u][r];
+                }
+              }
+            }
+            qsd[t][u] = qsm[t][u] = i32x4{0, 0, 0, 0};
+          }
+        }
+      }
+    } else if constexpr (BLK32) {
       // weights (Q4_0, IQ4_NL): row group g holds block 4s+g; after the transpose ta[t][j] (row group g) is dword g of
       // block 4s+j.  Q8_0: row group g holds half g%2 of block 2s + g/2; after the transpose ta[t][2j + h] (row group
       // g) is dword g of half h of block 2s+j.
@@ -337,8 +457,8 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
     for (int d = 0; d < D; ++d) {
       const int i = i0 + d;
       if (i < my) {
-        compute(ring[d], wk + WK * i);
-        load(ring[d], i + D < my ? wk + WK * (i + D) : nsteps);  // past the wave's last step: zeros, no traffic
+        compute(ring[d], step_of(i));
+        load(ring[d], i + D < my ? step_of(i + D) : nsteps);  // past the wave's last step: zeros, no traffic
       }
     }
   }
@@ -427,11 +547,28 @@ hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) 
   return hipErrorInvalidConfiguration;
 }
 
+// Q4_K's plans (gemm_plan in abi.hip): one row tile per wave and at most 2 column tiles, since every output tile
+// also holds the block's two integer sums.
+hipError_t launch_fmt_q4_k(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
+#define KOMP_GEMM_PLAN(WK, WR, WN, CN, D) \
+  if (p.wk == WK && p.wr == WR && p.wn == WN && p.cn == CN && p.d == D) return launch_t<FMT_Q4_K, WK, WR, WN, CN, D>(c, p, stream);
+  KOMP_GEMM_PLAN(8, 1, 1, 1, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 2, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 2, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 1, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 2, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 1, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 2, 2)
+#undef KOMP_GEMM_PLAN
+  return hipErrorInvalidConfiguration;
+}
+
 }  // namespace
 
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k) {
   const int nblk = k / fmt_info(fmt).block;
-  const size_t slab = (static_cast<size_t>(16) * p.wn * p.wr * gemm_impl::slab_stride(nblk) + 64) * 4;  // + spill slots
+  const size_t slab = fmt == FMT_Q4_K ? static_cast<size_t>(16) * p.wn * p.wr * nblk * 24  // 6 dwords a block
+                                      : (static_cast<size_t>(16) * p.wn * p.wr * gemm_impl::slab_stride(nblk) + 64) * 4;
   const size_t red = p.wk > 1 ? static_cast<size_t>(p.wk) * p.wr * p.wn * p.cn * 4 * 64 * 4 : 0;
   return slab > red ? slab : red;
 }
@@ -442,6 +579,7 @@ hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream)
     case FMT_TQ2_0: return launch_fmt<FMT_TQ2_0>(c, p, stream);
     case FMT_Q8_0: return launch_fmt<FMT_Q8_0>(c, p, stream);
     case FMT_IQ4_NL: return launch_fmt<FMT_IQ4_NL>(c, p, stream);
+    case FMT_Q4_K: return launch_fmt_q4_k(c, p, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -250,8 +250,6 @@ def gemv(fmt, wq, ws, xq, xd, n, k, block_n=32, nb=4, mode=0, num_warps=4, store
 
 
 def _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k):
-    if fmt == "q4_k":
-        raise _abi.KompArgumentError("gemm: q4_k has no matrix-core GEMM; gemv runs its batches")
     fn = f"komp_{fmt}_gemm"
     with torch.cuda.device(xq.device):
         _abi.call(fn, wq.data_ptr(), ws.data_ptr(), xq.data_ptr(), xd.data_ptr(), y.data_ptr(),
@@ -266,7 +264,7 @@ def gemm(fmt, wq, ws, xq, xd, n, k, store_s=False):
     on."""
     m, nblk = _check_gemv(fmt, wq, ws, xq, xd, n, k)
     y = torch.empty((m, n), dtype=torch.float32, device=xq.device)
-    s = torch.zeros((m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
+    s = torch.zeros(_s_shape(fmt, m, n, nblk), dtype=torch.int32, device=xq.device) if store_s else None
     _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k)
     return y, s
 
@@ -278,9 +276,10 @@ def gemm_into(fmt, wq, ws, xq, xd, y, n, k, s=None):
     if tuple(y.shape) != (m, n) or not y.is_contiguous():
         raise _abi.KompArgumentError(f"gemm_into: y must be a contiguous [{m}][{n}] tensor")
     if s is not None:
-        _need(s, "s", torch.int32, 3)
-        if tuple(s.shape) != (m, n, nblk) or not s.is_contiguous():
-            raise _abi.KompArgumentError(f"gemm_into: s must be a contiguous [{m}][{n}][{nblk}] tensor")
+        shape = _s_shape(fmt, m, n, nblk)
+        _need(s, "s", torch.int32, len(shape))
+        if tuple(s.shape) != shape or not s.is_contiguous():
+            raise _abi.KompArgumentError(f"gemm_into: s must be a contiguous {list(shape)} tensor")
     _launch_gemm(fmt, wq, ws, xq, xd, y, s, n, k)
 
 

@@ -139,8 +139,9 @@ int komp_iq4_nl_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int
  *   S i32 [M][N][K/256][2] = (sd, sm): sd = sum_i sc_i * (dot of sub-block i), sm = sum_i m_i * (sum of the
  *      activations of sub-block i), over the 8 sub-blocks of 32 values
  *   Y[m][n] = sum_b f16(d) * d_x * sd - f16(dmin) * d_x * sm                        (ggml vec_dot_q4_K_q8_K)
- * A lane loads a 32-byte group of a block per slot, so explicit knobs take nb <= 8.  No matrix-core GEMM: with
- * block_n == 0 every column count runs on the GEMV. */
+ * A lane loads a 32-byte group of a block per slot, so explicit knobs take nb <= 8.  komp_q4_k_gemm is the
+ * matrix-core GEMM for any M (komp_q4_0_gemm's contract; S as above), and block_n == 0 in dp4a mode routes 4+
+ * columns to it. */
 int komp_q4_k_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                    void* stream);
@@ -150,6 +151,8 @@ int komp_q4_k_gemv_f32(const uint8_t* WQ, const int16_t* WS, const float* X, flo
 int komp_q4_k_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,
                          const int64_t* N, const int64_t* SW, const int8_t* XQ, const float* XD, const float* X,
                          int64_t M, int64_t K, int block_n, int nb, int mode, int num_warps, void* stream);
+int komp_q4_k_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
+                   int64_t M, int64_t N, int64_t K, int64_t SW, void* stream);
 int komp_q4_k_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64_t K, int64_t SW, void* stream);
 
 /* The plan that block_n == 0 selects for a GEMV shape on the current device; fmt 0 = q4_0, 1 = tq2_0, 2 = q8_0,

@@ -66,7 +66,11 @@ def test_q4_k_rejects_bad_arguments():
     assert st == _abi.KOMP_EINVAL and "16-byte aligned" in _abi.last_error()
     st = lib.komp_q4_k_split(p16, p16, p8, 4, 256, 128, None)
     assert st == _abi.KOMP_EINVAL and "WS 16-byte aligned" in _abi.last_error()
-    assert lib.komp_gemm_plan(4, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL  # no q4_k GEMM
+    rows, cols, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.komp_gemm_plan(4, 64, 4096, 4096, 2048, ctypes.byref(rows), ctypes.byref(cols), ctypes.byref(waves)) == 0
+    assert cols.value == 32 and rows.value <= 128  # q4_k: at most 2 column tiles, one row tile per wave
+    st = lib.komp_q4_k_gemm(p16, p8, p16, p16, p16, None, 4, 4, 256, 128, None)
+    assert st == _abi.KOMP_EINVAL and "16-byte aligned" in _abi.last_error()
 
 
 def test_empty_shapes_are_no_ops():
@@ -142,8 +146,8 @@ def test_auto_plan(fmt, n, k, fused):
         assert blocks_per_step >= nblk or nb == 4  # one K step unless the q4_0 nb cap applies
     elif fmt == 0:  # throughput regime, q4_0: whole rows in one K step, two passes per wave
         assert passes == 2 and nw == 4 and bn == nw * (64 // lanes) * 2 and (blocks_per_step >= nblk or lanes == 64)
-    else:
-        assert (bn, nb, nw, lanes, passes) == (32, 2, 8, 16, 1)
+    else:  # throughput regime, tq2_0: nb 4, 8 lanes per row from 128 chunks per row, else 16
+        assert (bn, nb, nw, lanes, passes) == ((64, 4, 8, 8, 1) if 4 * nblk >= 128 else (32, 4, 8, 16, 1))
 
 
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])

@@ -1,4 +1,4 @@
-"""Matrix-core GEMM (komp_{q4_0,tq2_0,q8_0,iq4_nl}_gemm) vs the oracle: int32 block dots S exact, Y within 1e-5
+"""Matrix-core GEMM (komp_{q4_0,tq2_0,q8_0,iq4_nl,q4_k}_gemm) vs the oracle: int32 block dots S exact, Y within 1e-5
 (norm-wise) of the f64 reference_dot, on the same seeded problems.  Shapes cover the kernel's tails: rows not a
 multiple of 16, column counts around the 16-column tiles and the 64-column workgroups, Q4_0 block counts that are not
 a multiple of the 4-block K step, scale planes that take the 2-byte staging path, padded weight rows, and the
@@ -23,6 +23,8 @@ SHAPES = {
               (100, 2560, 33), (40, 6912, 64), (48, 256, 65), (300, 512, 130)],
 }
 SHAPES["q8_0"] = SHAPES["iq4_nl"] = SHAPES["q4_0"]
+SHAPES["q4_k"] = SHAPES["tq2_0"]  # 256-value blocks
+BLK32 = ("q4_0", "q8_0", "iq4_nl")
 
 
 def dev(a):
@@ -49,7 +51,7 @@ def check(fmt, n, k, m, seed, extreme=False, ws_offset=0, pad=0):
     return y
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 @pytest.mark.parametrize("shape", range(10))
 @pytest.mark.parametrize("extreme", [False, True])
 def test_gemm_matches_oracle(fmt, shape, extreme):
@@ -57,11 +59,12 @@ def test_gemm_matches_oracle(fmt, shape, extreme):
     check(fmt, n, k, m, 300 + shape, extreme)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemm_unaligned_scales_and_padded_rows(fmt):
-    k = 416 if fmt != "tq2_0" else 768
-    check(fmt, 45, k, 20, 11, ws_offset=1, pad=48)
-    check(fmt, 64, 2 * k if fmt != "tq2_0" else 1024, 8, 12, ws_offset=3)
+    k = 416 if fmt in BLK32 else 768
+    odd = (1, 3) if fmt != "q4_k" else (8, 24)  # q4_k's 16-byte scale entries need a 16-byte aligned plane
+    check(fmt, 45, k, 20, 11, ws_offset=odd[0], pad=48)
+    check(fmt, 64, 2 * k if fmt in BLK32 else 1024, 8, 12, ws_offset=odd[1])
 
 
 # one shape per plan family on a 256-CU device: (n, k, m, rows per workgroup, columns per workgroup)
@@ -76,23 +79,23 @@ FAMILIES = [
 ]
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 @pytest.mark.parametrize("fam", range(len(FAMILIES)))
 def test_gemm_plan_families(fmt, fam):
     n, k, m, rows, cols = FAMILIES[fam]
-    if fmt == "tq2_0":
+    if fmt in ("tq2_0", "q4_k"):
         k = 512 if k == 256 else 1024
     if fmt == "q8_0" and rows == 256:
         rows = 128  # Q8_0 waves take one row tile each (two would need more than 256 VGPRs)
     plan = host.gemm_plan(fmt, m, n, k)
-    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256 and fmt != "q4_k":  # q4_k: its own families
         assert (plan["rows"], plan["cols"]) == (rows, cols), plan
     check(fmt, n, k, m, 60 + fam)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemv_auto_routes_batches_to_gemm(fmt):
-    n, k, m = (96, 1024, 12) if fmt != "tq2_0" else (96, 1536, 12)
+    n, k, m = (96, 1024, 12) if fmt in BLK32 else (96, 1536, 12)
     W, x = O.problem(fmt, n, k, m, 31)
     wq, ws = host.split(fmt, W, n, k)
     xq, xd, *_ = host.quantize(fmt, dev(x))
@@ -111,7 +114,7 @@ def test_gemv_auto_routes_batches_to_gemm(fmt):
     assert O.relerr(y_gemm.cpu().numpy(), r) <= TOL and O.relerr(y_gemv.cpu().numpy(), r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemm_multi_matrix_batches(fmt):
     k = 512
     ns = (40, 24, 64)
@@ -131,7 +134,7 @@ def test_gemm_multi_matrix_batches(fmt):
         assert O.relerr(y.cpu().numpy(), r) <= TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemm_empty_k_writes_zeros(fmt):
     n, m = 20, 5
     wq = torch.zeros((n, 16), dtype=torch.uint8, device="cuda")  # a row stride of 16 bytes, no quant bytes used
@@ -144,9 +147,9 @@ def test_gemm_empty_k_writes_zeros(fmt):
     assert torch.count_nonzero(y).item() == 0
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl"])
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k"])
 def test_gemm_graph_replays(fmt):
-    n, k, m = (200, 1024, 24) if fmt != "tq2_0" else (200, 1280, 24)
+    n, k, m = (200, 1024, 24) if fmt in BLK32 else (200, 1280, 24)
     W, x = O.problem(fmt, n, k, m, 51)
     wq, ws = host.split(fmt, W, n, k)
     wq, ws = dev(wq), dev(ws)
@@ -166,3 +169,13 @@ def test_gemm_graph_replays(fmt):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, y_eager)
+
+
+@pytest.mark.parametrize("m", [4, 16, 33])
+def test_q4_k_gemm_plans_and_long_rows(m):
+    # every Q4_K plan family (one row tile per wave, 1-2 column tiles) and a row long enough that the unpacked scale
+    # slab pushes the plan down the family list
+    for n, k in ((4000, 512), (9600, 512), (33600, 256), (700, 14336)):
+        plan = host.gemm_plan("q4_k", m, n, k)
+        assert plan is not None and plan["cols"] <= 32 and plan["rows"] <= 128, plan
+        check("q4_k", n, k, m, 90 + m)
