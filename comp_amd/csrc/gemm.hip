@@ -1,5 +1,5 @@
-// Batched-column GEMMs on the gfx950 matrix cores: Q4_0, Q8_0 and IQ4_NL x q8_0, TQ2_0 x q8_K, for any number M of
-// activation columns, with the decode GEMVs' result definition (src/komp/kernels.py:48-94 and :97-142):
+// Batched-column GEMMs on the gfx950 matrix cores: Q4_0, Q8_0 and IQ4_NL x q8_0, TQ2_0 and Q4_K x q8_K, for any number
+// M of activation columns, with the decode GEMVs' result definition (src/komp/kernels.py:48-94 and :97-142):
 //   Y[m][n] = sum_b d_w(n, b) * d_x(m, b) * s(m, n, b),  s = the exact int32 dot of weight block b of row n with
 //   activation block b of column m,
 // and the same optional S [M][N][K/block] of exact block dots.  The GEMVs stream the weights once per 1..3 columns;
@@ -27,6 +27,10 @@
 //          select per dword), which gives signed values: no offset.
 //   TQ2_0  group g holds bytes 16g..16g+15 of the block; crumb j of byte 16g+e is value (g/2)*128 + 32j + 16(g%2) + e
 //          (kernels.py:102), so B for crumb j is 16 contiguous activation bytes and nothing is transposed.
+//   Q4_K   a step is half a 256-value block (4 sub-blocks of 32); after the transpose sub-block i is the low (even i)
+//          or high (odd i) nibbles of pieces 2(i/2) and 2(i/2)+1, i.e. Q4_0's block i; each sub-block's dot is
+//          weighted by its 6-bit scale in registers and a second MFMA with the row's 6-bit min in every k slot
+//          accumulates the mins term (see compute).
 // Nibbles and crumbs go in unsigned (0..15, 0..2).  Their offset (-8, resp. -1, times the block's activation sum)
 // comes from one more MFMA of a constant A (every byte -8, resp. -1) with the same B, which starts the accumulator,
 // so every C element is the exact block dot s.  C element r of lane (c, g) is row 4g + r, column c.
@@ -90,7 +94,7 @@ __device__ __forceinline__ long pack2(unsigned lo, unsigned hi) {
   return static_cast<long>(static_cast<unsigned long>(lo) | (static_cast<unsigned long>(hi) << 32));
 }
 
-// FMT: FMT_Q4_0 / FMT_TQ2_0.  WK x WR waves: WR row groups of WN 16-row tiles each, every group's K split over WK
+// FMT: any weight format above.  WK x WR waves: WR row groups of WN 16-row tiles each, every group's K split over WK
 // waves.  CN 16-column tiles.  D steps in flight per wave.  STORE_S: also write the block dots to S (a separate
 // instantiation, so the plain kernel's step loop has no branch between an MFMA and the scaling of its result).
 template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
