@@ -197,17 +197,17 @@ constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (
 bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p) {
   if (64 * k > INT32_MAX || 32 * sw > INT32_MAX) return false;
   if (fmt == FMT_Q4_K) {
-    // Q4_K: the same families with one row tile per wave and at most 2 column tiles (each output also holds the
-    // block's integer sums); long rows move down the family list until the unpacked scale slab fits in LDS
+    // Q4_K: the same families with one row tile per wave (each output also holds the block's two integer sums);
+    // long rows move down the family list until the unpacked scale slab fits in LDS
     const int64_t c16 = (m + 15) / 16;
-    const int64_t groups = (c16 + 1) / 2;
+    const int64_t groups = (c16 + 3) / 4;
     const int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
     const double r = static_cast<double>((n + 15) / 16) * groups / device_cus();
     static const int kFam[4][2] = {{1, 8}, {2, 4}, {4, 2}, {8, 1}};  // (wk, wr)
     int f = r > 8.0 ? 0 : (r > 2.0 ? 1 : (r > 1.25 && cn > 1 ? 2 : 3));
     for (;; ++f) {
-      if (f == 2 && cn == 1) continue;  // (4, 2) only with 2 column tiles
-      const GemmPlan q = {kFam[f][0], kFam[f][1], 1, cn, 2};
+      if (f == 2 && cn == 1) continue;  // (4, 2) only with 2+ column tiles
+      const GemmPlan q = {kFam[f][0], kFam[f][1], 1, cn, f == 0 && cn > 2 ? 1 : 2};
       if (gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax || f == 3) {
         *p = q;
         return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;

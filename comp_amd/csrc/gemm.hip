@@ -551,8 +551,8 @@ hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) 
   return hipErrorInvalidConfiguration;
 }
 
-// Q4_K's plans (gemm_plan in abi.hip): one row tile per wave and at most 2 column tiles, since every output tile
-// also holds the block's two integer sums.
+// Q4_K's plans (gemm_plan in abi.hip): one row tile per wave, since every output tile also holds the block's two
+// integer sums.
 hipError_t launch_fmt_q4_k(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
 #define KOMP_GEMM_PLAN(WK, WR, WN, CN, D) \
   if (p.wk == WK && p.wr == WR && p.wn == WN && p.cn == CN && p.d == D) return launch_t<FMT_Q4_K, WK, WR, WN, CN, D>(c, p, stream);
@@ -563,6 +563,14 @@ hipError_t launch_fmt_q4_k(const GemmCall& c, const GemmPlan& p, hipStream_t str
   KOMP_GEMM_PLAN(2, 4, 1, 2, 2)
   KOMP_GEMM_PLAN(1, 8, 1, 1, 2)
   KOMP_GEMM_PLAN(1, 8, 1, 2, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 3, 2)
+  KOMP_GEMM_PLAN(8, 1, 1, 4, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 3, 2)
+  KOMP_GEMM_PLAN(4, 2, 1, 4, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 3, 2)
+  KOMP_GEMM_PLAN(2, 4, 1, 4, 2)
+  KOMP_GEMM_PLAN(1, 8, 1, 3, 1)
+  KOMP_GEMM_PLAN(1, 8, 1, 4, 1)
 #undef KOMP_GEMM_PLAN
   return hipErrorInvalidConfiguration;
 }

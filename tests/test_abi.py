@@ -68,7 +68,7 @@ def test_q4_k_rejects_bad_arguments():
     assert st == _abi.KOMP_EINVAL and "WS 16-byte aligned" in _abi.last_error()
     rows, cols, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.komp_gemm_plan(4, 64, 4096, 4096, 2048, ctypes.byref(rows), ctypes.byref(cols), ctypes.byref(waves)) == 0
-    assert cols.value == 32 and rows.value <= 128  # q4_k: at most 2 column tiles, one row tile per wave
+    assert cols.value == 64 and rows.value <= 128  # q4_k: one row tile per wave
     st = lib.komp_q4_k_gemm(p16, p8, p16, p16, p16, None, 4, 4, 256, 128, None)
     assert st == _abi.KOMP_EINVAL and "16-byte aligned" in _abi.last_error()
 

@@ -177,5 +177,5 @@ def test_q4_k_gemm_plans_and_long_rows(m):
     # slab pushes the plan down the family list
     for n, k in ((4000, 512), (9600, 512), (33600, 256), (700, 14336)):
         plan = host.gemm_plan("q4_k", m, n, k)
-        assert plan is not None and plan["cols"] <= 32 and plan["rows"] <= 128, plan
+        assert plan is not None and plan["cols"] <= 64 and plan["rows"] <= 128, plan
         check("q4_k", n, k, m, 90 + m)
