@@ -46,13 +46,17 @@ __device__ __forceinline__ void iq4_nl_lut(unsigned q, unsigned& lo, unsigned& h
   constexpr unsigned T1 = 0xF6EADDCFu;  // -49, -35, -22, -10
   constexpr unsigned T2 = 0x26190D01u;  // 1, 13, 25, 38
   constexpr unsigned T3 = 0x71594535u;  // 53, 69, 89, 113
+  // The identity selector lives in a VGPR (a plain v_mov the compiler hoists), so each merge selector is one
+  // v_and_or_b32 (a VOP3 encoding holds one literal or SGPR constant, not the two the expression has).
+  unsigned ident;
+  asm("v_mov_b32 %0, 0x3020100" : "=v"(ident));
   const unsigned r = q >> 4;  // byte j: the high nibble of q byte j in its low 4 bits
   const unsigned sl = q & 0x07070707u;
   const unsigned sh = r & 0x07070707u;
   const unsigned l0 = __builtin_amdgcn_perm(T1, T0, sl), l1 = __builtin_amdgcn_perm(T3, T2, sl);
   const unsigned h0 = __builtin_amdgcn_perm(T1, T0, sh), h1 = __builtin_amdgcn_perm(T3, T2, sh);
-  lo = __builtin_amdgcn_perm(l1, l0, ((q >> 1) & 0x04040404u) | 0x03020100u);
-  hi = __builtin_amdgcn_perm(h1, h0, ((r >> 1) & 0x04040404u) | 0x03020100u);
+  lo = __builtin_amdgcn_perm(l1, l0, ((q >> 1) & 0x04040404u) | ident);
+  hi = __builtin_amdgcn_perm(h1, h0, ((r >> 1) & 0x04040404u) | ident);
 }
 
 // Signed byte e of a 32-bit word.
