@@ -15,11 +15,11 @@ Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: wei
 / their wall time (GB/s); roofline = the tq2_0_gemv
 dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
 (the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
-sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list (cold,
-library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
+sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list and
+Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
 gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
-(Q4_0) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3 columns; ingest = ggml block
-bytes split into the planes on the device.
+(Q4_0, and 14336 x 4096 in Q8_0, IQ4_NL and Q4_K) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against
+GEMV launches of 3 columns; ingest = ggml block bytes split into the planes on the device.
 """
 
 from __future__ import annotations

@@ -14,6 +14,12 @@ Differences a caller can observe:
   * gemv(..., block_n=None) lets the library choose block_n / nb / num_warps for the shape.
   * arguments the kernels cannot take (K not a multiple of the block, misaligned or strided planes, unknown knobs)
     raise KompArgumentError (a ValueError) instead of reading out of bounds.
+
+Beyond the reference: gemm (the matrix-core batched GEMM, which gemv(..., block_n=None) uses from GEMM_MIN_M
+columns), gemv_f32 (quantize and GEMV in one launch), gemv_multi (several matrices sharing one input), split_device
+(ggml blocks split on the device), the *_into variants that write preallocated outputs, and three more ggml weight
+formats in every call: q8_0, iq4_nl (q8_0 activations) and q4_k (q8_K activations; its scale plane holds each
+block's 16 leading bytes and its S two int32 per block).
 """
 
 from __future__ import annotations

@@ -1,4 +1,6 @@
-/* C ABI of the MI355X (gfx950) decode path of COMP: activation quantizers and Q4_0 / TQ2_0 decode GEMVs.
+/* C ABI of the MI355X (gfx950) decode path of COMP: activation quantizers, the Q4_0 / TQ2_0 decode GEMVs of the
+ * reference, batched matrix-core GEMMs, weight splitting on the device, and the ggml formats Q8_0, IQ4_NL and Q4_K
+ * (declared further below) through the same entries.
  *
  * Plain C: pointers are device pointers (HIP), sizes are int64_t, `stream` is a hipStream_t passed as void*
  * (NULL = the default stream).  Every call is asynchronous on `stream` and allocates nothing.  Each entry validates
