@@ -86,12 +86,16 @@ def cmd_verify(args):
 
 # GEMV configs listed by `mix` (block_n, nb, num_warps), the reference's set (src/komp/cli.py:136)
 MIX_KOMP = {"q4_0": ((64, 4, 4), (32, 8, 4)), "tq2_0": ((64, 1, 4), (32, 2, 4))}
-VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64}  # weights per 16-byte weight load
+# the ggml formats beyond the reference's two, at the library's common plan shape
+MIX_MORE = {"q8_0": ((64, 4, 4),), "iq4_nl": ((64, 4, 4),), "q4_k": ((64, 2, 4),)}
+# weights per 16-byte load of the hot loop (q4_k: a slot's two weight loads come with one 16-byte scale-entry load)
+VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64, "q8_0": 16, "iq4_nl": 32, "q4_k": 64 / 3}
+FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kernels' format template argument
 
 
 def _gemv_kernel(fmt, mode, nb, m=1):
     """The gemv_kernel instantiation a launch of this config runs: <format, mode, columns per launch, nb, fused>."""
-    return f"gemv_impl::gemv_kernel<{0 if fmt == 'q4_0' else 1}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
+    return f"gemv_impl::gemv_kernel<{FMT_NUM[fmt]}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
 
 
 def _mix_line(r, name):
@@ -180,6 +184,12 @@ def cmd_mix(args):
                             + (" SPILL" if spill else ""))  # fmt: skip
                     print(_mix_line(r, name))
             print(f"KURN-CUDA {fmt}: not available (NVIDIA target; this build holds gfx950 code only)")
+        for fmt, cfgs in MIX_MORE.items():
+            for bn, nb, nw in cfgs:
+                r = isa.summary(_gemv_kernel(fmt, 2, nb), VALUES_PER_LOAD[fmt])
+                spill = r["vgpr_spill"] + r["sgpr_spill"]
+                fails += bool(spill or r["approx"])
+                print(_mix_line(r, f"KOMP {fmt} dp4a  {bn}/{nb}/{nw}w v{r['vgpr']}" + (" SPILL" if spill else "")))
         for prefix, label in (("gemm_impl::gemm_kernel<0, 8, 1, 1, 1, 2, false>", "GEMM q4_0 16 rows x 16 cols"),
                               ("gemm_impl::gemm_kernel<0, 8, 1, 1, 4, 2, false>", "GEMM q4_0 16 rows x 64 cols"),
                               ("gemm_impl::gemm_kernel<1, 8, 1, 1, 1, 2, false>", "GEMM tq2_0 16 rows x 16 cols")):

@@ -58,6 +58,9 @@ def test_mix_lists_every_config():
         for bn, nb, nw in cfgs:
             for mode in ("bytes", "dp4a "):
                 assert f"KOMP {fmt} {mode} {bn}/{nb}/{nw}w" in r.stdout
+    for fmt, cfgs in cli.MIX_MORE.items():
+        for bn, nb, nw in cfgs:
+            assert f"KOMP {fmt} dp4a  {bn}/{nb}/{nw}w" in r.stdout
     assert "GEMM q4_0 16 rows x 64 cols" in r.stdout and "v_mfma 64" in r.stdout
     assert run("mix", "--archs", "sm_80").stdout.count("not built") == 1
 
