@@ -426,7 +426,7 @@ BATCH_M = (4, 16, 64)
 
 def batched_detail(torch, host, args):
     """Several activation columns (batched decode tokens) per weight matrix, q8 activations in: the matrix-core GEMM
-    (what gemv with block_n=None runs from 4 columns) vs the GEMV in launches of 3 columns (its own knobs for that
+    (what gemv with block_n=None runs from 4 columns, TQ2_0 from 3) vs the GEMV in launches of 3 columns (its own knobs for that
     column count), both as graph replays over cold weight copies.  Bytes: weights + q8 activations + f32 outputs."""
     rows = []
     gen = torch.Generator(device="cuda")

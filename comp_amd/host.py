@@ -46,7 +46,8 @@ for _f in FORMATS.values():
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
 FMT_ID = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}
 _XB_F32 = ("q4_0", "tq2_0", "q4_k")  # formats whose gemv_f32 entry takes the XB (bsums) output
-GEMM_MIN_M = {f: 4 for f in FMT_ID}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
+# columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM (abi.hip gemm_min_m)
+GEMM_MIN_M = {f: 3 if f == "tq2_0" else 4 for f in FMT_ID}
 
 
 def split(fmt, W, n, k):
@@ -299,7 +300,7 @@ def gemm_plan(fmt, m, n, k, sw=None):
 
 
 def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
-    """True when gemv(..., block_n=None) runs the matrix-core GEMM for this shape (unfused, dp4a, from 4 columns)."""
+    """True when gemv(..., block_n=None) runs the matrix-core GEMM for this shape (unfused, dp4a, from GEMM_MIN_M columns)."""
     return not fused and mode == 2 and m >= GEMM_MIN_M[fmt] and gemm_plan(fmt, m, n, k, sw) is not None
 
 
