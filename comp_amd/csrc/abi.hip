@@ -114,8 +114,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   const int64_t nblk = k / fmt_info(fmt).block;
   const int64_t chunks = nblk * bpb;                      // lane slots per row (16-byte chunks; Q4_K 32-byte groups)
   if (n >= 16384) {
-    if (fmt == FMT_TQ2_0)  // nb 4; 8 lanes per row (8 rows per wave) from 128 chunks per row, else 16
-      return chunks >= 128 ? plan_of(64, 4, 8, 8, 1) : plan_of(32, 4, 8, 16, 1);
+    if (fmt == FMT_TQ2_0)  // 16 lanes per row (4 rows per wave), nb 4, 8 waves: the fastest of a sweep over knob sets
+      return plan_of(32, 4, 8, 16, 1);                      // at 16400-32768 rows x 4096-8192 columns
     const int nb = chunks > 256 ? 8 : 4;
     int lpr = pow2_ceil((chunks + nb - 1) / nb);
     lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);

@@ -1,0 +1,307 @@
+// Single-column TQ2_0 decode GEMV in dp4a mode (the BitNet decode step), unfused (q8_K in) and fused with the q8_K
+// quantizer.  Same plans, results and S as the general kernel in gemv_kernel.h (kernels.py:97-142 semantics); the
+// lanes per row group and the chunks per lane are template arguments here, which is what makes it leaner:
+//   * weight and scale loads are buffer loads from loop-invariant per-lane offsets, the tile and chunk offsets being
+//     a scalar and an immediate.  A chunk past the row's last block, and every row past the matrix, reads zeros
+//     without touching memory (the buffer range check), so no load sits behind a branch and the compiler waits for
+//     each chunk's own load instead of for the whole tile;
+//   * the activation column lies in LDS in its natural order, 288 bytes per 256-value block (the 32-byte pad puts the
+//     four lane quads of a 16-lane row group on disjoint banks), so a chunk's four 16-byte activation pieces are one
+//     base address plus immediates;
+//   * each lane accumulates d_x * d_w * (its chunk's partial dot) in f32 and the row group's lanes are added at the
+//     end; the block dots of S are added across the lane quad only when S is stored;
+//   * the activation loads of the staging are issued before the weight loads, and the barrier that publishes the
+//     staged column waits for LDS writes only, so the weights stay in flight through the staging.
+#include <hip/hip_ext.h>
+
+#include "komp_device.h"
+#include "komp_internal.h"
+
+namespace komp {
+namespace gemv_tq2 {
+
+constexpr int kBlockStride = 288;        // LDS bytes per staged 256-value block
+constexpr unsigned kOob = 0x7FFFFFF0u;   // a buffer offset past every descriptor's range: the load returns zeros
+constexpr size_t kLdsLimit = 160 * 1024;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  const int n = static_cast<int>(bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);  // raw, 32-bit data
+}
+
+// The partial int32 dot of one 16-byte chunk with its four 16-byte activation pieces (piece j pairs with the crumbs
+// at bits 2j): three accumulators for the crumbs masked in place (x1, x4, x16) and one shift for the fourth.
+__device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], int init) {
+  int a1 = init, a4 = 0, a16 = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    a1 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x03030303u), static_cast<int>(x[0][d]), a1, false);
+    a4 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x0C0C0C0Cu), static_cast<int>(x[1][d]), a4, false);
+    a16 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x30303030u), static_cast<int>(x[2][d]), a16, false);
+    a16 = __builtin_amdgcn_sdot4(static_cast<int>((w[d] >> 2) & 0x30303030u), static_cast<int>(x[3][d]), a16, false);
+  }
+  return ((a1 << 4) + (a4 << 2) + a16) >> 4;
+}
+
+// LPR lanes per row group (4 per block: lane q of a quad takes bytes 16q..16q+15 of the block), NB chunks per lane
+// per K step.  The arguments every first load needs fill the 14 preloaded argument dwords.
+template <int LPR, int NB, bool FUSED>
+__global__ void __launch_bounds__(1024)
+tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
+              const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
+              float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
+              int16_t* __restrict__ XBo, int nseg, const GemvSegs segs) {
+  constexpr int RPW = 64 / LPR;          // rows per wave and pass
+  constexpr int BPG = LPR / 4;           // blocks a row group covers per chunk slot
+  constexpr int BSTEP = BPG * NB;        // blocks per K step
+  constexpr int XB = kBlockStride;
+  extern __shared__ __align__(16) unsigned char lds[];
+  int N = N1;
+  int64_t SW = SW1;
+  const uint8_t* WQ = WQ1;
+  const int16_t* WS = WS1;
+  float* Y = Y1;
+  int wg = blockIdx.x;
+  if (nseg > 1) {  // several matrices sharing the column: this workgroup's one (scalar compares on the arguments)
+    int sg = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; ++i)
+      if (i < nseg && wg >= segs.first_wg[i]) sg = i;
+    N = segs.n[sg];
+    SW = segs.sw[sg];
+    WQ = segs.wq[sg];
+    WS = segs.ws[sg];
+    Y = segs.y[sg];
+    wg -= segs.first_wg[sg];
+  }
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane & 3;
+  const int gblk = (lane & (LPR - 1)) >> 2;
+  const int grp = lane / LPR;
+  const int nsteps = (nblk + BSTEP - 1) / BSTEP;
+  const int nblk_pad = nsteps * BSTEP;
+  const int rows_per_wave = RPW * passes;
+  const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
+  const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);
+  const int vrows = max(0, min(wave_rows, N - row_base));  // rows of this wave inside the matrix
+  const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base) * SW, static_cast<int64_t>(vrows) * SW);
+  const auto srs = rsrc(WS + static_cast<int64_t>(row_base) * nblk, static_cast<int64_t>(vrows) * nblk * 2);
+  const unsigned vo_w = static_cast<unsigned>(grp * SW + gblk * 64 + q * 16);
+  const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
+
+  // ---- the staging's first loads (16 threads per block), issued before the weights so they do not queue behind
+  // them: f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) for thread i ----
+  const int nstage = nblk * 16;
+  const bool stg = tid < nstage;
+  f32x4 xf[4];
+  u32x4 x16;
+  float xdv = 0.0f;
+  if (stg) {
+    if constexpr (FUSED) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + tid * 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xf[t] = src[t];
+    } else {
+      x16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 16);
+      if ((tid & 15) == 0) xdv = XD[tid >> 4];
+    }
+  }
+
+  // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk ----
+  u32x4 w[NB];
+  int16_t sc[NB];
+  auto load = [&](int p, int st) {
+    const unsigned so_w = static_cast<unsigned>(p * RPW * SW + st * BSTEP * 64);
+    const unsigned so_s = static_cast<unsigned>((p * RPW * nblk + st * BSTEP) * 2);
+    const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
+    if (lim >= BSTEP) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u)  // the scales first: a chunk's dot then waits for its own weight load only
+        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * BPG * 2, so_s, 0));
+#pragma unroll
+      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * BPG * 64, so_w, 2);
+    } else {  // the row's last, partial step
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const bool ok = gblk + u * BPG < lim;
+        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_s + u * BPG * 2 : kOob, so_s, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const bool ok = gblk + u * BPG < lim;
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w + u * BPG * 64 : kOob, so_w, 2);
+      }
+    }
+  };
+  load(0, 0);
+
+  // ---- stage the column: LDS block b = its 256 q8 values in order at b * XB, then meta[b] = {d_x bits,
+  // -sum(x of the block)} for b < nblk_pad (zeros past nblk, so a chunk past the row's end adds 0 * 0) ----
+  unsigned char* xs = lds;
+  int2* meta = reinterpret_cast<int2*>(lds + nblk_pad * XB);
+  auto stage_one = [&](int i, const f32x4 (&v)[4], const u32x4& xq16, float dxv) {
+    const int r = i & 15;
+    const int b = i >> 4;
+    if constexpr (FUSED) {
+      u32x4 qv;
+      float d;
+      int qsum;
+      const int bsum = q8_K_row16(v, r, qv, d, qsum);  // the quant_q8_K arithmetic (byte-identical planes)
+      *reinterpret_cast<u32x4*>(xs + b * XB + r * 16) = qv;
+      if (r == 0) meta[b] = make_int2(__float_as_int(d), -qsum);
+      if (blockIdx.x == 0 && XQo != nullptr) {  // one workgroup writes the q8_K planes out
+        reinterpret_cast<u32x4*>(XQo)[i] = qv;
+        if (r == 0) XDo[b] = d;
+        if (XBo != nullptr) XBo[i] = static_cast<int16_t>(bsum);
+      }
+    } else {
+      int s16 = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) s16 = __builtin_amdgcn_sdot4(static_cast<int>(xq16[d]), 0x01010101, s16, false);
+      const int qsum = group_sum(s16, 16);
+      *reinterpret_cast<u32x4*>(xs + b * XB + r * 16) = xq16;
+      if (r == 0) meta[b] = make_int2(__float_as_int(dxv), -qsum);
+    }
+  };
+  if (stg) stage_one(tid, xf, x16, xdv);
+  for (int i = tid + nthreads; i < nstage; i += nthreads) {  // columns of more than 16 values per thread
+    f32x4 v[4];
+    u32x4 xq16;
+    float dxv = 0.0f;
+    if constexpr (FUSED) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = src[t];
+    } else {
+      xq16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 16);
+      if ((i & 15) == 0) dxv = XD[i >> 4];
+    }
+    stage_one(i, v, xq16, dxv);
+  }
+  for (int b = nblk + tid; b < nblk_pad; b += nthreads) meta[b] = make_int2(0, 0);
+  // Publish the LDS writes to the workgroup.  Nothing else needs publishing (no other shared or global data is read
+  // back), so the barrier waits for LDS operations only and the weight loads stay in flight; the compiler fences
+  // keep every LDS access on its side of the barrier.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left as they are
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // ---- stream the weights ----
+  const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
+  const int2* ml = meta + gblk;
+  const int qmask = q == 0 ? -1 : 0;  // the block's -sum(x) joins one lane of the quad
+  for (int p = 0; p < passes; ++p) {
+    const int rl = p * RPW + grp;
+    const int row = row_base + rl;
+    const bool rv = rl < wave_rows && row < N;
+    float acc = 0.0f;
+    for (int st = 0; st < nsteps; ++st) {
+      if (p != 0 || st != 0) load(p, st);
+      const int tb = st * BSTEP;
+      const int lim = nblk - tb;  // blocks from the tile's first to the row's end (wave-uniform)
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        if (u * BPG >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
+        const unsigned char* xp = xl + (tb + u * BPG) * XB;
+        u32x4 xv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
+        const int2 mt = ml[tb + u * BPG];
+        const int sl = chunk_dot(w[u], xv, mt.y & qmask);
+        if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
+          const int sb = group_sum(sl, 4);
+          const int b = tb + u * BPG + gblk;
+          if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
+        }
+        acc = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * f16_bits_to_f32(sc[u]), acc);
+      }
+    }
+    const float v = group_sum(acc, LPR);
+    if ((lane & (LPR - 1)) == 0 && rv) Y[row] = v;
+  }
+}
+
+template <int LPR, int NB, bool FUSED>
+hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+  auto kern = tq2_m1_kernel<LPR, NB, FUSED>;
+  GemvSegs segs = c.segs;
+  int64_t groups = (c.n + p.block_n - 1) / p.block_n;
+  if (c.nseg > 1) {
+    groups = 0;
+    for (int i = 0; i < c.nseg; ++i) {
+      segs.first_wg[i] = static_cast<int>(groups);
+      groups += (segs.n[i] + p.block_n - 1) / p.block_n;
+    }
+  }
+  const int nblk = c.k / 256;
+  const size_t lds = tq2_m1_lds_bytes(LPR, NB, c.k);
+  static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
+  if (lds > lds_attr) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    lds_attr = static_cast<unsigned>(lds);
+  }
+  const dim3 grid(static_cast<unsigned>(groups));
+  const dim3 block(static_cast<unsigned>(64 * p.waves));
+  const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
+  const Timing tm = timing_slot(gemv_kind(FMT_TQ2_0));
+  if (tm.on) {
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, c.sw, p.block_n, p.passes,
+                          c.wq, c.ws, xa, c.xd, c.y, c.s, c.xq_out, c.xd_out, c.xb_out, c.nseg, segs);
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, c.sw, p.block_n, p.passes, c.wq, c.ws, xa, c.xd,
+                       c.y, c.s, c.xq_out, c.xd_out, c.xb_out, c.nseg, segs);
+  }
+  return hipGetLastError();
+}
+
+template <int LPR, bool FUSED>
+hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (p.nb) {
+    case 1: return launch_k<LPR, 1, FUSED>(c, p, s);
+    case 2: return launch_k<LPR, 2, FUSED>(c, p, s);
+    case 4: return launch_k<LPR, 4, FUSED>(c, p, s);
+    case 8: return launch_k<LPR, 8, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool FUSED>
+hipError_t by_lpr(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (p.lpr_log2) {
+    case 2: return by_nb<4, FUSED>(c, p, s);
+    case 3: return by_nb<8, FUSED>(c, p, s);
+    case 4: return by_nb<16, FUSED>(c, p, s);
+    case 5: return by_nb<32, FUSED>(c, p, s);
+    case 6: return by_nb<64, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gemv_tq2
+
+size_t tq2_m1_lds_bytes(int lpr, int nb, int k) {
+  const int bstep = (lpr / 4) * nb;
+  const int64_t nblk = k / 256;
+  const int64_t pad = (nblk + bstep - 1) / bstep * bstep;
+  return static_cast<size_t>(pad) * (gemv_tq2::kBlockStride + 8);
+}
+
+bool tq2_m1_eligible(const GemvCall& c, const GemvPlan& p) {
+  return c.fmt == FMT_TQ2_0 && c.m == 1 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 && p.lpr_log2 <= 6 &&
+         (p.nb == 1 || p.nb == 2 || p.nb == 4 || p.nb == 8) && p.waves >= 1 && p.waves <= 16 &&
+         p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
+         tq2_m1_lds_bytes(1 << p.lpr_log2, p.nb, c.k) <= gemv_tq2::kLdsLimit;
+}
+
+hipError_t launch_gemv_tq2_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+  if (p.waves * p.rows_per_wave < p.block_n) return hipErrorInvalidConfiguration;
+  return c.x != nullptr ? gemv_tq2::by_lpr<true>(c, p, stream) : gemv_tq2::by_lpr<false>(c, p, stream);
+}
+
+}  // namespace komp

@@ -130,6 +130,10 @@ hipError_t launch_gemv_more(const GemvCall& c, const GemvPlan& p, hipStream_t st
 hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q4_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q4_k_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+// single-column TQ2_0 in dp4a mode (gemv_tq2.hip): the plans it runs, its LDS bytes and its launch
+bool tq2_m1_eligible(const GemvCall& c, const GemvPlan& p);
+size_t tq2_m1_lds_bytes(int lpr, int nb, int k);
+hipError_t launch_gemv_tq2_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
 hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,

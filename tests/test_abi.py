@@ -146,8 +146,8 @@ def test_auto_plan(fmt, n, k, fused):
         assert blocks_per_step >= nblk or nb == 4  # one K step unless the q4_0 nb cap applies
     elif fmt == 0:  # throughput regime, q4_0: whole rows in one K step, two passes per wave
         assert passes == 2 and nw == 4 and bn == nw * (64 // lanes) * 2 and (blocks_per_step >= nblk or lanes == 64)
-    else:  # throughput regime, tq2_0: nb 4, 8 lanes per row from 128 chunks per row, else 16
-        assert (bn, nb, nw, lanes, passes) == ((64, 4, 8, 8, 1) if 4 * nblk >= 128 else (32, 4, 8, 16, 1))
+    else:  # throughput regime, tq2_0: nb 4, 16 lanes per row, 8 waves
+        assert (bn, nb, nw, lanes, passes) == (32, 4, 8, 16, 1)
 
 
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])
