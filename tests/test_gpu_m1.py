@@ -1,0 +1,97 @@
+"""The single-column dp4a kernels (gemv_tq2.hip: TQ2_0; gemv_q4.hip: Q4_0, IQ4_NL) vs the oracle, over every
+lanes-per-row / chunks-per-lane instantiation they are built for: S exact, Y within 1e-5 of the f64 reference_dot, Y
+independent of whether S is stored, and the fused launch bit-identical to quantizer + GEMV.  Q4_0 and IQ4_NL keep the
+general kernel's accumulation order, so their Y is also bit-identical to the emulated-dp4a mode (which runs the general
+kernel).  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
+wave; padded weight rows and multi-matrix launches too.  Everything goes through the C ABI."""
+
+import numpy as np
+import pytest
+import torch
+
+from comp_amd import host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+# knob sets (block_n, num_warps) -> lanes per row 64, 32, 16, 8, 4 and 4 with two passes per wave
+LAYOUTS = [(8, 8), (16, 8), (32, 8), (64, 8), (128, 8), (128, 4)]
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+FORMATS = ["tq2_0", "q4_0", "iq4_nl"]
+K_TAIL = {"tq2_0": 2816, "q4_0": 2400, "iq4_nl": 2400}  # 11 / 75 blocks: a partial last K step for every layout, nb
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("nb", [1, 2, 4, 8])
+@pytest.mark.parametrize("extreme", [False, True])
+def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme):
+    bn, nw = layout
+    n, k = 300, K_TAIL[fmt]
+    W, x = O.problem(fmt, n, k, 1, 70 + nb + bn, extreme)
+    wq, ws = host.split(fmt, W, n, k)
+    wq_d, ws_d, x_d = dev(wq), dev(ws), dev(x)
+    print(f"{fmt} n={n} k={k} block_n={bn} nb={nb} num_warps={nw} extreme={extreme}", flush=True)
+    y_s, s = host.gemv_f32(fmt, wq_d, ws_d, x_d, n, k, bn, nb, 2, nw, store_s=True)
+    y = host.gemv_f32(fmt, wq_d, ws_d, x_d, n, k, bn, nb, 2, nw)[0]
+    xq, xd, *_ = host.quantize(fmt, x_d)
+    y2, s2 = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 2, nw, store_s=True)
+    y_emu, s_emu = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 1, nw, store_s=True)  # the general kernel
+    torch.cuda.synchronize()
+    rq, rd, _ = O.quantize(fmt, x)
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs) and torch.equal(s, s2) and torch.equal(s, s_emu)
+    assert torch.equal(y.view(torch.int32), y_s.view(torch.int32))
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    if fmt != "tq2_0":
+        assert torch.equal(y.view(torch.int32), y_emu.view(torch.int32))
+    assert O.relerr(y.cpu().numpy(), r) <= TOL
+
+
+SHAPES = {"tq2_0": [(6912, 2560), (2560, 6912), (5, 256), (16400, 8192), (257, 512)],
+          "q4_0": [(4096, 4096), (14336, 4096), (4096, 14336), (5, 32), (16400, 4192)]}
+SHAPES["iq4_nl"] = SHAPES["q4_0"]
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("shape", range(5))
+@pytest.mark.parametrize("fused", [False, True])
+def test_auto_plans_padded_rows(fmt, shape, fused):
+    n, k = SHAPES[fmt][shape]
+    W, x = O.problem(fmt, n, k, 1, 90 + shape)
+    wq, ws = host.split(fmt, W, n, k)
+    wq_pad = dev(np.pad(wq, ((0, 0), (0, 64))))[:, : wq.shape[1]]  # a row stride 64 bytes past the row
+    if fused:
+        y, s = host.gemv_f32(fmt, wq_pad, dev(ws), dev(x), n, k, store_s=True)
+    else:
+        xq, xd, *_ = host.quantize(fmt, dev(x))
+        y, s = host.gemv(fmt, wq_pad, dev(ws), xq, xd, n, k, store_s=True)
+    torch.cuda.synchronize()
+    rq, rd, _ = O.quantize(fmt, x)
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
+    assert O.relerr(y.cpu().numpy(), r) <= TOL
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_multi_matrix_launch(fmt):
+    k = 2560
+    ns = (6912, 300, 6912)
+    rng = np.random.default_rng(91)
+    x = O.activations(rng, k, 1, block=O.ACT_BLOCK[O.FORMATS[fmt]["act"]])
+    rq, rd, _ = O.quantize(fmt, x)
+    mats, refs = [], []
+    for n in ns:
+        wq, ws = host.split(fmt, O.weights(fmt, rng, n, k), n, k)
+        mats.append((dev(wq), dev(ws), n))
+        refs.append(O.gemv(fmt, wq, ws, rq, rd, n, k)[0])
+    ys = host.gemv_multi(fmt, mats, k, x=dev(x))
+    torch.cuda.synchronize()
+    for y, r in zip(ys, refs):
+        assert O.relerr(y.cpu().numpy(), r) <= TOL
