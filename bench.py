@@ -41,7 +41,7 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
 # profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
-TRAFFIC_FUSED_BITNET_M1 = 4881168
+TRAFFIC_FUSED_BITNET_M1 = 4862225
 
 
 # (values per weight block, weight bytes per block, values per activation block) of each weight format
@@ -183,6 +183,26 @@ def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
     return e0.elapsed_time(e1), wall
 
 
+def read_floor_us(torch, host, nbytes):
+    """Graph-replay us per call of the library's streaming-read probe (komp_stream_read: the bytes read once with
+    non-temporal 16-byte loads, nothing computed) over cold copies of nbytes, the same harness as the GEMVs: the time
+    of moving that many bytes alone, which a GEMV over them can at best reach."""
+    nb = -(-nbytes // 16) * 16
+    ncopy = max(2, math.ceil((COLD_BYTES // 2) / nb))
+    bufs = [torch.zeros(nb, dtype=torch.uint8, device="cuda") for _ in range(ncopy)]
+    out = torch.empty(host.stream_read_words(nb), dtype=torch.int32, device="cuda")
+
+    def call(i):
+        host.stream_read_into(bufs[i % ncopy], nb, out)
+
+    per_graph = ncopy * math.ceil(64 / ncopy)
+    reps = 4 * per_graph
+    ms, _ = timed_steps(torch, call, ncopy, reps, per_graph)
+    del bufs
+    torch.cuda.empty_cache()
+    return ms * 1e3 / reps
+
+
 def dispatch_times(abi, torch, step, count):
     """Run `count` eager steps with per-dispatch timing; -> {kind: (total_ms, dispatches)}."""
     torch.cuda.synchronize()
@@ -267,7 +287,8 @@ def headline(torch, host, abi, args):
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": TRAFFIC_FUSED_BITNET_M1 if default_cfg else None,
                 "kernel": "tq2_0_gemv (fused quantize)",
-                "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b)}  # fmt: skip
+                "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b),
+                "read_floor_us": round(read_floor_us(torch, host, int(launch_b)), 3)}  # fmt: skip
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
                           "activations quantized to q8_K inside each launch",  # fmt: skip
               "shapes_nk": [list(s) for s in shapes], "m": m, "mode": {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}[args.mode],
@@ -351,14 +372,16 @@ def detail(torch, host, abi, args):
         d_us = disp[kind][0] * 1e3 / disp[kind][1]
         b = gemv_bytes(fmt, n, k, m)
         us = ms * 1e3 / reps
+        del copies, call
+        torch.cuda.empty_cache()
+        floor = read_floor_us(torch, host, b)
         plan = host.auto_plan(fmt, m, n, k)
         rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "plan": [plan[key] for key in ("block_n", "nb", "waves",
                                                                                         "lanes_per_row", "passes")],
                      "bytes": b, "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                      "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "dispatch_us": round(d_us, 3),
-                     "gbs_dispatch": round(b / d_us / 1e3, 1), "copies": nc})  # fmt: skip
-        del copies
-        torch.cuda.empty_cache()
+                     "gbs_dispatch": round(b / d_us / 1e3, 1), "read_floor_us": round(floor, 3),
+                     "of_read_floor": round(floor / us, 3), "copies": nc})  # fmt: skip
     return rows
 
 

@@ -65,6 +65,7 @@ SIGNATURES = {
     "komp_q4_0_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "komp_tq2_0_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
+    "komp_stream_read": (_INT, [_P, _I64, _P, _P]),
     "komp_q4_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_timing_begin": (_INT, [_I64]),

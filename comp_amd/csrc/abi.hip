@@ -655,6 +655,15 @@ int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_
   return hip_status(launch_dp4a_probe(A, B, C, OUT, n, mode, static_cast<hipStream_t>(stream)), "komp_dp4a_probe");
 }
 
+int komp_stream_read(const void* SRC, int64_t bytes, uint32_t* OUT, void* stream) {
+  if (bytes < 0 || bytes % 16) return fail(KOMP_EINVAL, "komp_stream_read: bytes=%lld must be a multiple of 16", static_cast<long long>(bytes));
+  if (bytes / 16 > (int64_t{1} << 42)) return fail(KOMP_EINVAL, "komp_stream_read: bytes too large");
+  if (bytes == 0) return KOMP_OK;
+  if (!SRC || !OUT) return fail(KOMP_EINVAL, "komp_stream_read: NULL pointer");
+  if (!aligned(SRC, 16) || !aligned(OUT, 4)) return fail(KOMP_EINVAL, "komp_stream_read: SRC must be 16-byte and OUT 4-byte aligned");
+  return hip_status(launch_stream_read(SRC, bytes, OUT, static_cast<hipStream_t>(stream)), "komp_stream_read");
+}
+
 int komp_q4_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t R, void* stream) {
   if (R < 0) return fail(KOMP_EINVAL, "komp_q4_0_decode: negative R");
   if (R == 0) return KOMP_OK;

@@ -144,6 +144,7 @@ hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int
                         hipStream_t stream);
 hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
+hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream);
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,
                              hipStream_t stream);
 hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream);

@@ -99,6 +99,26 @@ __global__ void tq2_0_decode_kernel(const uint8_t* __restrict__ WQ, int32_t* __r
   }
 }
 
+// Streaming-read probe: every 16 bytes of SRC read once with non-temporal 16-byte loads (4 per thread, 512 threads
+// per workgroup, all in flight together), XOR-folded per wave into OUT[wave]: the time of moving the bytes alone, the
+// floor a GEMV over as many bytes is measured against.
+__global__ void __launch_bounds__(512) stream_read_kernel(const u32x4* __restrict__ SRC, int64_t n16,
+                                                          uint32_t* __restrict__ OUT) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 2048 + threadIdx.x;
+  u32x4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t j = base + u * 512;
+    v[u] = j < n16 ? __builtin_nontemporal_load(SRC + j) : u32x4{0u, 0u, 0u, 0u};
+  }
+  unsigned acc = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc ^= static_cast<unsigned>(__shfl_xor(static_cast<int>(acc), o, 64));
+  if ((threadIdx.x & 63) == 0) OUT[static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6)] = acc;
+}
+
 template <typename F, typename... Args>
 hipError_t launch(int kind, F kern, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
   const Timing tm = timing_slot(kind);
@@ -127,6 +147,12 @@ hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb,
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,
                              hipStream_t stream) {
   return launch(KIND_PROBE, dp4a_probe_kernel, dim3(blocks_for(n, 256)), dim3(256), stream, a, b, c, out, n, mode);
+}
+
+hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream) {
+  const int64_t n16 = bytes / 16;
+  return launch(KIND_PROBE, stream_read_kernel, dim3(blocks_for(n16, 2048)), dim3(512), stream,
+                static_cast<const u32x4*>(src), n16, out);
 }
 
 hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream) {

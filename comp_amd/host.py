@@ -523,6 +523,32 @@ def dp4a_probe(a, b, c, mode=2):
     return out
 
 
+def stream_read_words(nbytes):
+    """Words komp_stream_read writes for nbytes: one per wave, a wave reading 64 lanes x 4 x 16 = 4096 bytes."""
+    return 8 * -(-nbytes // 32768)
+
+
+def stream_read_into(src, nbytes, out):
+    """Read the first nbytes of the contiguous device tensor src once with the streaming-read probe (one launch) and
+    write each wave's XOR of its dwords to out (uint32 viewed as int32, stream_read_words(nbytes) words): the cost of
+    moving the bytes alone, which bench.py sets beside each GEMV over as many bytes.  Beyond the reference."""
+    if not src.is_cuda or not src.is_contiguous() or src.numel() * src.element_size() < nbytes:
+        raise _abi.KompArgumentError("src must be a contiguous device tensor of at least nbytes bytes")
+    _need(out, "out", torch.int32, 1)
+    if out.numel() < stream_read_words(nbytes):
+        raise _abi.KompArgumentError(f"out needs {stream_read_words(nbytes)} words")
+    with torch.cuda.device(src.device):
+        _abi.call("komp_stream_read", src.data_ptr(), nbytes, out.data_ptr(), _stream(src))
+
+
+def stream_read(src):
+    """stream_read_into over all of src (its byte count a multiple of 16); returns the per-wave XOR words."""
+    nbytes = src.numel() * src.element_size()
+    out = torch.empty(stream_read_words(nbytes), dtype=torch.int32, device=src.device)
+    stream_read_into(src, nbytes, out)
+    return out
+
+
 def q4_0_decode(wq):
     """[R][16] q4_0 quant bytes -> [R][32] int32 values (kernels.q4_0_decode, src/komp/kernels.py:152-157)."""
     _need(wq, "wq", torch.uint8, 2)

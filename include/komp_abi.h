@@ -203,6 +203,12 @@ int komp_tq2_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int6
 int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,
                     void* stream);
 
+/* Reads the BYTES of SRC once (non-temporal 16-byte loads, 2048 per 512-thread workgroup) and writes the XOR of each
+ * wave's 512 dwords to OUT[wave], 8 * ceil(BYTES / 32768) words: the cost of moving the bytes alone, the floor a GEMV
+ * over as many bytes is compared with.  BYTES % 16 == 0, SRC 16-byte and OUT 4-byte aligned.
+ * No reference counterpart: a measurement probe (bench.py reports every GEMV shape against it). */
+int komp_stream_read(const void* SRC, int64_t bytes, uint32_t* OUT, void* stream);
+
 /* [R][16] Q4_0 quant bytes -> [R][32] int32 values.  Replaces: kernels.q4_0_decode (src/komp/kernels.py:152-157). */
 int komp_q4_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t R, void* stream);
 

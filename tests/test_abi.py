@@ -79,6 +79,7 @@ def test_empty_shapes_are_no_ops():
     assert lib.komp_quant_q8_0(None, None, None, 0, 64, 4, None) == 0
     assert lib.komp_quant_q8_K(None, None, None, None, 3, 0, None) == 0
     assert lib.komp_dp4a_probe(None, None, None, None, 0, 2, None) == 0
+    assert lib.komp_stream_read(None, 0, None, None) == 0
 
 
 def _multi(count=2, n=(4, 4), K=64, sw=(32, 32), wq_ptr=16, x=False, xq=True, mode=2, arrays=True):
@@ -117,6 +118,9 @@ def test_quantizers_reject_bad_arguments():
     assert lib.komp_quant_q8_K(p, p, p, None, 1, 300, None) == _abi.KOMP_EINVAL
     assert lib.komp_quant_q8_K(ctypes.c_void_p(8), p, p, None, 1, 256, None) == _abi.KOMP_EINVAL
     assert lib.komp_dp4a_probe(p, p, p, p, 4, 0, None) == _abi.KOMP_EINVAL
+    assert lib.komp_stream_read(p, 24, p, None) == _abi.KOMP_EINVAL and "multiple of 16" in _abi.last_error()
+    assert lib.komp_stream_read(ctypes.c_void_p(8), 32, p, None) == _abi.KOMP_EINVAL
+    assert lib.komp_stream_read(None, 32, p, None) == _abi.KOMP_EINVAL
 
 
 def test_python_errors_carry_the_message():

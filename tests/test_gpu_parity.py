@@ -281,3 +281,21 @@ def test_q4_k_extreme_scales_every_mode():
         y, s, r, rs, _, _ = run_gemv("q4_k", 45, 2304, 3, 43, True, 16, 4, mode, 2)
         assert np.array_equal(s.astype(np.int64), rs)
         assert O.relerr(y, r) <= TOL
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096, 32768 + 48, 4599808, 33030144 + 16])
+def test_stream_read_probe_reads_every_byte(nbytes):
+    # the streaming-read probe bench.py measures GEMVs against: every dword is folded into exactly one wave's word
+    rng = np.random.default_rng(nbytes)
+    data = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint32)
+    out = host.stream_read(dev(data.view(np.int32)))
+    torch.cuda.synchronize()
+    words = out.cpu().numpy().view(np.uint32)
+    assert words.size == host.stream_read_words(nbytes)
+    assert np.bitwise_xor.reduce(words) == np.bitwise_xor.reduce(data)
+    # workgroup g, wave w, lane l reads 16-byte pieces 2048 g + 512 u + 64 w + l (u < 4)
+    grid = words.size // 8
+    pieces = np.zeros(grid * 2048 * 4, dtype=np.uint32)
+    pieces[: data.size] = data
+    per_wave = np.bitwise_xor.reduce(pieces.reshape(grid, 4, 8, 64 * 4), axis=(1, 3)).reshape(-1)
+    assert np.array_equal(words, per_wave)
