@@ -93,8 +93,15 @@ VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64, "q8_0": 16, "iq4_nl": 32, "q4_k": 64
 FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kernels' format template argument
 
 
-def _gemv_kernel(fmt, mode, nb, m=1):
-    """The gemv_kernel instantiation a launch of this config runs: <format, mode, columns per launch, nb, fused>."""
+def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None):
+    """The kernel instantiation a launch of this config runs: one column in dp4a mode of q4_0 / iq4_nl / tq2_0 with
+    nb <= 8 runs the single-column kernel <(format,) lanes per row, nb, fused>, where the knobs give lanes per row =
+    64 / min(block_n / num_warps, 16); everything else the general gemv_kernel <format, mode, columns, nb, fused>."""
+    if mode == 2 and m == 1 and nb in (1, 2, 4, 8) and block_n and num_warps and fmt in ("q4_0", "iq4_nl", "tq2_0"):
+        lanes = 64 // min(block_n // num_warps, 16)
+        if fmt == "tq2_0":
+            return f"gemv_tq2::tq2_m1_kernel<{lanes}, {nb}, false>"
+        return f"gemv_q4::q4_m1_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, false>"
     return f"gemv_impl::gemv_kernel<{FMT_NUM[fmt]}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
 
 
@@ -130,7 +137,8 @@ def cmd_gen(args):
     fmt = c["weights"]
     quant = "quant_q8_0" if fmt == "q4_0" else "quant_q8_K"
     try:
-        r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1)), VALUES_PER_LOAD[fmt], keep=out is not None)
+        r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1), c.get("block_n"), c.get("num_warps")),
+                        VALUES_PER_LOAD[fmt], keep=out is not None)  # fmt: skip
         q = isa.summary(f"{quant}_kernel", 1, keep=out is not None)
     except (OSError, RuntimeError, KeyError) as e:
         print(f"komp gen: {e}", file=sys.stderr)
@@ -177,7 +185,7 @@ def cmd_mix(args):
         for fmt in ("q4_0", "tq2_0"):
             for bn, nb, nw in MIX_KOMP[fmt]:
                 for mode in (0, 2):
-                    r = isa.summary(_gemv_kernel(fmt, mode, nb), VALUES_PER_LOAD[fmt])
+                    r = isa.summary(_gemv_kernel(fmt, mode, nb, 1, bn, nw), VALUES_PER_LOAD[fmt])
                     spill = r["vgpr_spill"] + r["sgpr_spill"]
                     fails += bool(spill or r["approx"])
                     name = (f"KOMP {fmt} {'dp4a ' if mode else 'bytes'} {bn}/{nb}/{nw}w v{r['vgpr']}"
@@ -186,7 +194,7 @@ def cmd_mix(args):
             print(f"KURN-CUDA {fmt}: not available (NVIDIA target; this build holds gfx950 code only)")
         for fmt, cfgs in MIX_MORE.items():
             for bn, nb, nw in cfgs:
-                r = isa.summary(_gemv_kernel(fmt, 2, nb), VALUES_PER_LOAD[fmt])
+                r = isa.summary(_gemv_kernel(fmt, 2, nb, 1, bn, nw), VALUES_PER_LOAD[fmt])
                 spill = r["vgpr_spill"] + r["sgpr_spill"]
                 fails += bool(spill or r["approx"])
                 print(_mix_line(r, f"KOMP {fmt} dp4a  {bn}/{nb}/{nw}w v{r['vgpr']}" + (" SPILL" if spill else "")))
