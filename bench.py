@@ -375,9 +375,13 @@ def detail(torch, host, abi, args):
         del copies, call
         torch.cuda.empty_cache()
         floor = read_floor_us(torch, host, b)
-        plan = host.auto_plan(fmt, m, n, k)
-        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "plan": [plan[key] for key in ("block_n", "nb", "waves",
-                                                                                        "lanes_per_row", "passes")],
+        if host.uses_gemm(fmt, m, n, k):  # block_n=None routes this many columns to the matrix-core GEMM
+            path, gp = "gemm", host.gemm_plan(fmt, m, n, k)
+            plan = [gp[key] for key in ("rows", "cols", "waves")]
+        else:
+            path, ap = "gemv", host.auto_plan(fmt, m, n, k)
+            plan = [ap[key] for key in ("block_n", "nb", "waves", "lanes_per_row", "passes")]
+        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "path": path, "plan": plan,
                      "bytes": b, "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                      "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "dispatch_us": round(d_us, 3),
                      "gbs_dispatch": round(b / d_us / 1e3, 1), "read_floor_us": round(floor, 3),
