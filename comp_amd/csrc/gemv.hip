@@ -13,7 +13,7 @@ hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream)
   if (c.x != nullptr) return launch_gemv_fused(c, p, stream);
   switch (c.fmt) {
     case FMT_Q4_0:
-      if (q4_m1_eligible(c, p)) return launch_gemv_q4_m1(c, p, stream);
+      if (q4_lean_eligible(c, p)) return launch_gemv_q4_lean(c, p, stream);
       return gemv_impl::by_mode<FMT_Q4_0, false>(c, p, stream);
     case FMT_TQ2_0:
       if (tq2_m1_eligible(c, p)) return launch_gemv_tq2_m1(c, p, stream);

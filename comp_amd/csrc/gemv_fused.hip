@@ -6,7 +6,7 @@ namespace komp {
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   switch (c.fmt) {
     case FMT_Q4_0:
-      if (q4_m1_eligible(c, p)) return launch_gemv_q4_m1(c, p, stream);
+      if (q4_lean_eligible(c, p)) return launch_gemv_q4_lean(c, p, stream);
       return gemv_impl::by_mode<FMT_Q4_0, true>(c, p, stream);
     case FMT_TQ2_0:
       if (tq2_m1_eligible(c, p)) return launch_gemv_tq2_m1(c, p, stream);

@@ -7,7 +7,7 @@ namespace komp {
 hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, true>(c, p, stream);
   if (c.fmt == FMT_IQ4_NL)
-    return q4_m1_eligible(c, p) ? launch_gemv_q4_m1(c, p, stream) : gemv_impl::by_mode<FMT_IQ4_NL, true>(c, p, stream);
+    return q4_lean_eligible(c, p) ? launch_gemv_q4_lean(c, p, stream) : gemv_impl::by_mode<FMT_IQ4_NL, true>(c, p, stream);
   return c.fmt == FMT_Q4_K ? launch_gemv_q4_k_fused(c, p, stream) : hipErrorInvalidValue;
 }
 

@@ -1,13 +1,13 @@
-// Single-column Q4_0 and IQ4_NL decode GEMVs in dp4a mode (16-byte blocks of 32 nibbles, q8_0 activations), unfused
-// and fused with the q8_0 quantizer.  Same plans, lanes, accumulation order, results and S as the general kernel in
-// gemv_kernel.h (kernels.py:48-94 semantics: lane g of a row group takes blocks st * G * nb + u * G + g and adds
-// s * d_w * d_x per block, the row group's lanes are added at the end), with what the general kernel keeps at run
-// time made compile-time (G lanes per row, nb blocks per lane and K step):
+// Q4_0 and IQ4_NL decode GEMVs of 1-3 activation columns in dp4a mode (16-byte blocks of 32 nibbles, q8_0
+// activations), unfused and fused with the q8_0 quantizer.  Same plans, lanes, accumulation order, results and S as the
+// general kernel in gemv_kernel.h (kernels.py:48-94 semantics: lane g of a row group takes blocks st * G * nb + u * G +
+// g and adds s * d_w * d_x per block and column, the row group's lanes are added at the end), with what the general
+// kernel keeps at run time made compile-time (G lanes per row, nb blocks per lane and K step, MC columns):
 //   * weight and scale loads are buffer loads from loop-invariant per-lane offsets, the step and block offsets being
 //     a scalar and an immediate; a block past the row's end, and every row past the matrix, reads zeros without
 //     touching memory, so no load sits behind a branch and each block's dot waits for its own load only;
-//   * the staged column's low halves, high halves and block metadata are three LDS arrays indexed by block, so a
-//     block's reads are per-lane bases plus immediates;
+//   * the staged columns' low halves, high halves and block metadata are three LDS arrays indexed by column and
+//     block, so a block's reads are per-lane bases plus immediates;
 //   * the staging's activation loads are issued before the weight loads, and the barrier that publishes the staged
 //     column waits for LDS writes only, so the weights stay in flight through the staging.
 #include "gemv_kernel.h"
@@ -22,11 +22,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);  // raw, 32-bit data
 }
 
-// G lanes per row group, NB blocks per lane per K step.  The arguments every first load needs fill the 14
-// preloaded argument dwords.
-template <int FMT, int G, int NB, bool FUSED>
+// G lanes per row group, NB blocks per lane per K step, MC activation columns.  The arguments every first load needs
+// fill the 14 preloaded argument dwords.
+template <int FMT, int G, int NB, int MC, bool FUSED>
 __global__ void __launch_bounds__(1024)
-q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
+q4_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
              const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
              float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
              int nseg, const GemvSegs segs) {
@@ -69,8 +69,9 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + g) * 2);
 
   // ---- the staging's first loads, before the weights: fused, 8 lanes per block with 4 f32 values each; unfused,
-  // one lane per block with its 32 q8 bytes and d_x ----
-  const int nstage = FUSED ? nblk * 8 : nblk;
+  // one lane per block with its 32 q8 bytes and d_x.  Blocks of all columns in order (X [MC][K] and XQ [MC][K] are
+  // dense, so block i of the flattened columns starts at 32 i; XD [MC][nblk] likewise) ----
+  const int nstage = FUSED ? MC * nblk * 8 : MC * nblk;
   const bool stg = tid < nstage;
   f32x4 xf;
   u32x4 xa, xb;
@@ -114,14 +115,21 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
   };
   load(0, 0);
 
-  // ---- stage the column: xl[b] = activations 0..15 of block b, xh[b] = 16..31, meta[b] = {d_x bits, -8 * sum(x)
-  // (Q4_0; IQ4_NL 0)} for b < nblk_pad (zeros past nblk, so a block past the row's end adds 0) ----
+  // ---- stage the columns: xl[m][b] = activations 0..15 of block b of column m, xh[m][b] = 16..31, meta[m][b] =
+  // {d_x bits, -8 * sum(x) (Q4_0; IQ4_NL 0)} for b < nblk_pad (zeros past nblk, so a block past the row's end adds 0);
+  // column m at m * nblk_pad ----
   u32x4* xl = reinterpret_cast<u32x4*>(lds);
-  u32x4* xh = xl + nblk_pad;
-  int2* meta = reinterpret_cast<int2*>(xh + nblk_pad);
+  u32x4* xh = xl + MC * nblk_pad;
+  int2* meta = reinterpret_cast<int2*>(xh + MC * nblk_pad);
+  auto slot = [&](int i) {  // flattened block i of the columns -> its LDS slot
+    if constexpr (MC == 1) return i;
+    const int m = i / nblk;
+    return i + m * (nblk_pad - nblk);
+  };
   auto stage_fused = [&](int i, const f32x4& v) {
     const int e = i & 7;
-    const int b = i >> 3;
+    const int bi = i >> 3;
+    const int b = slot(bi);
     float d;
     int qsum;
     const unsigned packed = q8_0_group8(v, d, qsum);  // the quant_q8_0 arithmetic (byte-identical planes)
@@ -129,10 +137,11 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
     if (e == 0) meta[b] = make_int2(__float_as_int(d), FMT == FMT_Q4_0 ? -8 * qsum : 0);
     if (blockIdx.x == 0 && XQo != nullptr) {  // one workgroup writes the q8_0 planes out
       reinterpret_cast<unsigned*>(XQo)[i] = packed;
-      if (e == 0) XDo[b] = d;
+      if (e == 0) XDo[bi] = d;
     }
   };
-  auto stage_q8 = [&](int b, const u32x4& a, const u32x4& c, float dxv) {
+  auto stage_q8 = [&](int bi, const u32x4& a, const u32x4& c, float dxv) {
+    const int b = slot(bi);
     xl[b] = a;
     xh[b] = c;
     int sum = 0;
@@ -157,7 +166,10 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
       stage_q8(i, src[0], src[1], XD[i]);
     }
   }
-  for (int b = nblk + tid; b < nblk_pad; b += nthreads) meta[b] = make_int2(0, 0);
+  for (int i = tid; i < MC * (nblk_pad - nblk); i += nthreads) {
+    const int m = i / (nblk_pad - nblk);
+    meta[m * nblk_pad + nblk + (i - m * (nblk_pad - nblk))] = make_int2(0, 0);
+  }
   // Publish the LDS writes to the workgroup.  Nothing else needs publishing (no other shared or global data is read
   // back), so the barrier waits for LDS operations only and the weight loads stay in flight; the compiler fences
   // keep every LDS access on its side of the barrier.
@@ -174,7 +186,9 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
-    float acc = 0.0f;
+    float acc[MC];
+#pragma unroll
+    for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
     for (int st = 0; st < nsteps; ++st) {
       if (p != 0 || st != 0) load(p, st);
       const int tb = st * BSTEP;
@@ -183,21 +197,29 @@ q4_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const u
       for (int u = 0; u < NB; ++u) {
         if (u * G >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
         const int bo = tb + u * G;
-        const int2 mt = mg[bo];
-        const int s = FMT == FMT_Q4_0 ? gemv_impl::q4_0_block_dot<MODE_DP4A>(w[u], xlg[bo], xhg[bo], mt.y)
-                                      : gemv_impl::iq4_nl_block_dot<MODE_DP4A>(w[u], xlg[bo], xhg[bo]);
-        if (S != nullptr && rv && bo + g < nblk) S[static_cast<int64_t>(row) * nblk + bo + g] = s;
-        acc += static_cast<float>(s) * f16_bits_to_f32(sc[u]) * __int_as_float(mt.x);  // kernels.py:93 order
+        const float dw = f16_bits_to_f32(sc[u]);
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+          const int bm = m * nblk_pad + bo;
+          const int2 mt = mg[bm];
+          const int s = FMT == FMT_Q4_0 ? gemv_impl::q4_0_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm], mt.y)
+                                        : gemv_impl::iq4_nl_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm]);
+          if (S != nullptr && rv && bo + g < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + bo + g] = s;
+          acc[m] += static_cast<float>(s) * dw * __int_as_float(mt.x);  // kernels.py:93 order
+        }
       }
     }
-    const float v = group_sum(acc, G);
-    if (g == 0 && rv) Y[row] = v;
+#pragma unroll
+    for (int m = 0; m < MC; ++m) {
+      const float v = group_sum(acc[m], G);
+      if (g == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+    }
   }
 }
 
-template <int FMT, int G, int NB, bool FUSED>
+template <int FMT, int G, int NB, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  auto kern = q4_m1_kernel<FMT, G, NB, FUSED>;
+  auto kern = q4_lean_kernel<FMT, G, NB, MC, FUSED>;
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -208,7 +230,7 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     }
   }
   const int nblk = c.k / 32;
-  const size_t lds = q4_m1_lds_bytes(G, NB, c.k);
+  const size_t lds = q4_lean_lds_bytes(G, NB, MC, c.k);
   static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
   if (lds > lds_attr) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -230,13 +252,24 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int FMT, int G, bool FUSED>
+template <int FMT, int G, int MC, bool FUSED>
 hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (p.nb) {
-    case 1: return launch_k<FMT, G, 1, FUSED>(c, p, s);
-    case 2: return launch_k<FMT, G, 2, FUSED>(c, p, s);
-    case 4: return launch_k<FMT, G, 4, FUSED>(c, p, s);
-    case 8: return launch_k<FMT, G, 8, FUSED>(c, p, s);
+    case 1: return launch_k<FMT, G, 1, MC, FUSED>(c, p, s);
+    case 2: return launch_k<FMT, G, 2, MC, FUSED>(c, p, s);
+    case 4: return launch_k<FMT, G, 4, MC, FUSED>(c, p, s);
+    case 8:
+      if constexpr (MC == 1) return launch_k<FMT, G, 8, MC, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int FMT, int G, bool FUSED>
+hipError_t by_mc(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (c.m) {
+    case 1: return by_nb<FMT, G, 1, FUSED>(c, p, s);
+    case 2: return by_nb<FMT, G, 2, FUSED>(c, p, s);
+    case 3: return by_nb<FMT, G, 3, FUSED>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -244,32 +277,35 @@ hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
 template <int FMT, bool FUSED>
 hipError_t by_g(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (p.lpr_log2) {
-    case 2: return by_nb<FMT, 4, FUSED>(c, p, s);
-    case 3: return by_nb<FMT, 8, FUSED>(c, p, s);
-    case 4: return by_nb<FMT, 16, FUSED>(c, p, s);
-    case 5: return by_nb<FMT, 32, FUSED>(c, p, s);
-    case 6: return by_nb<FMT, 64, FUSED>(c, p, s);
+    case 2: return by_mc<FMT, 4, FUSED>(c, p, s);
+    case 3: return by_mc<FMT, 8, FUSED>(c, p, s);
+    case 4: return by_mc<FMT, 16, FUSED>(c, p, s);
+    case 5: return by_mc<FMT, 32, FUSED>(c, p, s);
+    case 6: return by_mc<FMT, 64, FUSED>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace gemv_q4
 
-size_t q4_m1_lds_bytes(int g, int nb, int k) {
+size_t q4_lean_lds_bytes(int g, int nb, int mc, int k) {
   const int bstep = g * nb;
   const int64_t nblk = k / 32;
   const int64_t pad = (nblk + bstep - 1) / bstep * bstep;
-  return static_cast<size_t>(pad) * (16 + 16 + 8);
+  return static_cast<size_t>(mc) * pad * (16 + 16 + 8);
 }
 
-bool q4_m1_eligible(const GemvCall& c, const GemvPlan& p) {
-  return (c.fmt == FMT_Q4_0 || c.fmt == FMT_IQ4_NL) && c.m == 1 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 &&
-         p.lpr_log2 <= 6 && (p.nb == 1 || p.nb == 2 || p.nb == 4 || p.nb == 8) && p.waves >= 1 && p.waves <= 16 &&
+bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p) {
+  // one column with nb up to 8, two or three columns with nb up to 4 (the instantiations); 1024 threads hold at most
+  // 128 VGPRs, which three columns at nb 4 stay within
+  const bool nb_ok = p.nb == 1 || p.nb == 2 || p.nb == 4 || (p.nb == 8 && c.m == 1);
+  return (c.fmt == FMT_Q4_0 || c.fmt == FMT_IQ4_NL) && c.m >= 1 && c.m <= 3 && c.mode == MODE_DP4A &&
+         p.lpr_log2 >= 2 && p.lpr_log2 <= 6 && nb_ok && p.waves >= 1 && p.waves <= 16 &&
          p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
-         q4_m1_lds_bytes(1 << p.lpr_log2, p.nb, c.k) <= gemv_impl::kLdsLimit;
+         q4_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k) <= gemv_impl::kLdsLimit;
 }
 
-hipError_t launch_gemv_q4_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+hipError_t launch_gemv_q4_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (p.waves * p.rows_per_wave < p.block_n) return hipErrorInvalidConfiguration;
   const bool fused = c.x != nullptr;
   if (c.fmt == FMT_Q4_0)

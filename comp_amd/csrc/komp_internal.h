@@ -134,10 +134,10 @@ hipError_t launch_gemv_q4_k_fused(const GemvCall& c, const GemvPlan& p, hipStrea
 bool tq2_m1_eligible(const GemvCall& c, const GemvPlan& p);
 size_t tq2_m1_lds_bytes(int lpr, int nb, int k);
 hipError_t launch_gemv_tq2_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
-// single-column Q4_0 and IQ4_NL in dp4a mode (gemv_q4.hip)
-bool q4_m1_eligible(const GemvCall& c, const GemvPlan& p);
-size_t q4_m1_lds_bytes(int g, int nb, int k);
-hipError_t launch_gemv_q4_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+// Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip)
+bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p);
+size_t q4_lean_lds_bytes(int g, int nb, int mc, int k);
+hipError_t launch_gemv_q4_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
 hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,

@@ -1,8 +1,8 @@
-"""The single-column dp4a kernels (gemv_tq2.hip: TQ2_0; gemv_q4.hip: Q4_0, IQ4_NL) vs the oracle, over every
-lanes-per-row / chunks-per-lane instantiation they are built for: S exact, Y within 1e-5 of the f64 reference_dot, Y
-independent of whether S is stored, and the fused launch bit-identical to quantizer + GEMV.  Q4_0 and IQ4_NL keep the
-general kernel's accumulation order, so their Y is also bit-identical to the emulated-dp4a mode (which runs the general
-kernel).  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
+"""The lean dp4a kernels (gemv_tq2.hip: one TQ2_0 column; gemv_q4.hip: 1-3 Q4_0 / IQ4_NL columns) vs the oracle,
+over every lanes-per-row / chunks-per-lane / column-count instantiation they are built for: S exact, Y within 1e-5 of
+the f64 reference_dot, Y independent of whether S is stored, and the fused launch bit-identical to quantizer + GEMV.
+Q4_0 and IQ4_NL keep the general kernel's accumulation order, so their Y is also bit-identical to the emulated-dp4a
+mode (which runs the general kernel); so are TQ2_0's 2-3 columns, which run the general kernel in both modes.  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
 wave; padded weight rows and multi-matrix launches too.  Everything goes through the C ABI."""
 
 import numpy as np
@@ -31,13 +31,14 @@ K_TAIL = {"tq2_0": 2816, "q4_0": 2400, "iq4_nl": 2400}  # 11 / 75 blocks: a part
 @pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("nb", [1, 2, 4, 8])
 @pytest.mark.parametrize("extreme", [False, True])
-def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme):
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme, m):
     bn, nw = layout
     n, k = 300, K_TAIL[fmt]
-    W, x = O.problem(fmt, n, k, 1, 70 + nb + bn, extreme)
+    W, x = O.problem(fmt, n, k, m, 70 + nb + bn + 7 * m, extreme)
     wq, ws = host.split(fmt, W, n, k)
     wq_d, ws_d, x_d = dev(wq), dev(ws), dev(x)
-    print(f"{fmt} n={n} k={k} block_n={bn} nb={nb} num_warps={nw} extreme={extreme}", flush=True)
+    print(f"{fmt} n={n} k={k} m={m} block_n={bn} nb={nb} num_warps={nw} extreme={extreme}", flush=True)
     y_s, s = host.gemv_f32(fmt, wq_d, ws_d, x_d, n, k, bn, nb, 2, nw, store_s=True)
     y = host.gemv_f32(fmt, wq_d, ws_d, x_d, n, k, bn, nb, 2, nw)[0]
     xq, xd, *_ = host.quantize(fmt, x_d)
@@ -49,7 +50,7 @@ def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme):
     assert np.array_equal(s.cpu().numpy().astype(np.int64), rs) and torch.equal(s, s2) and torch.equal(s, s_emu)
     assert torch.equal(y.view(torch.int32), y_s.view(torch.int32))
     assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
-    if fmt != "tq2_0":
+    if fmt != "tq2_0" or m > 1:
         assert torch.equal(y.view(torch.int32), y_emu.view(torch.int32))
     assert O.relerr(y.cpu().numpy(), r) <= TOL
 
