@@ -117,7 +117,7 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     if (fmt == FMT_TQ2_0)  // 16 lanes per row (4 rows per wave), nb 4, 8 waves: the fastest of a sweep over knob sets
       return plan_of(32, 4, 8, 16, 1);                      // at 16400-32768 rows x 4096-8192 columns
     if ((fmt == FMT_Q4_0 || fmt == FMT_IQ4_NL) && m == 1 && mode == KOMP_MODE_DP4A && chunks <= 128)
-      // one column of rows of up to 128 blocks (the single-column kernel): 16 lanes per row, nb 2, 8 waves; 3-7%
+      // one column of rows of up to 128 blocks (the lean kernel): 16 lanes per row, nb 2, 8 waves; 3-7%
       // faster than the rule below at 28672-128256 rows x 4096 columns
       return plan_of(32, 2, 8, 16, 1);
     const int nb = chunks > 256 ? 8 : 4;
