@@ -95,15 +95,15 @@ FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kern
 
 def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None):
     """The kernel instantiation a launch of this config runs, the knobs giving lanes per row = 64 / min(block_n /
-    num_warps, 16): in dp4a mode, q4_0 / iq4_nl with 1-3 columns (nb <= 4, or 8 for one column) run the lean kernel
-    <format, lanes per row, nb, columns, fused> and one tq2_0 column (nb <= 8) the single-column kernel <lanes per
-    row, nb, fused>; everything else the general gemv_kernel <format, mode, columns, nb, fused>."""
+    num_warps, 16): in dp4a mode, q4_0 / iq4_nl / tq2_0 with 1-3 columns (nb <= 4, or 8 for one column) run the lean
+    kernel <(format,) lanes per row, nb, columns, fused>; everything else the general gemv_kernel <format, mode,
+    columns, nb, fused>."""
     cols = min(max(m, 1), 3)
-    if mode == 2 and block_n and num_warps:
+    if mode == 2 and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
         lanes = 64 // min(block_n // num_warps, 16)
-        if fmt == "tq2_0" and cols == 1 and nb in (1, 2, 4, 8):
-            return f"gemv_tq2::tq2_m1_kernel<{lanes}, {nb}, false>"
-        if fmt in ("q4_0", "iq4_nl") and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
+        if fmt == "tq2_0":
+            return f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false>"
+        if fmt in ("q4_0", "iq4_nl"):
             return f"gemv_q4::q4_lean_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, {cols}, false>"
     return f"gemv_impl::gemv_kernel<{FMT_NUM[fmt]}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
 

@@ -16,7 +16,7 @@ hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream)
       if (q4_lean_eligible(c, p)) return launch_gemv_q4_lean(c, p, stream);
       return gemv_impl::by_mode<FMT_Q4_0, false>(c, p, stream);
     case FMT_TQ2_0:
-      if (tq2_m1_eligible(c, p)) return launch_gemv_tq2_m1(c, p, stream);
+      if (tq2_lean_eligible(c, p)) return launch_gemv_tq2_lean(c, p, stream);
       return gemv_impl::by_mode<FMT_TQ2_0, false>(c, p, stream);
     default: return launch_gemv_more(c, p, stream);  // Q8_0, IQ4_NL (gemv_more.hip)
   }

@@ -1,11 +1,12 @@
-// Single-column TQ2_0 decode GEMV in dp4a mode (the BitNet decode step), unfused (q8_K in) and fused with the q8_K
-// quantizer.  Same plans, results and S as the general kernel in gemv_kernel.h (kernels.py:97-142 semantics); the
-// lanes per row group and the chunks per lane are template arguments here, which is what makes it leaner:
+// TQ2_0 decode GEMV of 1-3 activation columns in dp4a mode (the BitNet decode step), unfused (q8_K in) and fused with
+// the q8_K quantizer.  Same plans, results and S as the general kernel in gemv_kernel.h (kernels.py:97-142 semantics);
+// the lanes per row group, the chunks per lane and the columns are template arguments here, which is what makes it
+// leaner:
 //   * weight and scale loads are buffer loads from loop-invariant per-lane offsets, the tile and chunk offsets being
 //     a scalar and an immediate.  A chunk past the row's last block, and every row past the matrix, reads zeros
 //     without touching memory (the buffer range check), so no load sits behind a branch and the compiler waits for
 //     each chunk's own load instead of for the whole tile;
-//   * the activation column lies in LDS in its natural order, 288 bytes per 256-value block (the 32-byte pad puts the
+//   * the activation columns lie in LDS in their natural order, 288 bytes per 256-value block (the 32-byte pad puts the
 //     four lane quads of a 16-lane row group on disjoint banks), so a chunk's four 16-byte activation pieces are one
 //     base address plus immediates;
 //   * each lane accumulates d_x * d_w * (its chunk's partial dot) in f32 and the row group's lanes are added at the
@@ -44,10 +45,10 @@ __device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], in
 }
 
 // LPR lanes per row group (4 per block: lane q of a quad takes bytes 16q..16q+15 of the block), NB chunks per lane
-// per K step.  The arguments every first load needs fill the 14 preloaded argument dwords.
-template <int LPR, int NB, bool FUSED>
+// per K step, MC activation columns.  The arguments every first load needs fill the 14 preloaded argument dwords.
+template <int LPR, int NB, int MC, bool FUSED>
 __global__ void __launch_bounds__(1024)
-tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
+tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
               const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
               float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
               int16_t* __restrict__ XBo, int nseg, const GemvSegs segs) {
@@ -93,8 +94,9 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
 
   // ---- the staging's first loads (16 threads per block), issued before the weights so they do not queue behind
-  // them: f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) for thread i ----
-  const int nstage = nblk * 16;
+  // them: f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) of the flattened columns
+  // (X [MC][K], XQ [MC][K] and XD [MC][nblk] are dense) for thread i ----
+  const int nstage = MC * nblk * 16;
   const bool stg = tid < nstage;
   f32x4 xf[4];
   u32x4 x16;
@@ -138,13 +140,16 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
   };
   load(0, 0);
 
-  // ---- stage the column: LDS block b = its 256 q8 values in order at b * XB, then meta[b] = {d_x bits,
-  // -sum(x of the block)} for b < nblk_pad (zeros past nblk, so a chunk past the row's end adds 0 * 0) ----
+  // ---- stage the columns: LDS block b of column m = its 256 q8 values in order at (m * nblk_pad + b) * XB, then
+  // meta[m * nblk_pad + b] = {d_x bits, -sum(x of the block)} for b < nblk_pad (zeros past nblk, so a chunk past the
+  // row's end adds 0 * 0) ----
   unsigned char* xs = lds;
-  int2* meta = reinterpret_cast<int2*>(lds + nblk_pad * XB);
+  int2* meta = reinterpret_cast<int2*>(lds + MC * nblk_pad * XB);
   auto stage_one = [&](int i, const f32x4 (&v)[4], const u32x4& xq16, float dxv) {
     const int r = i & 15;
-    const int b = i >> 4;
+    const int bi = i >> 4;  // flattened block of the columns
+    int b = bi;             // its LDS slot
+    if constexpr (MC > 1) b += (bi / nblk) * (nblk_pad - nblk);
     if constexpr (FUSED) {
       u32x4 qv;
       float d;
@@ -154,7 +159,7 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
       if (r == 0) meta[b] = make_int2(__float_as_int(d), -qsum);
       if (blockIdx.x == 0 && XQo != nullptr) {  // one workgroup writes the q8_K planes out
         reinterpret_cast<u32x4*>(XQo)[i] = qv;
-        if (r == 0) XDo[b] = d;
+        if (r == 0) XDo[bi] = d;
         if (XBo != nullptr) XBo[i] = static_cast<int16_t>(bsum);
       }
     } else {
@@ -181,7 +186,10 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
     }
     stage_one(i, v, xq16, dxv);
   }
-  for (int b = nblk + tid; b < nblk_pad; b += nthreads) meta[b] = make_int2(0, 0);
+  for (int i = tid; i < MC * (nblk_pad - nblk); i += nthreads) {
+    const int m = i / (nblk_pad - nblk);
+    meta[m * nblk_pad + nblk + (i - m * (nblk_pad - nblk))] = make_int2(0, 0);
+  }
   // Publish the LDS writes to the workgroup.  Nothing else needs publishing (no other shared or global data is read
   // back), so the barrier waits for LDS operations only and the weight loads stay in flight; the compiler fences
   // keep every LDS access on its side of the barrier.
@@ -198,7 +206,9 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
-    float acc = 0.0f;
+    float acc[MC];
+#pragma unroll
+    for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
     for (int st = 0; st < nsteps; ++st) {
       if (p != 0 || st != 0) load(p, st);
       const int tb = st * BSTEP;
@@ -206,28 +216,36 @@ tq2_m1_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const 
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         if (u * BPG >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
-        const unsigned char* xp = xl + (tb + u * BPG) * XB;
-        u32x4 xv[4];
+        const float dw = f16_bits_to_f32(sc[u]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
-        const int2 mt = ml[tb + u * BPG];
-        const int sl = chunk_dot(w[u], xv, mt.y & qmask);
-        if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
-          const int sb = group_sum(sl, 4);
-          const int b = tb + u * BPG + gblk;
-          if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
+        for (int m = 0; m < MC; ++m) {
+          const int bo = m * nblk_pad + tb + u * BPG;
+          const unsigned char* xp = xl + bo * XB;
+          u32x4 xv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
+          const int2 mt = ml[bo];
+          const int sl = chunk_dot(w[u], xv, mt.y & qmask);
+          if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
+            const int sb = group_sum(sl, 4);
+            const int b = tb + u * BPG + gblk;
+            if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
+          }
+          acc[m] = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * dw, acc[m]);
         }
-        acc = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * f16_bits_to_f32(sc[u]), acc);
       }
     }
-    const float v = group_sum(acc, LPR);
-    if ((lane & (LPR - 1)) == 0 && rv) Y[row] = v;
+#pragma unroll
+    for (int m = 0; m < MC; ++m) {
+      const float v = group_sum(acc[m], LPR);
+      if ((lane & (LPR - 1)) == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+    }
   }
 }
 
-template <int LPR, int NB, bool FUSED>
+template <int LPR, int NB, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  auto kern = tq2_m1_kernel<LPR, NB, FUSED>;
+  auto kern = tq2_lean_kernel<LPR, NB, MC, FUSED>;
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -238,7 +256,7 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     }
   }
   const int nblk = c.k / 256;
-  const size_t lds = tq2_m1_lds_bytes(LPR, NB, c.k);
+  const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k);
   static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
   if (lds > lds_attr) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -260,13 +278,24 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int LPR, bool FUSED>
+template <int LPR, int MC, bool FUSED>
 hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (p.nb) {
-    case 1: return launch_k<LPR, 1, FUSED>(c, p, s);
-    case 2: return launch_k<LPR, 2, FUSED>(c, p, s);
-    case 4: return launch_k<LPR, 4, FUSED>(c, p, s);
-    case 8: return launch_k<LPR, 8, FUSED>(c, p, s);
+    case 1: return launch_k<LPR, 1, MC, FUSED>(c, p, s);
+    case 2: return launch_k<LPR, 2, MC, FUSED>(c, p, s);
+    case 4: return launch_k<LPR, 4, MC, FUSED>(c, p, s);
+    case 8:
+      if constexpr (MC == 1) return launch_k<LPR, 8, MC, FUSED>(c, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int LPR, bool FUSED>
+hipError_t by_mc(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
+  switch (c.m) {
+    case 1: return by_nb<LPR, 1, FUSED>(c, p, s);
+    case 2: return by_nb<LPR, 2, FUSED>(c, p, s);
+    case 3: return by_nb<LPR, 3, FUSED>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -274,32 +303,33 @@ hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
 template <bool FUSED>
 hipError_t by_lpr(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (p.lpr_log2) {
-    case 2: return by_nb<4, FUSED>(c, p, s);
-    case 3: return by_nb<8, FUSED>(c, p, s);
-    case 4: return by_nb<16, FUSED>(c, p, s);
-    case 5: return by_nb<32, FUSED>(c, p, s);
-    case 6: return by_nb<64, FUSED>(c, p, s);
+    case 2: return by_mc<4, FUSED>(c, p, s);
+    case 3: return by_mc<8, FUSED>(c, p, s);
+    case 4: return by_mc<16, FUSED>(c, p, s);
+    case 5: return by_mc<32, FUSED>(c, p, s);
+    case 6: return by_mc<64, FUSED>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace gemv_tq2
 
-size_t tq2_m1_lds_bytes(int lpr, int nb, int k) {
+size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k) {
   const int bstep = (lpr / 4) * nb;
   const int64_t nblk = k / 256;
   const int64_t pad = (nblk + bstep - 1) / bstep * bstep;
-  return static_cast<size_t>(pad) * (gemv_tq2::kBlockStride + 8);
+  return static_cast<size_t>(mc) * pad * (gemv_tq2::kBlockStride + 8);
 }
 
-bool tq2_m1_eligible(const GemvCall& c, const GemvPlan& p) {
-  return c.fmt == FMT_TQ2_0 && c.m == 1 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 && p.lpr_log2 <= 6 &&
-         (p.nb == 1 || p.nb == 2 || p.nb == 4 || p.nb == 8) && p.waves >= 1 && p.waves <= 16 &&
-         p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
-         tq2_m1_lds_bytes(1 << p.lpr_log2, p.nb, c.k) <= gemv_tq2::kLdsLimit;
+bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p) {
+  // one column with nb up to 8, two or three with nb up to 4 (the instantiations)
+  const bool nb_ok = p.nb == 1 || p.nb == 2 || p.nb == 4 || (p.nb == 8 && c.m == 1);
+  return c.fmt == FMT_TQ2_0 && c.m >= 1 && c.m <= 3 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 && p.lpr_log2 <= 6 &&
+         nb_ok && p.waves >= 1 && p.waves <= 16 && p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
+         tq2_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k) <= gemv_tq2::kLdsLimit;
 }
 
-hipError_t launch_gemv_tq2_m1(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
+hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (p.waves * p.rows_per_wave < p.block_n) return hipErrorInvalidConfiguration;
   return c.x != nullptr ? gemv_tq2::by_lpr<true>(c, p, stream) : gemv_tq2::by_lpr<false>(c, p, stream);
 }

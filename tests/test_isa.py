@@ -21,23 +21,22 @@ def run(*args):
 
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
-    for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_m1_kernel<", "gemv_q4::q4_lean_kernel<",
+    for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_q4::q4_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
         assert any(family in n for n in names), family
 
 
 @pytest.mark.parametrize("fmt,bn,nb,nw,name", [("q4_0", 64, 4, 4, "gemv_q4::q4_lean_kernel<0, 4, 4, 1, false>"),
-                                               ("tq2_0", 32, 2, 4, "gemv_tq2::tq2_m1_kernel<8, 2, false>"),
+                                               ("tq2_0", 32, 2, 4, "gemv_tq2::tq2_lean_kernel<8, 2, 1, false>"),
                                                ("iq4_nl", 8, 2, 8, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false>")])
 def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     # one column in dp4a mode runs the single-column kernel with 64 / min(block_n / num_warps, 16) lanes per row
     assert cli._gemv_kernel(fmt, 2, nb, 1, bn, nw) == name
     r = isa.summary(name, cli.VALUES_PER_LOAD[fmt])
     assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"] and r["loop"].get("dot4", 0) > 0
-    three = cli._gemv_kernel(fmt, 2, nb, 3, bn, nw)  # three columns: the lean kernel (q4_0, iq4_nl) or the general one
-    assert three == (name.replace(", 1, false>", ", 3, false>") if fmt != "tq2_0" else
-                     f"gemv_impl::gemv_kernel<1, 2, 3, {nb}, false>")
+    assert cli._gemv_kernel(fmt, 2, nb, 3, bn, nw) == name.replace(", 1, false>", ", 3, false>")  # three columns
+    assert cli._gemv_kernel(fmt, 2, 8, 3, bn, nw).startswith("gemv_impl::gemv_kernel<")  # nb 8 at three columns
     assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw).startswith("gemv_impl::gemv_kernel<")  # bytes mode
 
 
