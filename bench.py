@@ -41,7 +41,7 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
 # profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
-TRAFFIC_FUSED_BITNET_M1 = 4862225
+TRAFFIC_FUSED_BITNET_M1 = 4871460
 
 
 # (values per weight block, weight bytes per block, values per activation block) of each weight format
@@ -453,7 +453,7 @@ BATCH_M = (4, 16, 64)
 
 def batched_detail(torch, host, args):
     """Several activation columns (batched decode tokens) per weight matrix, q8 activations in: the matrix-core GEMM
-    (what gemv with block_n=None runs from 4 columns, TQ2_0 from 3) vs the GEMV in launches of 3 columns (its own knobs for that
+    (what gemv with block_n=None runs from 4 columns) vs the GEMV in launches of 3 columns (its own knobs for that
     column count), both as graph replays over cold weight copies.  Bytes: weights + q8 activations + f32 outputs."""
     rows = []
     gen = torch.Generator(device="cuda")

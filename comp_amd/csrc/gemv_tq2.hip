@@ -216,6 +216,21 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         if (u * BPG >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
+        if constexpr (MC == 1) {  // one column: this form of the loop compiles ~10% faster at 32768 x 8192
+          const unsigned char* xp = xl + (tb + u * BPG) * XB;
+          u32x4 xv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
+          const int2 mt = ml[tb + u * BPG];
+          const int sl = chunk_dot(w[u], xv, mt.y & qmask);
+          if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
+            const int sb = group_sum(sl, 4);
+            const int b = tb + u * BPG + gblk;
+            if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
+          }
+          acc[0] = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * f16_bits_to_f32(sc[u]), acc[0]);
+          continue;
+        }
         const float dw = f16_bits_to_f32(sc[u]);
 #pragma unroll
         for (int m = 0; m < MC; ++m) {
