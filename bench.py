@@ -12,9 +12,9 @@ served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-gr
 does not bound them.
 
 Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in + f32 outputs)
-/ their wall time (GB/s); roofline = the tq2_0_gemv
-dispatches' algorithmic bytes / their average dispatch duration, timed per dispatch with hipExtLaunchKernel events
-(the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
+/ their wall time (GB/s); roofline = the fused tq2_0_gemv launches' algorithmic bytes / their average duration over the
+timed region (events around the graph replays / launches; dispatch_us beside it is each dispatch timed alone with
+hipExtLaunchKernel events, the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
 sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list and
 Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
 gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
@@ -282,11 +282,15 @@ def headline(torch, host, abi, args):
     g_ms, g_n = disp["tq2_0_gemv"]
     launch_b = step_bytes / len(shapes)
     g_us = g_ms * 1e3 / g_n
-    achieved = launch_b / (g_us * 1e-6) / 1e9
+    # the kernel's average launch duration over the timed region: torch events around the graph replays (on the stream
+    # the kernels are launched on) / the launches in them; the eager per-dispatch events beside it (dispatch_us) read
+    # 4.5-5.4 us from run to run, since an eager launch leaves the GPU idle in between
+    launch_us = ms_per_step * 1e3 / len(shapes)
+    achieved = launch_b / (launch_us * 1e-6) / 1e9
     default_cfg = m == 1 and args.mode == 2 and args.block_n is None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": TRAFFIC_FUSED_BITNET_M1 if default_cfg else None,
-                "kernel": "tq2_0_gemv (fused quantize)",
+                "kernel": "tq2_0_gemv (fused quantize)", "launch_us": round(launch_us, 3),
                 "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b),
                 "read_floor_us": round(read_floor_us(torch, host, int(launch_b)), 3)}  # fmt: skip
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
