@@ -186,12 +186,12 @@ GemvPlan knob_plan(int block_n, int nb, int num_warps) {
 }
 
 // ---- matrix-core GEMM ----------------------------------------------------------------------------------------------
-// From gemm_min_m(fmt) activation columns on, block_n == 0 in dp4a mode (unfused) runs the matrix-core GEMM, which
-// reads the weights once per 64 columns, instead of the GEMV in column chunks of 3 (which reads them once for up to 3
-// columns, in one launch).  At 4 columns the GEMM is 1.2-1.8x faster at Llama-3-8B and BitNet-2B shapes; TQ2_0, whose
-// GEMV dot costs the most VALU work per byte, gains from 3 columns (6912 x 2560: 5.9 against 6.8 us; 32768 x 8192:
-// 23.9 against 25.4 us), every other format loses there (1.04-1.3x slower).
-int64_t gemm_min_m(int fmt) { return fmt == FMT_TQ2_0 ? 3 : 4; }
+// From kGemmMinM activation columns on, block_n == 0 in dp4a mode (unfused) runs the matrix-core GEMM, which reads the
+// weights once per 64 columns, instead of the GEMV in column chunks of 3 (which reads them once for up to 3 columns,
+// in one launch).  At 4 columns the GEMM is 1.2-1.8x faster at Llama-3-8B and BitNet-2B shapes; at 3 the lean GEMVs
+// are as fast or faster (TQ2_0 6912 x 2560: 5.6 against 5.8 us, 2560 x 6912: 5.7 against 5.2, 32768 x 8192: 22.5
+// against 23.9; Q4_0 4096 x 14336: 9.9 against 13.9).
+constexpr int64_t kGemmMinM = 4;
 constexpr int64_t kGemmMaxCols = int64_t{1} << 20;  // columns per GEMM launch (grid.y = columns / 64 at most 16384)
 
 // The GEMM's plan for m columns (one launch) and n rows.  Columns go in groups of at most 64 (4 tiles of 16), split
@@ -316,7 +316,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     mats[count++] = w;
   }
   const int64_t nblk = K / blk;
-  if (route == kRouteGemm || (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && M >= gemm_min_m(fmt))) {
+  if (route == kRouteGemm || (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && M >= kGemmMinM)) {
     GemmPlan gp;
     bool fits = true;
     for (int i = 0; i < count; ++i)

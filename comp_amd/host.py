@@ -46,8 +46,7 @@ for _f in FORMATS.values():
 MODES = {"bytes": 0, "dp4a": 2}  # mode 1 = dp4a emulated with shifts and multiplies
 FMT_ID = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}
 _XB_F32 = ("q4_0", "tq2_0", "q4_k")  # formats whose gemv_f32 entry takes the XB (bsums) output
-# columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM (abi.hip gemm_min_m)
-GEMM_MIN_M = {f: 3 if f == "tq2_0" else 4 for f in FMT_ID}
+GEMM_MIN_M = {f: 4 for f in FMT_ID}  # columns from which gemv(..., block_n=None, mode=2) runs the matrix-core GEMM
 
 
 def split(fmt, W, n, k):

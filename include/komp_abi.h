@@ -176,7 +176,7 @@ int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, in
  * rounding (the f32 sums run in another order).  Arguments and alignment as komp_q4_0_gemv / komp_tq2_0_gemv without
  * the knobs; also 64*K and 32*SW must be below 2^31 and the 16 or 32 rows of WS a workgroup stages must fit in LDS
  * (komp_gemm_plan says whether a shape qualifies).  komp_q4_0_gemv / komp_tq2_0_gemv with block_n == 0 and
- * KOMP_MODE_DP4A run this kernel for M >= 4 (TQ2_0: M >= 3) when the shape qualifies.
+ * KOMP_MODE_DP4A run this kernel for M >= 4 when the shape qualifies.
  * No reference counterpart: the reference launches its GEMV once per column (grid (cdiv(N, BLOCK_N), M),
  * src/komp/kernels.py:50); this serves batched decode, where M columns share every weight byte. */
 int komp_q4_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
