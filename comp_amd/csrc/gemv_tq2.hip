@@ -88,8 +88,6 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
   const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);
   const int vrows = max(0, min(wave_rows, N - row_base));  // rows of this wave inside the matrix
-  const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base) * SW, static_cast<int64_t>(vrows) * SW);
-  const auto srs = rsrc(WS + static_cast<int64_t>(row_base) * nblk, static_cast<int64_t>(vrows) * nblk * 2);
   const unsigned vo_w = static_cast<unsigned>(grp * SW + gblk * 64 + q * 16);
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
 
@@ -116,29 +114,32 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
   u32x4 w[NB];
   int16_t sc[NB];
   auto load = [&](int p, int st) {
-    // the pass's rows go into the per-lane offset, which the range check always sees, so a row past the matrix
-    // reads zeros in every pass; the step goes into the scalar offset
-    const unsigned vw = vo_w + static_cast<unsigned>(p * RPW * SW);
-    const unsigned vs = vo_s + static_cast<unsigned>(p * RPW * nblk * 2);
+    // a descriptor per pass, over the wave's rows from the pass's first on: a row past the matrix lies past the
+    // range, which the per-lane offset is checked against, and reads zeros in every pass; the step goes into the
+    // scalar offset, and the per-lane offsets stay the same in every pass
+    const int prow = p * RPW;  // wave-uniform
+    const int64_t left = max(0, vrows - prow);
+    const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base + prow) * SW, left * SW);
+    const auto srs = rsrc(WS + static_cast<int64_t>(row_base + prow) * nblk, left * nblk * 2);
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 64);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
     if (lim >= BSTEP) {
 #pragma unroll
       for (int u = 0; u < NB; ++u)  // the scales first: a chunk's dot then waits for its own weight load only
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vs + u * BPG * 2, so_s, 0));
+        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * BPG * 2, so_s, 0));
 #pragma unroll
-      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vw + u * BPG * 64, so_w, 2);
+      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * BPG * 64, so_w, 2);
     } else {  // the row's last, partial step
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const bool ok = gblk + u * BPG < lim;
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vs + u * BPG * 2 : kOob, so_s, 0));
+        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_s + u * BPG * 2 : kOob, so_s, 0));
       }
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const bool ok = gblk + u * BPG < lim;
-        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vw + u * BPG * 64 : kOob, so_w, 2);
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w + u * BPG * 64 : kOob, so_w, 2);
       }
     }
   };
