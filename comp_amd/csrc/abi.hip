@@ -95,7 +95,6 @@ GemvPlan plan_of(int block_n, int nb, int waves, int lpr, int passes) {
   return plan;
 }
 
-constexpr int kMaxDevices = 64;
 std::atomic<int> g_cus[kMaxDevices];
 
 // CUs of the current device (256 on MI355X; also the answer when no device can be queried)

@@ -10,8 +10,9 @@
 // w, w + W, w + 2W, ...; at the end the waves add their f32 partials in wave order.  Lane (r, g) (r = lane % 16,
 // g = lane / 16) loads bytes 16g..16g+15 of a step for row r, so one load instruction reads 64 bytes of each of 16
 // rows.  Each wave keeps D steps of loads in flight (a register ring).  Loads go through buffer descriptors whose
-// range ends at the tile's last valid row / column: a load past it, or one the kernel points past it on purpose
-// (blocks past K, steps past the wave's last), returns zeros without touching memory.
+// range ends at the tile's last valid row / column, with the whole offset of a load in its per-lane offset (no scalar
+// offset): a load past the range (a block past K in the tile's last row, every load of a step past the wave's last)
+// returns zeros without touching memory.
 //
 // Integer dots.  Operand lane l holds k slots of group l / 16 for row / column l % 16, the same slots in A and B
 // (v_mfma_i32_16x16x32_i8: 8 bytes a lane, v_mfma_i32_16x16x64_i8: 16 bytes), so a block dot needs all four lane
@@ -53,12 +54,13 @@ constexpr unsigned kOob = 0x7FFFFFF0u;     // an offset (or offset part) past ev
 constexpr unsigned NIB = 0x0F0F0F0Fu;
 constexpr unsigned CRUMB = 0x03030303u;
 
-// A raw buffer descriptor over [base, base + bytes), the range capped at 0x7FFFFFF0 (every offset the kernel uses
-// below the cap is also below 2^31, which the host checks).
+// A raw buffer descriptor over [base, base + bytes), the range clamped to [0, 0x7FFFFFF0] (every offset the kernel
+// uses below the cap is also below 2^31, which the host checks).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
-  const int n = static_cast<int>(bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0);
+  const int n = static_cast<int>(bytes <= 0 ? 0 : (bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0));
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, kRsrcWord3);
 }
+
 
 // 4x4 dword transpose across the four 16-lane rows of a wave: on entry row g of v[q] holds element (q, g), on exit
 // row g of t[j] holds element (g, j).  permlane32_swap(x, y) exchanges x's rows 2-3 with y's rows 0-1;
@@ -136,9 +138,12 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   const auto xq = rsrc(XQ + static_cast<int64_t>(m0) * K, static_cast<int64_t>(cols) * K);
   const auto xd = rsrc(XD + static_cast<int64_t>(m0) * nblk, static_cast<int64_t>(cols) * nblk * 4);
 
-  // Per-lane offsets are fixed; a step adds a wave-uniform offset (SGPR), and a step past the wave's last adds kOob,
-  // which makes all of its loads return zeros.  In a partial last Q4_0 step the lanes of blocks past K read other
-  // bytes of the tensor (never past the descriptors' ranges); those blocks are skipped when the step is computed.
+  // Per-lane offsets are fixed, and a step adds its wave-uniform offset to them, so the whole offset of every load is
+  // its per-lane offset (plus an immediate), which the range check covers; the buffer instruction's scalar offset is
+  // always 0.  A step past the wave's last adds kOob instead (every per-lane offset is below 2^31, so the sum does
+  // not wrap), which makes all of its loads return zeros without touching memory.  In a partial last Q4_0 step the
+  // lanes of blocks past K read the next row's (column's) first bytes, or zeros past the tensor's end; those blocks
+  // are skipped when the step is computed.
   unsigned va[WN];
 #pragma unroll
   for (int t = 0; t < WN; ++t) va[t] = static_cast<unsigned>((16 * t + r16) * SW + 16 * g);
@@ -164,13 +169,13 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
     const unsigned sx = sv ? (QK ? 128u : 32u * BPS * (TQ2 ? 8u : 1u)) * s : kOob;  // activation bytes per step
     const unsigned sd = sv ? (QK ? 4u * (s >> 1) : 4u * BPS * s) : kOob;
 #pragma unroll
-    for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t], sa, 2);  // nt: read once
+    for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t] + sa, 0, 2);  // nt: read once
 #pragma unroll
     for (int u = 0; u < CN; ++u) {
 #pragma unroll
       for (int v = 0; v < XV; ++v)
-        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + ((BLK32 || QK) ? 64 * v : 32 * v), sx, 0);
-      st.dx[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u], sd, 0));
+        st.x[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xq, vx[u] + sx + ((BLK32 || QK) ? 64 * v : 32 * v), 0, 0);
+      st.dx[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xd, vd[u] + sd, 0, 0));
     }
   };
 
@@ -512,6 +517,9 @@ hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
   const dim3 block(64 * WK * WR);
   const size_t lds = gemm_lds_bytes(FMT, p, c.k);
   auto kern = gemm_impl::gemm_kernel<FMT, WK, WR, WN, CN, D, STORE_S>;
+  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  if (le != hipSuccess) return le;
   const Timing tm = timing_slot(gemv_kind(FMT));
   hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, c.m, c.k, nblk, c.sw, c.wq, c.ws,
                         c.xq, c.xd, c.y, c.s);

@@ -629,13 +629,9 @@ hipError_t launch_t(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (nblk > 0 && (nblk * scw) % 8 == 0 && ws_aligned && sc_bytes <= kScaleSlabMax && sc_off + sc_bytes <= kLdsLimit)
     sc_mode = 1;
   const unsigned lds = static_cast<unsigned>(sc_mode != 0 ? sc_off + sc_bytes : base);
-  static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
-  if (lds > lds_attr) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) return e;
-    lds_attr = lds;
-  }
+  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  if (le != hipSuccess) return le;
   const Timing tm = timing_slot(gemv_kind(FMT));
   const int cpb = fmt_info(FMT).qbytes / (FMT == FMT_Q4_K ? 32 : 16);  // lane slots per block
   if ((1 << p.lpr_log2) < cpb) return hipErrorInvalidConfiguration;  // a row group holds whole blocks

@@ -236,13 +236,9 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 32;
   const size_t lds = q4_lean_lds_bytes(G, NB, MC, c.k);
-  static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
-  if (lds > lds_attr) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) return e;
-    lds_attr = static_cast<unsigned>(lds);
-  }
+  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
@@ -306,7 +302,7 @@ bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p) {
   const bool nb_ok = p.nb == 1 || p.nb == 2 || p.nb == 4 || (p.nb == 8 && c.m == 1);
   return (c.fmt == FMT_Q4_0 || c.fmt == FMT_IQ4_NL) && c.m >= 1 && c.m <= 3 && c.mode == MODE_DP4A &&
          p.lpr_log2 >= 2 && p.lpr_log2 <= 6 && nb_ok && p.waves >= 1 && p.waves <= 16 &&
-         p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
+         p.rows_per_wave == (64 >> p.lpr_log2) * p.passes && lean_strides_fit(c, 64 >> p.lpr_log2) &&
          q4_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k) <= gemv_impl::kLdsLimit;
 }
 

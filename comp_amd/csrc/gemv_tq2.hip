@@ -9,8 +9,9 @@
 //   * the activation columns lie in LDS in their natural order, 288 bytes per 256-value block (the 32-byte pad puts the
 //     four lane quads of a 16-lane row group on disjoint banks), so a chunk's four 16-byte activation pieces are one
 //     base address plus immediates;
-//   * each lane accumulates d_x * d_w * (its chunk's partial dot) in f32 and the row group's lanes are added at the
-//     end; the block dots of S are added across the lane quad only when S is stored;
+//   * the lane quad's partial dots are added (two DPP adds) into the block's exact dot, which one lane of the quad
+//     scales as d_x * d_w * f32(s) (kernels.py:141) and accumulates in f32; the row group's lanes are added at the
+//     end, in the general kernel's order, so Y is bit-identical to it;
 //   * the activation loads of the staging are issued before the weight loads, and the barrier that publishes the
 //     staged column waits for LDS writes only, so the weights stay in flight through the staging.
 #include <hip/hip_ext.h>
@@ -227,13 +228,13 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[tb + u * BPG];
-          const int sl = chunk_dot(w[u], xv, mt.y & qmask);
-          if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
-            const int sb = group_sum(sl, 4);
+          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
+          if (S != nullptr) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
           }
-          acc[0] = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * f16_bits_to_f32(sc[u]), acc[0]);
+          const float f = __int_as_float(mt.x) * f16_bits_to_f32(sc[u]) * static_cast<float>(sb);  // kernels.py:141
+          acc[0] += q == 0 ? f : 0.0f;
           continue;
         }
         const float dw = f16_bits_to_f32(sc[u]);
@@ -245,13 +246,13 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[bo];
-          const int sl = chunk_dot(w[u], xv, mt.y & qmask);
-          if (S != nullptr) {  // the block's exact dot: the quad's partial dots added
-            const int sb = group_sum(sl, 4);
+          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
+          if (S != nullptr) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
           }
-          acc[m] = __builtin_fmaf(static_cast<float>(sl), __int_as_float(mt.x) * dw, acc[m]);
+          const float f = __int_as_float(mt.x) * dw * static_cast<float>(sb);  // kernels.py:141 order
+          acc[m] += q == 0 ? f : 0.0f;
         }
       }
     }
@@ -277,13 +278,9 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 256;
   const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k);
-  static unsigned lds_attr = 64 * 1024;  // dynamic LDS above 64 KiB must be requested per kernel
-  if (lds > lds_attr) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) return e;
-    lds_attr = static_cast<unsigned>(lds);
-  }
+  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
@@ -346,6 +343,7 @@ bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p) {
   const bool nb_ok = p.nb == 1 || p.nb == 2 || p.nb == 4 || (p.nb == 8 && c.m == 1);
   return c.fmt == FMT_TQ2_0 && c.m >= 1 && c.m <= 3 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 && p.lpr_log2 <= 6 &&
          nb_ok && p.waves >= 1 && p.waves <= 16 && p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
+         lean_strides_fit(c, 64 >> p.lpr_log2) &&
          tq2_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k) <= gemv_tq2::kLdsLimit;
 }
 

@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 namespace komp {
 
 enum Fmt { FMT_Q4_0 = 0, FMT_TQ2_0 = 1, FMT_Q8_0 = 2, FMT_IQ4_NL = 3, FMT_Q4_K = 4 };
@@ -114,6 +117,39 @@ struct GemmCall {
   int k;
   int64_t sw;
 };
+
+// The lean kernels address one pass of a wave's rows with 32-bit per-lane offsets inside a buffer descriptor whose
+// range is capped at 0x7FFFFFF0 bytes, so every matrix's `rows_per_pass` row strides must fit below the cap; other
+// strides take the general kernel, which addresses rows in 64 bits.
+inline bool lean_strides_fit(const GemvCall& c, int rows_per_pass) {
+  constexpr int64_t kCap = 0x7FFFFFF0;
+  if (c.nseg <= 1) return rows_per_pass * c.sw <= kCap;
+  for (int i = 0; i < c.nseg; ++i)
+    if (rows_per_pass * c.segs.sw[i] > kCap) return false;
+  return true;
+}
+
+// Dynamic LDS above 64 KiB has to be allowed per kernel, on each device.  `limit` is one kernel's cache of the
+// largest size allowed so far, per device: the fast path reads it without a lock, and raising it happens under a
+// lock, so the allowed size only grows and a thread that sees a large enough value may launch at once.
+constexpr int kMaxDevices = 64;
+inline std::mutex& dynamic_lds_mutex() {
+  static std::mutex mu;
+  return mu;
+}
+inline hipError_t allow_dynamic_lds(const void* kernel, size_t bytes, std::atomic<unsigned> (&limit)[kMaxDevices]) {
+  if (bytes <= 64 * 1024) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached && limit[dev].load(std::memory_order_acquire) >= bytes) return hipSuccess;
+  std::lock_guard<std::mutex> lock(dynamic_lds_mutex());
+  if (cached && limit[dev].load(std::memory_order_relaxed) >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+  if (e == hipSuccess && cached) limit[dev].store(static_cast<unsigned>(bytes), std::memory_order_release);
+  return e;
+}
 
 // Dispatch hook: every launch goes through it so the tuning harness can time dispatches with hipExtLaunchKernel events.
 struct Timing {

@@ -30,6 +30,7 @@ def lib():
             "oracle_block_dots": [INT, P, P, P, I64, I64, I64, I64],
             "oracle_reference_dot": [INT, P, P, P, P, I64, I64, I64],
             "oracle_gemv_f32": [INT, P, P, P, P, P, I64, I64, I64, I64],
+            "oracle_quantize_q4_0": [P, P, I64],
         }.items():
             getattr(_lib, name).argtypes = args
             getattr(_lib, name).restype = None
@@ -95,3 +96,12 @@ def gemv_f32(fmt, wq, ws, xq, xd, n, k):
     y = np.empty((m, n), np.float32)
     lib().oracle_gemv_f32(FMT[fmt], _p(wq), _p(ws), _p(xq), _p(xd), _p(y), m, n, k, wq.shape[1])
     return y
+
+
+def quantize_q4_0_weights(w):
+    """f32 [n][k] -> ggml q4_0 blocks (bytes), as oracle.quantize_q4_0_weights."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    out = np.empty(n * (k // 32) * 18, np.uint8)
+    lib().oracle_quantize_q4_0(_p(w), _p(out), n * (k // 32))
+    return out.tobytes()

@@ -12,6 +12,9 @@
  *   oracle_reference_dot   the f64 block-order sum, src/komp/verify.py:103-120
  *   oracle_gemv_f32        the kernels' arithmetic: int32 block dot, then f32 scale and accumulate in block order,
  *                          src/komp/kernels.py:93 (q4_0: s * dw * dx) and :141 (tq2_0: dx * dw * s)
+ *   oracle_quantize_q4_0   ggml quantize_row_q4_0_ref, the rule BASELINE's workloads quantize their f32 weights
+ *                          with (restated as oracle.py quantize_q4_0_weights, which the tests compare it with); the
+ *                          large workloads' weights come from here because numpy takes tens of seconds for them
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math: every float operation is one correctly rounded
  * IEEE operation, as the reference's quantizers require).
@@ -180,5 +183,35 @@ void oracle_gemv_f32(int fmt, const uint8_t* wq, const int16_t* ws, const int8_t
       }
       y[m * N + n] = acc;
     }
+  }
+}
+
+/* f32 weights w [nblocks * 32] -> ggml q4_0 blocks out [nblocks * 18] (ggml quantize_row_q4_0_ref): max = the signed
+ * value of the first largest |x|; d = max / -8; id = d != 0 ? 1 / d : 0; q = min(15, trunc(x * id + 8.5)); bytes
+ * f16(d), then q[j] | q[j + 16] << 4 */
+void oracle_quantize_q4_0(const float* w, uint8_t* out, int64_t nblocks) {
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const float* x = w + b * 32;
+    float amax = 0.0f, mx = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+      if (fabsf(x[i]) > amax) {
+        amax = fabsf(x[i]);
+        mx = x[i];
+      }
+    }
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t q[32];
+    for (int i = 0; i < 32; ++i) {
+      const float v = x[i] * id + 8.5f; /* two roundings: -ffp-contract=off keeps them apart */
+      float t = truncf(v);
+      if (t > 15.0f) t = 15.0f;
+      q[i] = (uint8_t)(t < 0.0f ? 0 : t);
+    }
+    uint8_t* o = out + b * 18;
+    const uint16_t h = oracle_f32_to_f16(d);
+    o[0] = (uint8_t)(h & 0xFF);
+    o[1] = (uint8_t)(h >> 8);
+    for (int j = 0; j < 16; ++j) o[2 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
   }
 }

@@ -34,7 +34,12 @@ How each function is pinned (tests/test_oracle_pins.py):
   block_dots             vs brute-force Python integer loops on tiny shapes, plus bilinearity
   reference_dot          each term is exact in f64 (proved in the docstring) so tests compare the sum against
                          math.fsum-free sequential Fraction sums rounded per step
-  relerr                 parity unpinned: KURN's `relerr` formula is in the absent `kurn` package
+  relerr                 parity unpinned: KURN's `relerr` formula is in the absent `kurn` package; it is only
+                         reported (the reference's `komp verify` line prints it), no output check rests on it
+  output_error_bound     every device output is gated by it: f32 simulations in five summation orders (sequential,
+                         reversed, pairwise, lane-strided like the kernels, fused multiply-add) stay within it on
+                         random and extreme problems, and planted mistakes (a shifted scale index, a dropped block,
+                         flushed subnormal scales, a flipped sign, another column's d_x) break it
 """
 
 from __future__ import annotations
@@ -376,6 +381,87 @@ def relerr(y, r):
     if den == 0.0:
         return 0.0 if num == 0.0 else float("inf")
     return num / den
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# per-output error bound of an f32 evaluation (the gate every device output passes)
+
+F32_UNIT = 2.0**-24          # unit roundoff of f32 round-to-nearest
+F64_UNIT = 2.0**-53
+F32_HALF_MIN = 2.0**-150     # half the smallest f32 subnormal: a product's absolute rounding error below 2**-126
+
+
+def _gamma(n, u):
+    """Higham's gamma_n = n u / (1 - n u)."""
+    nu = n * u
+    return nu / (1.0 - nu)
+
+
+def output_terms(fmt, ws, xd, s):
+    """The exact terms of every output, f64 [M][N][T], and each term's factor magnitudes for the underflow slack.
+
+    Output y[m][n] of the decode GEMV is sum_t term[m][n][t] (kernels.py:93, :141): one term per block,
+    s * d_w * d_x; q4_k has two per block, sd * d * d_x and -sm * dmin * d_x (ggml vec_dot_q4_K_q8_K).  The terms
+    are exact in f64 (an integer of at most 19 significant bits times an 11-bit f16 scale and an 11-bit q8_0 or a
+    24-bit q8_K scale) except q4_k's, whose sd reaches 25 bits and rounds once.  Returns (terms, factor_sum) with
+    factor_sum[m][n][t] = |int| + |d_w| + |d_x|."""
+    dx = np.asarray(xd, np.float32).astype(np.float64)  # [M][nb]
+    s = np.asarray(s, dtype=np.int64)
+    if fmt == "q4_k":
+        meta = np.ascontiguousarray(ws, dtype=np.int16).reshape(ws.shape[0], -1, 8)
+        d = f16_bits_to_f32(meta[:, :, 0]).astype(np.float64)
+        dmin = f16_bits_to_f32(meta[:, :, 1]).astype(np.float64)
+        sd = s[..., 0].astype(np.float64)
+        sm = s[..., 1].astype(np.float64)
+        t1 = d[None] * dx[:, None, :] * sd
+        t2 = -(dmin[None] * dx[:, None, :] * sm)
+        f1 = np.abs(sd) + np.abs(d)[None] + np.abs(dx)[:, None, :]
+        f2 = np.abs(sm) + np.abs(dmin)[None] + np.abs(dx)[:, None, :]
+        return np.concatenate([t1, t2], axis=-1), np.concatenate([f1, f2], axis=-1)
+    dw = f16_bits_to_f32(ws).astype(np.float64)  # [N][nb]
+    sf = s.astype(np.float64)
+    terms = dw[None] * dx[:, None, :] * sf
+    return terms, np.abs(sf) + np.abs(dw)[None] + np.abs(dx)[:, None, :]
+
+
+def output_error_bound(fmt, ws, xd, s):
+    """Bound on |y - r| per output [M][N], for any f32 evaluation y of the GEMV against the f64 reference r.
+
+    The device forms each term as a chain of two f32 multiplications of the exact integer dot (|s| < 2**24, so
+    f32(s) is exact) and the two scales, or folds the last multiplication into a fused multiply-add, and adds the
+    terms in an order of its own (per-lane running sums, then DPP / LDS trees).  With u = 2**-24 and every f32
+    operation fl(x) = x (1 + d) + e, |d| <= u, |e| <= 2**-150 (e only for results below 2**-126; sums that land
+    there are exact):
+      * a term's product chain: |p - t| <= (2u + u^2) |t| + 2**-150 (1 + |the factor applied last|);
+      * any summation tree over n terms: |fl(sum p) - sum p| <= gamma_{n-1} sum |p| (Higham, Accuracy and
+        Stability of Numerical Algorithms, 2nd ed., eq. 4.4, which holds for every order);
+    so |y - sum t| <= gamma_{n+2} sum |t| + 2 sum_t 2**-150 (1 + |s| + |d_w| + |d_x|).  The reference sums the same
+    exact terms in f64 (q4_k's products round there once more): |r - sum t| <= gamma^{f64}_{n+2} sum |t|.
+    n is the number of terms (blocks; q4_k two per block)."""
+    terms, factors = output_terms(fmt, ws, xd, s)
+    n = terms.shape[-1]
+    mag = np.abs(terms).sum(axis=-1)
+    slack = 2.0 * F32_HALF_MIN * (terms.shape[-1] + factors.sum(axis=-1))
+    return (_gamma(n + 2, F32_UNIT) + _gamma(n + 2, F64_UNIT)) * mag + slack
+
+
+def output_check(fmt, y, ws, xd, s, r):
+    """(ok, worst): every output of y within output_error_bound of the f64 reference r; worst = max |y - r| / bound
+    over the outputs (0 when all match exactly), inf when an output is not finite or misses a zero bound."""
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64).reshape(y.shape)
+    bound = output_error_bound(fmt, ws, xd, s).reshape(y.shape)
+    if y.size == 0:
+        return True, 0.0
+    if not np.all(np.isfinite(y)):
+        return False, float("inf")
+    err = np.abs(y - r)
+    if np.any((bound == 0.0) & (err > 0.0)):
+        return False, float("inf")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(bound > 0.0, err / np.where(bound > 0.0, bound, 1.0), 0.0)
+    worst = float(ratio.max())
+    return worst <= 1.0, worst
 
 
 # ---------------------------------------------------------------------------------------------------------------------

@@ -47,4 +47,4 @@ def test_gemv_references_agree(fmt, n, k, m, extreme):
     r = C.reference_dot(fmt, ws, xd, s)
     assert np.array_equal(r, O.reference_dot(fmt, ws, xd, s))
     y = C.gemv_f32(fmt, wq, ws, xq, xd, n, k)
-    assert O.relerr(y, r) <= 1e-5
+    assert O.output_check(fmt, y, ws, xd, s, r)[0]  # the C f32 evaluation stays within the per-output bound

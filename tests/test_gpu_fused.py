@@ -8,6 +8,7 @@ import torch
 
 from comp_amd import host
 from oracle import oracle as O
+from tests.checks import outputs_ok
 
 pytestmark = pytest.mark.gpu
 
@@ -46,9 +47,10 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
         assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int16 else a, b.view(torch.uint8) if b.dtype != torch.int16 else b)
     rq, rd, rb = O.quantize(fmt, x)
     assert np.array_equal(q[0].cpu().numpy(), rq)
-    r, rs = O.gemv(fmt, host.split(fmt, W, n, k)[0], host.split(fmt, W, n, k)[1], rq, rd, n, k)
+    wq_h, ws_h = host.split(fmt, W, n, k)
+    r, rs = O.gemv(fmt, wq_h, ws_h, rq, rd, n, k)
     assert np.array_equal(s1.cpu().numpy().astype(np.int64), rs)
-    assert O.relerr(y1.cpu().numpy(), r) <= 1e-5 and O.relerr(y2.cpu().numpy(), r) <= 1e-5
+    assert outputs_ok(fmt, y1.cpu().numpy(), ws_h, rd, rs, r) and outputs_ok(fmt, y2.cpu().numpy(), ws_h, rd, rs, r)
 
 
 def test_fused_without_q_outputs():
@@ -57,5 +59,5 @@ def test_fused_without_q_outputs():
     wq, ws = host.split(fmt, W, n, k)
     y, s = host.gemv_f32(fmt, dev(wq), dev(ws), dev(x), n, k)
     rq, rd, _ = O.quantize(fmt, x)
-    r, _ = O.gemv(fmt, wq, ws, rq, rd, n, k)
-    assert s is None and O.relerr(y.cpu().numpy(), r) <= 1e-5
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    assert s is None and outputs_ok(fmt, y.cpu().numpy(), ws, rd, rs, r)

@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from comp_amd import host
+from tests.checks import outputs_ok
 from tests.golden import fixtures as G
 
 pytestmark = pytest.mark.gpu
@@ -40,5 +41,4 @@ def test_gemv_golden(mode, knobs):
         y, s = host.gemv(fmt, torch.from_numpy(wq).cuda(), torch.from_numpy(ws).cuda(), torch.from_numpy(xq).cuda(),
                          torch.from_numpy(xd).cuda(), n, k, bn, nb, mode, nw, store_s=True)  # fmt: skip
         assert np.array_equal(s.cpu().numpy().astype(np.int64), S)
-        yy = y.cpu().numpy().astype(np.float64)
-        assert np.max(np.abs(yy - Y)) <= 1e-5 * np.max(np.abs(Y))
+        assert outputs_ok(fmt, y.cpu().numpy(), ws, xd, S, Y)
