@@ -560,18 +560,16 @@ gemv_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int rows_per_wave, i
             // 24-bit multiplies (full rate): |dots| < 2^16, |sums| < 2^13, scales and mins < 64
             const int sd = __mul24(static_cast<int>(scm & 0xFFu), dd.x) + __mul24(static_cast<int>((scm >> 8) & 0xFFu), dd.y);
             const int sm = __mul24(static_cast<int>((scm >> 16) & 0xFFu), xs.x) + __mul24(static_cast<int>(scm >> 24), xs.y);
-            if (S != nullptr) {  // the block's exact (sd, sm): the quad's partial sums added
-              const int sdb = group_sum(sd, 4), smb = group_sum(sm, 4);
-              if (rv && q == 0) {
-                int32_t* sp = S + ((static_cast<int64_t>(m) * N + row) * nblk + b) * SPB;
-                sp[0] = sdb;
-                sp[1] = smb;
-              }
+            const int sdb = group_sum(sd, 4), smb = group_sum(sm, 4);  // the block's exact (sd, sm), every lane
+            if (S != nullptr && rv && q == 0) {
+              int32_t* sp = S + ((static_cast<int64_t>(m) * N + row) * nblk + b) * SPB;
+              sp[0] = sdb;
+              sp[1] = smb;
             }
-            // y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K), each lane adding its group's part (the
-            // lane sums meet in the row reduction), so Y does not depend on whether S is stored
-            acc[m] = __builtin_fmaf(static_cast<float>(sd), dw * dx, acc[m]);
-            acc[m] = __builtin_fmaf(-static_cast<float>(sm), dmin * dx, acc[m]);
+            // y += d * dx * sd - dmin * dx * sm (ggml vec_dot_q4_K_q8_K), once per block (lane 0 of the quad)
+            const float t = __builtin_fmaf(static_cast<float>(sdb), dw * dx, acc[m]);
+            const float t2 = __builtin_fmaf(-static_cast<float>(smb), dmin * dx, t);
+            acc[m] = q == 0 ? t2 : acc[m];
           } else if constexpr (FMT == FMT_Q8_0) {
             // lane pair: chunk q holds the block's values 16q .. 16q+15, dotted with the matching staged half
             const int s = group_sum(q8_0_chunk_dot<MODE>(w[u], xv[(q * MC + m) * nblk + b]), 2);

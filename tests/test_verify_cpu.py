@@ -1,5 +1,5 @@
-"""The verify module's CPU parts: KURN-shaped references, exact int dots, the bit-identical rebuild and the report line
-grammar (src/komp/verify.py:37-41, 94-120, 145-149)."""
+"""The verify module's CPU parts: the dp4a definition, the weight values, exact int dots, the bit-identical rebuild, the
+per-output bound and the report line grammar (src/komp/verify.py:37-41, 94-120, 145-149)."""
 
 import random
 
@@ -10,11 +10,34 @@ from comp_amd import host, verify
 from oracle import oracle as O
 
 
-def test_dp4a_ref_matches_oracle():
-    rng = random.Random(0)
-    for _ in range(2000):
-        a, b, c = (rng.randrange(-(2**31), 2**31) for _ in range(3))
-        assert verify.dp4a_ref(a, b, c) == int(O.dp4a(a, b, c))
+def test_dp4a_expected_matches_oracle():
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.integers(-(2**31), 2**31, size=2000).astype(np.int32) for _ in range(3))
+    a[:10] = np.asarray(verify.DP4A_EDGE_WORDS, np.int64).astype(np.int32)
+    assert np.array_equal(verify.dp4a_expected(a, b, c), O.dp4a(a, b, c))
+
+
+@pytest.mark.parametrize("fmt,n,k,m", [("q4_0", 37, 416, 3), ("tq2_0", 29, 1792, 3)])
+@pytest.mark.parametrize("extreme", [False, True])
+def test_output_bound_is_the_oracles(fmt, n, k, m, extreme):
+    """verify's per-output bound (the product package cannot import the oracle) equals oracle.output_error_bound."""
+    from kurn.gpu import ref
+
+    W, x = ref.problem(fmt, n, k, m, 3 + extreme, extreme)
+    xq, xd, _ = O.quantize(fmt, x)
+    wq, ws = host.split(fmt, W, n, k)
+    s = O.block_dots(fmt, wq, xq, n, k)
+    got = verify._output_bound(fmt, W, host.act_blocks(fmt, xq, xd), s, n, m)
+    assert np.allclose(got, O.output_error_bound(fmt, ws, xd, s), rtol=1e-12, atol=0)
+
+
+def test_weight_values_are_the_oracles():
+    from kurn.gpu import ref
+
+    for fmt, k in (("q4_0", 416), ("tq2_0", 768)):
+        W = ref.weights(fmt, random.Random(4), 9, k, True)
+        v = verify.weight_values(fmt, W).reshape(9, k)
+        assert np.array_equal(v, O.weight_values(fmt, O.split(fmt, W, 9, k)[0], 9, k))
 
 
 @pytest.mark.parametrize("fmt,n,k,m", [("q4_0", 37, 416, 3), ("tq2_0", 5, 1280, 2)])
