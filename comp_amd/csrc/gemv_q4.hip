@@ -22,17 +22,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);  // raw, 32-bit data
 }
 
-// G lanes per row group, NB blocks per lane per K step, MC activation columns.  The arguments every first load needs
-// fill the 14 preloaded argument dwords.
+// G lanes per row group, NB blocks per lane per K step, MC activation columns.  The arguments every first load needs,
+// and the segment count, fill the 14 preloaded argument dwords (a 32-bit row stride: the plans that run here keep a
+// pass's rows below 2^31 bytes).
 template <int FMT, int G, int NB, int MC, bool FUSED>
 __global__ void __launch_bounds__(1024)
-q4_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
-             const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
-             float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
-             int nseg, const GemvSegs segs) {
+q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
+               const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
+               float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
+               const GemvSegs segs) {
   constexpr int RPW = 64 / G;   // rows per wave and pass
   constexpr int BSTEP = G * NB;  // blocks per K step
   extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x;
+  // ---- the staging's first loads, issued first (they need only preloaded arguments, so they go out before the
+  // segment table of a multi-matrix launch is read, and before the weights): fused, 8 lanes per block with 4 f32
+  // values each; unfused, one lane per block with its 32 q8 bytes and d_x.  Blocks of all columns in order (X [MC][K]
+  // and XQ [MC][K] are dense, so block i of the flattened columns starts at 32 i; XD [MC][nblk] likewise) ----
+  const int nstage = FUSED ? MC * nblk * 8 : MC * nblk;
+  const bool stg = tid < nstage;
+  f32x4 xf;
+  u32x4 xa, xb;
+  float xdv = 0.0f;
+  if (stg) {
+    if constexpr (FUSED) {
+      xf = *reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + tid * 4);
+    } else {
+      const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 32);
+      xa = src[0];
+      xb = src[1];
+      xdv = XD[tid];
+    }
+  }
   int N = N1;
   int64_t SW = SW1;
   const uint8_t* WQ = WQ1;
@@ -51,7 +72,6 @@ q4_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const
     Y = segs.y[sg];
     wg -= segs.first_wg[sg];
   }
-  const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -65,25 +85,6 @@ q4_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const
   const int vrows = max(0, min(wave_rows, N - row_base));  // rows of this wave inside the matrix
   const unsigned vo_w = static_cast<unsigned>(grp * SW + g * 16);
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + g) * 2);
-
-  // ---- the staging's first loads, before the weights: fused, 8 lanes per block with 4 f32 values each; unfused,
-  // one lane per block with its 32 q8 bytes and d_x.  Blocks of all columns in order (X [MC][K] and XQ [MC][K] are
-  // dense, so block i of the flattened columns starts at 32 i; XD [MC][nblk] likewise) ----
-  const int nstage = FUSED ? MC * nblk * 8 : MC * nblk;
-  const bool stg = tid < nstage;
-  f32x4 xf;
-  u32x4 xa, xb;
-  float xdv = 0.0f;
-  if (stg) {
-    if constexpr (FUSED) {
-      xf = *reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + tid * 4);
-    } else {
-      const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 32);
-      xa = src[0];
-      xb = src[1];
-      xdv = XD[tid];
-    }
-  }
 
   // ---- weights: step (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * G + g ----
   u32x4 w[NB];
@@ -242,13 +243,14 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
+  const int sw = static_cast<int>(c.nseg > 1 ? 0 : c.sw);  // below 2^31 (q4_lean_eligible); segments carry theirs
   const Timing tm = timing_slot(gemv_kind(FMT));
   if (tm.on) {
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, c.sw, p.block_n, p.passes,
-                          c.wq, c.ws, xa, c.xd, c.y, c.s, c.xq_out, c.xd_out, c.nseg, segs);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, sw, c.nseg, p.block_n,
+                          p.passes, c.wq, c.ws, xa, c.xd, c.y, c.s, c.xq_out, c.xd_out, segs);
   } else {
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, c.sw, p.block_n, p.passes, c.wq, c.ws, xa, c.xd,
-                       c.y, c.s, c.xq_out, c.xd_out, c.nseg, segs);
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, sw, c.nseg, p.block_n, p.passes, c.wq, c.ws, xa,
+                       c.xd, c.y, c.s, c.xq_out, c.xd_out, segs);
   }
   return hipGetLastError();
 }

@@ -46,18 +46,39 @@ __device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], in
 }
 
 // LPR lanes per row group (4 per block: lane q of a quad takes bytes 16q..16q+15 of the block), NB chunks per lane
-// per K step, MC activation columns.  The arguments every first load needs fill the 14 preloaded argument dwords.
+// per K step, MC activation columns.  The arguments every first load needs, and the segment count, fill the 14
+// preloaded argument dwords (a 32-bit row stride: the plans that run here keep a pass's rows below 2^31 bytes).
 template <int LPR, int NB, int MC, bool FUSED>
 __global__ void __launch_bounds__(1024)
-tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
-              const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
-              float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
-              int16_t* __restrict__ XBo, int nseg, const GemvSegs segs) {
+tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
+                const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
+                float* __restrict__ Y1, int32_t* __restrict__ S, int8_t* __restrict__ XQo, float* __restrict__ XDo,
+                int16_t* __restrict__ XBo, const GemvSegs segs) {
   constexpr int RPW = 64 / LPR;          // rows per wave and pass
   constexpr int BPG = LPR / 4;           // blocks a row group covers per chunk slot
   constexpr int BSTEP = BPG * NB;        // blocks per K step
   constexpr int XB = kBlockStride;
   extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x;
+  // ---- the staging's first loads (16 threads per block), issued first: they need only preloaded arguments, so they
+  // go out before anything else (the segment table of a multi-matrix launch included) and do not queue behind the
+  // weights.  f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) of the flattened
+  // columns (X [MC][K], XQ [MC][K] and XD [MC][nblk] are dense) for thread i ----
+  const int nstage = MC * nblk * 16;
+  const bool stg = tid < nstage;
+  f32x4 xf[4];
+  u32x4 x16;
+  float xdv = 0.0f;
+  if (stg) {
+    if constexpr (FUSED) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + tid * 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xf[t] = src[t];
+    } else {
+      x16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 16);
+      if ((tid & 15) == 0) xdv = XD[tid >> 4];
+    }
+  }
   int N = N1;
   int64_t SW = SW1;
   const uint8_t* WQ = WQ1;
@@ -76,7 +97,6 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
     Y = segs.y[sg];
     wg -= segs.first_wg[sg];
   }
-  const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -92,24 +112,6 @@ tq2_lean_kernel(int N1, int nblk, int64_t SW1, int rows_per_wg, int passes, cons
   const unsigned vo_w = static_cast<unsigned>(grp * SW + gblk * 64 + q * 16);
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
 
-  // ---- the staging's first loads (16 threads per block), issued before the weights so they do not queue behind
-  // them: f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) of the flattened columns
-  // (X [MC][K], XQ [MC][K] and XD [MC][nblk] are dense) for thread i ----
-  const int nstage = MC * nblk * 16;
-  const bool stg = tid < nstage;
-  f32x4 xf[4];
-  u32x4 x16;
-  float xdv = 0.0f;
-  if (stg) {
-    if constexpr (FUSED) {
-      const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + tid * 16);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) xf[t] = src[t];
-    } else {
-      x16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 16);
-      if ((tid & 15) == 0) xdv = XD[tid >> 4];
-    }
-  }
 
   // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk ----
   u32x4 w[NB];
@@ -284,13 +286,14 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
   const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
+  const int sw = static_cast<int>(c.nseg > 1 ? 0 : c.sw);  // below 2^31 (tq2_lean_eligible); segments carry theirs
   const Timing tm = timing_slot(gemv_kind(FMT_TQ2_0));
   if (tm.on) {
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, c.sw, p.block_n, p.passes,
-                          c.wq, c.ws, xa, c.xd, c.y, c.s, c.xq_out, c.xd_out, c.xb_out, c.nseg, segs);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.n, nblk, sw, c.nseg, p.block_n,
+                          p.passes, c.wq, c.ws, xa, c.xd, c.y, c.s, c.xq_out, c.xd_out, c.xb_out, segs);
   } else {
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, c.sw, p.block_n, p.passes, c.wq, c.ws, xa, c.xd,
-                       c.y, c.s, c.xq_out, c.xd_out, c.xb_out, c.nseg, segs);
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.n, nblk, sw, c.nseg, p.block_n, p.passes, c.wq, c.ws, xa,
+                       c.xd, c.y, c.s, c.xq_out, c.xd_out, c.xb_out, segs);
   }
   return hipGetLastError();
 }
