@@ -16,7 +16,8 @@ Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: wei
 timed region (events around the graph replays / launches; dispatch_us beside it is each dispatch timed alone with
 hipExtLaunchKernel events, the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
 sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list and
-Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs); multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
+Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs); configs = every configuration of the workload
+list in the modes (dp4a, bytes) and knob sets it names; multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
 gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
 (Q4_0, and 14336 x 4096 in Q8_0, IQ4_NL and Q4_K) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against
 GEMV launches of 3 columns; ingest = ggml block bytes split into the planes on the device.
@@ -393,6 +394,72 @@ def detail(torch, host, abi, args):
     return rows
 
 
+# The workload list's configurations with the modes and knobs each names: (config, fmt, N, K, column counts, modes,
+# knob sets (block_n, nb, num_warps), None = the library's plan, activation outlier fraction).  Knob sets apply at the
+# first column count only (config 3's tune space is the spec's, at one column).
+CONFIG_ROWS = (
+    (1, "q4_0", 4096, 4096, (1,), (2, 0), (None, (64, 4, 4)), 0.0),
+    (2, "tq2_0", 6912, 2560, (1, 2, 3), (2, 0), (None, (64, 1, 4)), 0.0),
+    (2, "tq2_0", 2560, 6912, (1, 2, 3), (2, 0), (None, (64, 1, 4)), 0.0),
+    (3, "q4_0", 6144, 4096, (1, 2, 3), (2, 0), (None,), 0.01),
+    (3, "q4_0", 4096, 4096, (1, 2, 3), (2, 0), (None, (32, 4, 4), (32, 8, 4), (64, 4, 4), (64, 8, 4)), 0.01),
+    (3, "q4_0", 28672, 4096, (1, 2, 3), (2, 0), (None,), 0.01),
+    (3, "q4_0", 4096, 14336, (1, 2, 3), (2, 0), (None,), 0.01),
+    (4, "q4_0", 128256, 4096, (1,), (2,), (None,), 0.0),
+    (4, "q4_0", 28672, 8192, (1,), (2,), (None,), 0.0),
+    (4, "tq2_0", 32768, 8192, (1,), (2,), (None,), 0.0),
+    (5, "q4_0", 4097, 4192, (1, 3), (2, 0), (None,), 0.0),
+    (5, "q4_0", 6913, 4192, (1, 3), (2, 0), (None,), 0.0),
+    (5, "q4_0", 127, 4192, (1, 3), (2, 0), (None,), 0.0),
+    (5, "tq2_0", 4097, 2816, (1, 3), (2, 0), (None,), 0.0),
+    (5, "tq2_0", 6913, 2816, (1, 3), (2, 0), (None,), 0.0),
+    (5, "tq2_0", 127, 2816, (1, 3), (2, 0), (None,), 0.0),
+)  # fmt: skip
+
+
+def config_detail(torch, host, args):
+    """Every configuration of the workload list in each mode and knob set it names: quantizer output (q8 planes) in,
+    the GEMV alone as graph replays over cold weight copies; us/call, GB/s, % of peak and the streaming-read floor of
+    the shape's bytes.  Mode 0 is the bytes mode (bytes unpacked to int first), 2 dp4a (v_dot4c_i32_i8)."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 5)
+    for cfg, fmt, n, k, ms, modes, knob_sets, outliers in CONFIG_ROWS:
+        copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
+        nc = len(copies)
+        floor = read_floor_us(torch, host, gemv_bytes(fmt, n, k, 1))
+        for m in ms:
+            x = torch.randn((m, k), generator=gen, device="cuda")
+            if outliers:
+                x = torch.where(torch.rand((m, k), generator=gen, device="cuda") < outliers, x * 20.0, x)
+            xq, xd = host.quantize(fmt, x)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            for mode in modes:
+                for knobs in knob_sets if m == ms[0] else (None,):
+                    bn, nb, nw = knobs if knobs else (None, 0, 0)
+
+                    def call(i, copies=copies, xq=xq, xd=xd, y=y, fmt=fmt, n=n, k=k, kn=(bn, nb, nw), mode=mode):
+                        wq, ws = copies[i % nc]
+                        host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, kn[0], kn[1], mode, kn[2])
+
+                    per_graph = nc * math.ceil(64 / nc)
+                    reps = 2 * per_graph
+                    ms_t, _ = timed_steps(torch, call, nc, reps, per_graph)
+                    b = gemv_bytes(fmt, n, k, m)
+                    us = ms_t * 1e3 / reps
+                    gemm = knobs is None and host.uses_gemm(fmt, m, n, k, mode=mode)
+                    rows.append({"config": cfg, "fmt": fmt, "n": n, "k": k, "m": m,
+                                 "mode": {0: "bytes", 2: "dp4a"}[mode],
+                                 "knobs": list(knobs) if knobs else "library plan",
+                                 "path": "gemm" if gemm else "gemv", "outliers": outliers, "bytes": b,
+                                 "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                                 "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "read_floor_us": round(floor, 3),
+                                 "of_read_floor": round(floor / us, 3), "copies": nc})  # fmt: skip
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
 MULTI_CASES = (  # (name, fmt, [rows per matrix], K): projections stored as separate tensors that share one input
     ("bitnet2b_ffn_gate_up", "tq2_0", (6912, 6912), 2560),
     ("llama3_8b_q_k_v", "q4_0", (4096, 1024, 1024), 4096),
@@ -567,6 +634,42 @@ def batched_calls(torch, host, args):
     return rows
 
 
+COUNTER_CASES = (  # (fmt, N, K, columns, launch): the kernels the hardware-counter tables cover
+    ("tq2_0", 6912, 2560, 1, "fused"), ("tq2_0", 2560, 6912, 1, "fused"),
+    ("tq2_0", 6912, 2560, 3, "fused"), ("tq2_0", 2560, 6912, 3, "fused"),
+    ("tq2_0", 32768, 8192, 1, "gemv"), ("q4_0", 4096, 14336, 1, "gemv"), ("q4_0", 4096, 14336, 3, "gemv"),
+    ("q4_0", 128256, 4096, 1, "gemv"), ("q4_0", 14336, 4096, 64, "gemm"),
+)  # fmt: skip
+
+
+def counter_calls(torch, host, args):
+    """COUNTER_CASES, args.counter_calls eager launches each over cold weight copies, untimed (library plans, dp4a;
+    fused = f32 activations quantized inside the launch, gemv / gemm = q8 activations in): the dispatches one
+    rocprofv3 --pmc pass reads."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 6)
+    for fmt, n, k, m, launch in COUNTER_CASES:
+        copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
+        x = torch.randn((m, k), generator=gen, device="cuda")
+        xq, xd = host.quantize(fmt, x)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for i in range(args.counter_calls):
+            wq, ws = copies[i % len(copies)]
+            if launch == "fused":
+                host.gemv_f32_into(fmt, wq, ws, x, y, n, k)
+            elif launch == "gemm":
+                host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)
+            else:
+                host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, 2, 0)
+        torch.cuda.synchronize()
+        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "launch": launch, "calls": args.counter_calls,
+                     "bytes": step_bytes_fused(fmt, n, k, m) if launch == "fused" else gemv_bytes(fmt, n, k, m)})
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -586,6 +689,8 @@ def main():
     ap.add_argument("--batched-calls", type=int, default=0, metavar="N",
                     help="with --batched-only: run each case's GEMM N times eagerly instead of timing it (a few "
                          "dispatches, for hardware-counter runs)")
+    ap.add_argument("--counter-calls", type=int, default=0, metavar="N",
+                    help="only launch the COUNTER_CASES kernels N times each, untimed (for rocprofv3 --pmc passes)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB device buffer 10 times (the known-size kernel that scales the PMC "
                          "FETCH_SIZE / WRITE_SIZE readings)")  # fmt: skip
@@ -616,6 +721,10 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 10}), flush=True)
         return 0
 
+    if args.counter_calls > 0:
+        print(json.dumps({"counter_calls": counter_calls(torch, host, args)}), flush=True)
+        return 0
+
     if args.batched_only:
         rows = batched_calls(torch, host, args) if args.batched_calls > 0 else batched_detail(torch, host, args)
         print(json.dumps({"batched_gemm": rows}), flush=True)
@@ -630,6 +739,7 @@ def main():
         out["cpu_baseline"] = cpu_baseline(args, step_bytes, args.cpu_seconds)
     if not args.no_detail:
         out["detail"] = detail(torch, host, _abi, args)
+        out["configs"] = config_detail(torch, host, args)
         out["multi_matrix"] = multi_detail(torch, host, args)
         out["batched_gemm"] = batched_detail(torch, host, args)
         out["ingest"] = ingest_detail(torch, host, args)
