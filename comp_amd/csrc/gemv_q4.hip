@@ -89,7 +89,7 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
   // ---- weights: step (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * G + g ----
   u32x4 w[NB];
   int16_t sc[NB];
-  auto load = [&](int p, int st) {
+  auto load = [&](int p, int st, bool first) {
     // a descriptor per pass, over the wave's rows from the pass's first on: a row past the matrix lies past the
     // range, which the per-lane offset is checked against, and reads zeros in every pass; the step goes into the
     // scalar offset, and the per-lane offsets stay the same in every pass
@@ -100,13 +100,13 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 16);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the step's first to the row's end (wave-uniform)
-    if (lim >= BSTEP) {
+    if (!first && lim >= BSTEP) {
 #pragma unroll
       for (int u = 0; u < NB; ++u)  // the scales first: a block's dot then waits for its own weight load only
         sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * G * 2, so_s, 0));
 #pragma unroll
       for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * G * 16, so_w, 2);
-    } else {  // the row's last, partial step
+    } else {  // the row's last, partial step, and the first tile
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const bool ok = g + u * G < lim;
@@ -119,7 +119,9 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
       }
     }
   };
-  load(0, 0);
+  // The first tile's loads take the selecting form whatever the step: behind an if / else the compiler's wait
+  // counting loses their place after the staging loads, and the staging then waits for the weights as well.
+  load(0, 0, true);
 
   // ---- stage the columns: xl[m][b] = activations 0..15 of block b of column m, xh[m][b] = 16..31, meta[m][b] =
   // {d_x bits, -8 * sum(x) (Q4_0; IQ4_NL 0)} for b < nblk_pad (zeros past nblk, so a block past the row's end adds 0);
@@ -196,7 +198,7 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
 #pragma unroll
     for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
     for (int st = 0; st < nsteps; ++st) {
-      if (p != 0 || st != 0) load(p, st);
+      if (p != 0 || st != 0) load(p, st, false);
       const int tb = st * BSTEP;
       const int lim = nblk - tb;  // blocks from the step's first to the row's end (wave-uniform)
 #pragma unroll

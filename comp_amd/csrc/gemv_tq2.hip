@@ -116,7 +116,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk ----
   u32x4 w[NB];
   int16_t sc[NB];
-  auto load = [&](int p, int st) {
+  auto load = [&](int p, int st, bool first) {
     // a descriptor per pass, over the wave's rows from the pass's first on: a row past the matrix lies past the
     // range, which the per-lane offset is checked against, and reads zeros in every pass; the step goes into the
     // scalar offset, and the per-lane offsets stay the same in every pass
@@ -127,13 +127,13 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 64);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
-    if (lim >= BSTEP) {
+    if (!first && lim >= BSTEP) {
 #pragma unroll
       for (int u = 0; u < NB; ++u)  // the scales first: a chunk's dot then waits for its own weight load only
         sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * BPG * 2, so_s, 0));
 #pragma unroll
       for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * BPG * 64, so_w, 2);
-    } else {  // the row's last, partial step
+    } else {  // the row's last, partial step, and the first tile
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const bool ok = gblk + u * BPG < lim;
@@ -146,7 +146,9 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
       }
     }
   };
-  load(0, 0);
+  // The first tile's loads take the selecting form whatever the step: behind an if / else the compiler's wait
+  // counting loses their place after the staging loads, and the staging then waits for the weights as well.
+  load(0, 0, true);
 
   // ---- stage the columns: LDS block b of column m = its 256 q8 values in order at (m * nblk_pad + b) * XB, then
   // meta[m * nblk_pad + b] = {d_x bits, -sum(x of the block)} for b < nblk_pad (zeros past nblk, so a chunk past the
@@ -218,7 +220,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
 #pragma unroll
     for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
     for (int st = 0; st < nsteps; ++st) {
-      if (p != 0 || st != 0) load(p, st);
+      if (p != 0 || st != 0) load(p, st, false);
       const int tb = st * BSTEP;
       const int lim = nblk - tb;  // blocks from the tile's first to the row's end (wave-uniform)
 #pragma unroll
