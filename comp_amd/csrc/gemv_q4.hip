@@ -17,15 +17,17 @@ namespace gemv_q4 {
 
 constexpr unsigned kOob = 0x7FFFFFF0u;  // a buffer offset past every descriptor's range: the load returns zeros
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
-  const int n = static_cast<int>(bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);  // raw, 32-bit data
+// A raw buffer descriptor over `bytes` (at most 0x7FFFFFF0: one pass's rows, which the plans keep below 2^31 bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
 // G lanes per row group, NB blocks per lane per K step, MC activation columns.  The arguments every first load needs,
 // and the segment count, fill the 14 preloaded argument dwords (a 32-bit row stride: the plans that run here keep a
-// pass's rows below 2^31 bytes).
-template <int FMT, int G, int NB, int MC, bool FUSED>
+// pass's rows below 2^31 bytes).  ONE: the plan has one pass and one K step, so the weight stream is straight-line
+// code with no loop and no reload (a launch starts with a cold instruction cache, and every 64-byte line of code on
+// the way to the first dot costs tens of nanoseconds of fetch).
+template <int FMT, int G, int NB, int MC, bool FUSED, bool ONE>
 __global__ void __launch_bounds__(1024)
 q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
                const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
@@ -55,18 +57,18 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
     }
   }
   int N = N1;
-  int64_t SW = SW1;
+  unsigned SW = static_cast<unsigned>(SW1);  // a row's bytes: one pass's rows span at most 0x7FFFFFF0 of them
   const uint8_t* WQ = WQ1;
   const int16_t* WS = WS1;
   float* Y = Y1;
   int wg = blockIdx.x;
-  if (nseg > 1) {  // several matrices sharing the column: this workgroup's one (scalar compares on the arguments)
+  if (__builtin_expect(nseg > 1, 0)) {  // several matrices sharing the column: this workgroup's one (scalar compares on the arguments)
     int sg = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSegs; ++i)
       if (i < nseg && wg >= segs.first_wg[i]) sg = i;
     N = segs.n[sg];
-    SW = segs.sw[sg];
+    SW = static_cast<unsigned>(segs.sw[sg]);
     WQ = segs.wq[sg];
     WS = segs.ws[sg];
     Y = segs.y[sg];
@@ -77,26 +79,27 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane & (G - 1);
   const int grp = lane / G;
-  const int nsteps = (nblk + BSTEP - 1) / BSTEP;
+  const int nsteps = ONE ? 1 : (nblk + BSTEP - 1) / BSTEP;
+  const int npass = ONE ? 1 : passes;
   const int nblk_pad = nsteps * BSTEP;
-  const int rows_per_wave = RPW * passes;
+  const int rows_per_wave = RPW * npass;
   const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);
   const int vrows = max(0, min(wave_rows, N - row_base));  // rows of this wave inside the matrix
-  const unsigned vo_w = static_cast<unsigned>(grp * SW + g * 16);
+  const unsigned vo_w = grp * SW + g * 16;
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + g) * 2);
 
   // ---- weights: step (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * G + g ----
   u32x4 w[NB];
   int16_t sc[NB];
   auto load = [&](int p, int st, bool first) {
-    // a descriptor per pass, over the wave's rows from the pass's first on: a row past the matrix lies past the
-    // range, which the per-lane offset is checked against, and reads zeros in every pass; the step goes into the
-    // scalar offset, and the per-lane offsets stay the same in every pass
+    // a descriptor per pass, over the pass's rows inside the matrix: a row past the matrix lies past the range,
+    // which the per-lane offset is checked against, and reads zeros; the step goes into the scalar offset, and the
+    // per-lane offsets stay the same in every pass
     const int prow = p * RPW;  // wave-uniform
-    const int64_t left = max(0, vrows - prow);
-    const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base + prow) * SW, left * SW);
-    const auto srs = rsrc(WS + static_cast<int64_t>(row_base + prow) * nblk, left * nblk * 2);
+    const unsigned rows = __builtin_amdgcn_readfirstlane(min(RPW, max(0, vrows - prow)));  // wave-uniform
+    const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base + prow) * SW, rows * SW);
+    const auto srs = rsrc(WS + static_cast<int64_t>(row_base + prow) * nblk, rows * static_cast<unsigned>(nblk) * 2);
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 16);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the step's first to the row's end (wave-uniform)
@@ -143,7 +146,7 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
     const unsigned packed = q8_0_group8(v, d, qsum);  // the quant_q8_0 arithmetic (byte-identical planes)
     reinterpret_cast<unsigned*>(e < 4 ? xl + b : xh + b)[e & 3] = packed;
     if (e == 0) meta[b] = make_int2(__float_as_int(d), FMT == FMT_Q4_0 ? -8 * qsum : 0);
-    if (blockIdx.x == 0 && XQo != nullptr) {  // one workgroup writes the q8_0 planes out
+    if (__builtin_expect(blockIdx.x == 0 && XQo != nullptr, 0)) {  // one workgroup writes the q8_0 planes out
       reinterpret_cast<unsigned*>(XQo)[i] = packed;
       if (e == 0) XDo[bi] = d;
     }
@@ -190,7 +193,7 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
   const u32x4* xlg = xl + g;
   const u32x4* xhg = xh + g;
   const int2* mg = meta + g;
-  for (int p = 0; p < passes; ++p) {
+  for (int p = 0; p < npass; ++p) {
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
@@ -212,7 +215,7 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
           const int2 mt = mg[bm];
           const int s = FMT == FMT_Q4_0 ? gemv_impl::q4_0_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm], mt.y)
                                         : gemv_impl::iq4_nl_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm]);
-          if (S != nullptr && rv && bo + g < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + bo + g] = s;
+          if (__builtin_expect(S != nullptr, 0) && rv && bo + g < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + bo + g] = s;
           acc[m] += static_cast<float>(s) * dw * __int_as_float(mt.x);  // kernels.py:93 order
         }
       }
@@ -227,7 +230,9 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
 
 template <int FMT, int G, int NB, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  auto kern = q4_lean_kernel<FMT, G, NB, MC, FUSED>;
+  // the single-pass, single-step form for one column (the decode case; two and three columns keep the general one)
+  const bool one = MC == 1 && p.passes == 1 && c.k / 32 <= G * NB;
+  auto kern = one ? q4_lean_kernel<FMT, G, NB, MC, FUSED, MC == 1> : q4_lean_kernel<FMT, G, NB, MC, FUSED, false>;
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -239,8 +244,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 32;
   const size_t lds = q4_lean_lds_bytes(G, NB, MC, c.k);
-  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
-  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  static std::atomic<unsigned> lds_limit[2][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[one ? 1 : 0]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));

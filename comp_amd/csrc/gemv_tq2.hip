@@ -26,9 +26,9 @@ constexpr int kBlockStride = 288;        // LDS bytes per staged 256-value block
 constexpr unsigned kOob = 0x7FFFFFF0u;   // a buffer offset past every descriptor's range: the load returns zeros
 constexpr size_t kLdsLimit = 160 * 1024;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
-  const int n = static_cast<int>(bytes < 0x7FFFFFF0 ? bytes : 0x7FFFFFF0);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);  // raw, 32-bit data
+// A raw buffer descriptor over `bytes` (at most 0x7FFFFFF0: one pass's rows, which the plans keep below 2^31 bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
 // The partial int32 dot of one 16-byte chunk with its four 16-byte activation pieces (piece j pairs with the crumbs
@@ -48,7 +48,10 @@ __device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], in
 // LPR lanes per row group (4 per block: lane q of a quad takes bytes 16q..16q+15 of the block), NB chunks per lane
 // per K step, MC activation columns.  The arguments every first load needs, and the segment count, fill the 14
 // preloaded argument dwords (a 32-bit row stride: the plans that run here keep a pass's rows below 2^31 bytes).
-template <int LPR, int NB, int MC, bool FUSED>
+// ONE: the plan has one pass and one K step (every decode shape whose rows fit one step), so the weight stream is
+// straight-line code with no loop and no reload: a launch starts with a cold instruction cache, and every 64-byte
+// line of code on the way to the first dot costs tens of nanoseconds of fetch.
+template <int LPR, int NB, int MC, bool FUSED, bool ONE>
 __global__ void __launch_bounds__(1024)
 tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
                 const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
@@ -80,18 +83,18 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
     }
   }
   int N = N1;
-  int64_t SW = SW1;
+  unsigned SW = static_cast<unsigned>(SW1);  // a row's bytes: one pass's rows span at most 0x7FFFFFF0 of them
   const uint8_t* WQ = WQ1;
   const int16_t* WS = WS1;
   float* Y = Y1;
   int wg = blockIdx.x;
-  if (nseg > 1) {  // several matrices sharing the column: this workgroup's one (scalar compares on the arguments)
+  if (__builtin_expect(nseg > 1, 0)) {  // several matrices sharing the column: this workgroup's one (scalar compares on the arguments)
     int sg = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSegs; ++i)
       if (i < nseg && wg >= segs.first_wg[i]) sg = i;
     N = segs.n[sg];
-    SW = segs.sw[sg];
+    SW = static_cast<unsigned>(segs.sw[sg]);
     WQ = segs.wq[sg];
     WS = segs.ws[sg];
     Y = segs.y[sg];
@@ -103,13 +106,14 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   const int q = lane & 3;
   const int gblk = (lane & (LPR - 1)) >> 2;
   const int grp = lane / LPR;
-  const int nsteps = (nblk + BSTEP - 1) / BSTEP;
+  const int nsteps = ONE ? 1 : (nblk + BSTEP - 1) / BSTEP;
+  const int npass = ONE ? 1 : passes;
   const int nblk_pad = nsteps * BSTEP;
-  const int rows_per_wave = RPW * passes;
+  const int rows_per_wave = RPW * npass;
   const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);
   const int vrows = max(0, min(wave_rows, N - row_base));  // rows of this wave inside the matrix
-  const unsigned vo_w = static_cast<unsigned>(grp * SW + gblk * 64 + q * 16);
+  const unsigned vo_w = grp * SW + gblk * 64 + q * 16;
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
 
 
@@ -117,13 +121,13 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   u32x4 w[NB];
   int16_t sc[NB];
   auto load = [&](int p, int st, bool first) {
-    // a descriptor per pass, over the wave's rows from the pass's first on: a row past the matrix lies past the
-    // range, which the per-lane offset is checked against, and reads zeros in every pass; the step goes into the
-    // scalar offset, and the per-lane offsets stay the same in every pass
+    // a descriptor per pass, over the pass's rows inside the matrix: a row past the matrix lies past the range,
+    // which the per-lane offset is checked against, and reads zeros; the step goes into the scalar offset, and the
+    // per-lane offsets stay the same in every pass
     const int prow = p * RPW;  // wave-uniform
-    const int64_t left = max(0, vrows - prow);
-    const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base + prow) * SW, left * SW);
-    const auto srs = rsrc(WS + static_cast<int64_t>(row_base + prow) * nblk, left * nblk * 2);
+    const unsigned rows = __builtin_amdgcn_readfirstlane(min(RPW, max(0, vrows - prow)));  // wave-uniform
+    const auto wrs = rsrc(WQ + static_cast<int64_t>(row_base + prow) * SW, rows * SW);
+    const auto srs = rsrc(WS + static_cast<int64_t>(row_base + prow) * nblk, rows * static_cast<unsigned>(nblk) * 2);
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 64);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
@@ -167,7 +171,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
       const int bsum = q8_K_row16(v, r, qv, d, qsum);  // the quant_q8_K arithmetic (byte-identical planes)
       *reinterpret_cast<u32x4*>(xs + b * XB + r * 16) = qv;
       if (r == 0) meta[b] = make_int2(__float_as_int(d), -qsum);
-      if (blockIdx.x == 0 && XQo != nullptr) {  // one workgroup writes the q8_K planes out
+      if (__builtin_expect(blockIdx.x == 0 && XQo != nullptr, 0)) {  // one workgroup writes the q8_K planes out
         reinterpret_cast<u32x4*>(XQo)[i] = qv;
         if (r == 0) XDo[bi] = d;
         if (XBo != nullptr) XBo[i] = static_cast<int16_t>(bsum);
@@ -212,7 +216,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
   const int2* ml = meta + gblk;
   const int qmask = q == 0 ? -1 : 0;  // the block's -sum(x) joins one lane of the quad
-  for (int p = 0; p < passes; ++p) {
+  for (int p = 0; p < npass; ++p) {
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
@@ -233,7 +237,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[tb + u * BPG];
           const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
-          if (S != nullptr) {
+          if (__builtin_expect(S != nullptr, 0)) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
           }
@@ -251,7 +255,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[bo];
           const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
-          if (S != nullptr) {
+          if (__builtin_expect(S != nullptr, 0)) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
           }
@@ -270,7 +274,8 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
 
 template <int LPR, int NB, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  auto kern = tq2_lean_kernel<LPR, NB, MC, FUSED>;
+  const bool one = p.passes == 1 && c.k / 256 <= (LPR / 4) * NB;
+  auto kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false>;
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -282,8 +287,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 256;
   const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k);
-  static std::atomic<unsigned> lds_limit[kMaxDevices];  // this instantiation's allowed dynamic LDS, per device
-  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit);
+  static std::atomic<unsigned> lds_limit[2][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[one ? 1 : 0]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
