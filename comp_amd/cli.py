@@ -93,18 +93,24 @@ VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64, "q8_0": 16, "iq4_nl": 32, "q4_k": 64
 FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kernels' format template argument
 
 
-def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None):
+def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     """The kernel instantiation a launch of this config runs, the knobs giving lanes per row = 64 / min(block_n /
     num_warps, 16): in dp4a mode, q4_0 / iq4_nl / tq2_0 with 1-3 columns (nb <= 4, or 8 for one column) run the lean
-    kernel <(format,) lanes per row, nb, columns, fused>; everything else the general gemv_kernel <format, mode,
-    columns, nb, fused>."""
+    kernel <(format,) lanes per row, nb, columns, fused, one pass>; everything else the general gemv_kernel <format,
+    mode, columns, nb, fused>.  "One pass" is the lean kernel's single-pass, single-K-step form, which the launch picks
+    when the rows per wave fit one pass and a row's K blocks one step (the single-column form only for q4_0 / iq4_nl);
+    without k the loop form is named."""
     cols = min(max(m, 1), 3)
     if mode == 2 and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
-        lanes = 64 // min(block_n // num_warps, 16)
+        rpw = block_n // num_warps
+        lanes = 64 // min(rpw, 16)
+        one_pass = rpw <= 16 and k is not None
         if fmt == "tq2_0":
-            return f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false>"
+            one = one_pass and k // 256 <= (lanes // 4) * nb
+            return f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
         if fmt in ("q4_0", "iq4_nl"):
-            return f"gemv_q4::q4_lean_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, {cols}, false>"
+            one = one_pass and cols == 1 and k // 32 <= lanes * nb
+            return f"gemv_q4::q4_lean_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, {cols}, false, {str(one).lower()}>"
     return f"gemv_impl::gemv_kernel<{FMT_NUM[fmt]}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
 
 
@@ -140,8 +146,8 @@ def cmd_gen(args):
     fmt = c["weights"]
     quant = "quant_q8_0" if fmt == "q4_0" else "quant_q8_K"
     try:
-        r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1), c.get("block_n"), c.get("num_warps")),
-                        VALUES_PER_LOAD[fmt], keep=out is not None)  # fmt: skip
+        r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1), c.get("block_n"), c.get("num_warps"),
+                                     c.get("k")), VALUES_PER_LOAD[fmt], keep=out is not None)  # fmt: skip
         q = isa.summary(f"{quant}_kernel", 1, keep=out is not None)
     except (OSError, RuntimeError, KeyError) as e:
         print(f"komp gen: {e}", file=sys.stderr)

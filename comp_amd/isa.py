@@ -202,12 +202,17 @@ _INT_VALU = re.compile(r"^v_(and|or|xor|lshl|lshr|ashr|bfe|bfi|perm|alignbyte|ad
 
 
 def loops(insts):
-    """Loops as (first, last) instruction index ranges: each backward branch and the instruction it jumps to."""
+    """Loops as (first, last) instruction index ranges: each backward branch and the instruction it jumps to.  A
+    backward branch across an `s_endpgm` is the way back from a block the compiler placed after the kernel's end (an
+    unlikely path), not a loop."""
     index = {addr: i for i, (addr, _, _, _) in enumerate(insts)}
+    ends = [i for i, (_, mn, _, _) in enumerate(insts) if mn.startswith("s_endpgm")]
     spans = set()
     for i, (addr, mn, _, target) in enumerate(insts):
         if mn.startswith(("s_cbranch", "s_branch")) and target is not None and target <= addr and target in index:
-            spans.add((index[target], i))
+            a = index[target]
+            if not any(a <= e < i for e in ends):
+                spans.add((a, i))
     return sorted(spans)
 
 
@@ -236,9 +241,21 @@ def approx_ops(insts):
 
 def hot_loop(insts, weight_bytes_per_load=None):
     """The kernel's hot loop: among its loops, the one with the most weight loads (128-bit) and then VALU work;
-    -> (first, last, counts) or None."""
+    -> (first, last, counts) or None.  A kernel with no loop after its last barrier (the lean kernels' single-pass
+    form, whose weight stream after the staged activations are published is straight-line code) reports that stream
+    instead, up to the end of the kernel, with the kernel's 128-bit buffer loads (its weight loads) as its loads."""
+    spans = loops(insts)
+    bars = [i for i, (_, mn, _, _) in enumerate(insts) if mn.startswith("s_barrier")]
+    ends = [i for i, (_, mn, _, _) in enumerate(insts) if mn.startswith("s_endpgm")]
+    if bars and any(e > bars[-1] for e in ends):
+        last = min(e for e in ends if e > bars[-1])
+        if not any(bars[-1] <= a <= last for a, _ in spans):
+            c = mix(insts, bars[-1], last)
+            if c.get("dot4", 0) or c.get("mfma", 0):
+                c["ld128"] = sum(mn.startswith("buffer_load_dwordx4") for _, mn, _, _ in insts)
+                return bars[-1], last, c
     best = None
-    for a, b in loops(insts):
+    for a, b in spans:
         c = mix(insts, a, b)
         key = (c.get("ld128", 0), c.get("valu", 0) + c.get("dot4", 0) + c.get("mfma", 0))
         if best is None or key > best[0]:
