@@ -169,12 +169,14 @@ q4_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
     if constexpr (FUSED) stage_fused(tid, xf);
     else stage_q8(tid, xa, xb, xdv);
   }
-  for (int i = tid + nthreads; i < nstage; i += nthreads) {  // columns longer than one pass of the workgroup
-    if constexpr (FUSED) {
-      stage_fused(i, *reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 4));
-    } else {
-      const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 32);
-      stage_q8(i, src[0], src[1], XD[i]);
+  if (__builtin_expect(nstage > nthreads, 0)) {  // columns longer than one pass of the workgroup (out of line)
+    for (int i = tid + nthreads; i < nstage; i += nthreads) {
+      if constexpr (FUSED) {
+        stage_fused(i, *reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 4));
+      } else {
+        const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 32);
+        stage_q8(i, src[0], src[1], XD[i]);
+      }
     }
   }
   for (int i = tid; i < MC * (nblk_pad - nblk); i += nthreads) {

@@ -31,16 +31,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// The crumb masks, held in SGPRs: each masking AND is then a 4-byte instruction instead of an 8-byte one carrying a
+// literal.  A launch runs from a cold instruction cache, where the weight stream's code bytes cost fetch time.
+struct CrumbMasks {
+  unsigned m1, m4, m16;
+};
+__device__ __forceinline__ CrumbMasks crumb_masks() {
+  CrumbMasks k;
+  asm("s_mov_b32 %0, 0x03030303" : "=s"(k.m1));
+  asm("s_mov_b32 %0, 0x0c0c0c0c" : "=s"(k.m4));
+  asm("s_mov_b32 %0, 0x30303030" : "=s"(k.m16));
+  return k;
+}
+
 // The partial int32 dot of one 16-byte chunk with its four 16-byte activation pieces (piece j pairs with the crumbs
 // at bits 2j): three accumulators for the crumbs masked in place (x1, x4, x16) and one shift for the fourth.
-__device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], int init) {
+__device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], int init, const CrumbMasks& k) {
   int a1 = init, a4 = 0, a16 = 0;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    a1 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x03030303u), static_cast<int>(x[0][d]), a1, false);
-    a4 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x0C0C0C0Cu), static_cast<int>(x[1][d]), a4, false);
-    a16 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & 0x30303030u), static_cast<int>(x[2][d]), a16, false);
-    a16 = __builtin_amdgcn_sdot4(static_cast<int>((w[d] >> 2) & 0x30303030u), static_cast<int>(x[3][d]), a16, false);
+    a1 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m1), static_cast<int>(x[0][d]), a1, false);
+    a4 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m4), static_cast<int>(x[1][d]), a4, false);
+    a16 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m16), static_cast<int>(x[2][d]), a16, false);
+    a16 = __builtin_amdgcn_sdot4(static_cast<int>((w[d] >> 2) & k.m16), static_cast<int>(x[3][d]), a16, false);
   }
   return ((a1 << 4) + (a4 << 2) + a16) >> 4;
 }
@@ -186,19 +199,22 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
     }
   };
   if (stg) stage_one(tid, xf, x16, xdv);
-  for (int i = tid + nthreads; i < nstage; i += nthreads) {  // columns of more than 16 values per thread
-    f32x4 v[4];
-    u32x4 xq16;
-    float dxv = 0.0f;
-    if constexpr (FUSED) {
-      const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 16);
+  // columns of more than 16 values per thread (none at the decode shapes: the loop sits out of line)
+  if (__builtin_expect(nstage > nthreads, 0)) {
+    for (int i = tid + nthreads; i < nstage; i += nthreads) {
+      f32x4 v[4];
+      u32x4 xq16;
+      float dxv = 0.0f;
+      if constexpr (FUSED) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 16);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = src[t];
-    } else {
-      xq16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 16);
-      if ((i & 15) == 0) dxv = XD[i >> 4];
+        for (int t = 0; t < 4; ++t) v[t] = src[t];
+      } else {
+        xq16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 16);
+        if ((i & 15) == 0) dxv = XD[i >> 4];
+      }
+      stage_one(i, v, xq16, dxv);
     }
-    stage_one(i, v, xq16, dxv);
   }
   for (int i = tid; i < MC * (nblk_pad - nblk); i += nthreads) {
     const int m = i / (nblk_pad - nblk);
@@ -216,6 +232,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
   const int2* ml = meta + gblk;
   const int qmask = q == 0 ? -1 : 0;  // the block's -sum(x) joins one lane of the quad
+  const CrumbMasks km = crumb_masks();
   for (int p = 0; p < npass; ++p) {
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
@@ -236,7 +253,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[tb + u * BPG];
-          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
+          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask, km), 4);  // the block's exact dot, in every lane
           if (__builtin_expect(S != nullptr, 0)) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
@@ -254,7 +271,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
           const int2 mt = ml[bo];
-          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask), 4);  // the block's exact dot, in every lane
+          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask, km), 4);  // the block's exact dot, in every lane
           if (__builtin_expect(S != nullptr, 0)) {
             const int b = tb + u * BPG + gblk;
             if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;

@@ -150,6 +150,19 @@ __device__ __forceinline__ int row16_max_i(int v) {
   return max(v, dpp_i<KOMP_DPP_MIRROR>(v));
 }
 
+// The max of `hi` and the min of `lo` over each aligned 16-lane row, the two reductions interleaved step by step so
+// that neither waits on its own previous DPP result.
+__device__ __forceinline__ void row16_max_min_i(int& hi, int& lo) {
+  hi = max(hi, dpp_i<KOMP_DPP_XOR1>(hi));
+  lo = min(lo, dpp_i<KOMP_DPP_XOR1>(lo));
+  hi = max(hi, dpp_i<KOMP_DPP_XOR2>(hi));
+  lo = min(lo, dpp_i<KOMP_DPP_XOR2>(lo));
+  hi = max(hi, dpp_i<KOMP_DPP_HALF_MIRROR>(hi));
+  lo = min(lo, dpp_i<KOMP_DPP_HALF_MIRROR>(lo));
+  hi = max(hi, dpp_i<KOMP_DPP_MIRROR>(hi));
+  lo = min(lo, dpp_i<KOMP_DPP_MIRROR>(lo));
+}
+
 // f32 bits -> int32 whose signed order is the float order (-0 just below +0); the map is its own inverse.  Row
 // reductions of floats run on these keys because integer max/min fold into single DPP instructions, while float ones
 // need NaN-quieting moves around every DPP step.
@@ -170,18 +183,20 @@ __device__ __forceinline__ int f32_order_key(int bits) { return bits ^ ((bits >>
 // mode, exactly as round_half_even does, and the low byte of the sum's bits is that integer's two's-complement byte.
 __device__ __forceinline__ int q8_K_row16(const f32x4 (&v)[4], int r, u32x4& qout, float& d_out, int& qsum) {
 #pragma clang fp contract(off)
-  // three-operand chains (v_max3 / v_min3), which take the loaded values as they are
-  float hi = fmaxf(fmaxf(v[0][0], v[0][1]), v[0][2]);
-  float lo = fminf(fminf(v[0][0], v[0][1]), v[0][2]);
+  // three-operand trees (v_max3 / v_min3, depth 3 rather than a chain of 8), which take the loaded values as they are
+  auto at = [&](int i) { return v[i >> 2][i & 3]; };
+  float hp[5], lp[5];
 #pragma unroll
-  for (int i = 3; i < 15; i += 2) {
-    hi = fmaxf(fmaxf(hi, v[i >> 2][i & 3]), v[(i + 1) >> 2][(i + 1) & 3]);
-    lo = fminf(fminf(lo, v[i >> 2][i & 3]), v[(i + 1) >> 2][(i + 1) & 3]);
+  for (int i = 0; i < 5; ++i) {
+    hp[i] = fmaxf(fmaxf(at(3 * i), at(3 * i + 1)), at(3 * i + 2));
+    lp[i] = fminf(fminf(at(3 * i), at(3 * i + 1)), at(3 * i + 2));
   }
-  hi = fmaxf(hi, v[3][3]);
-  lo = fminf(lo, v[3][3]);
-  hi = __int_as_float(f32_order_key(row16_max_i(f32_order_key(__float_as_int(hi)))));
-  lo = __int_as_float(f32_order_key(row16_min_i(f32_order_key(__float_as_int(lo)))));
+  float hi = fmaxf(fmaxf(fmaxf(hp[0], hp[1]), hp[2]), fmaxf(fmaxf(hp[3], hp[4]), at(15)));
+  float lo = fminf(fminf(fminf(lp[0], lp[1]), lp[2]), fminf(fminf(lp[3], lp[4]), at(15)));
+  int hk = f32_order_key(__float_as_int(hi)), lk = f32_order_key(__float_as_int(lo));
+  row16_max_min_i(hk, lk);
+  hi = __int_as_float(f32_order_key(hk));
+  lo = __int_as_float(f32_order_key(lk));
   float mx = hi >= -lo ? hi : lo;
   const bool tie = hi == -lo && hi != 0.0f;
   if (__builtin_expect(__ballot(tie) != 0, 0)) {
@@ -196,7 +211,12 @@ __device__ __forceinline__ int q8_K_row16(const f32x4 (&v)[4], int r, u32x4& qou
   }
   const bool nz = mx != 0.0f;
   const float iscale = -127.0f / (nz ? mx : 1.0f);  // an all-zero block gives q = 0 through the same arithmetic
-  constexpr float kRound = 12582912.0f;             // 1.5 * 2^23
+  // 1.5 * 2^23 and the all-ones bytes in SGPRs: the 16 adds and 4 dots are then 4-byte instructions rather than
+  // 8-byte ones carrying a literal (the fused GEMVs run this code from a cold instruction cache)
+  float kRound;
+  int ones;
+  asm("s_mov_b32 %0, 0x4b400000" : "=s"(kRound));  // 12582912.0f
+  asm("s_mov_b32 %0, 0x01010101" : "=s"(ones));
   int s16 = 0;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -206,7 +226,7 @@ __device__ __forceinline__ int q8_K_row16(const f32x4 (&v)[4], int r, u32x4& qou
     const unsigned p01 = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);  // bytes {b0, b1, 0, 0}
     const unsigned p23 = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
     qout[t] = p01 | (p23 << 16);
-    s16 = __builtin_amdgcn_sdot4(static_cast<int>(qout[t]), 0x01010101, s16, false);
+    s16 = __builtin_amdgcn_sdot4(static_cast<int>(qout[t]), ones, s16, false);
   }
   qsum = group_sum(s16, 16);
   d_out = nz ? 1.0f / iscale : 0.0f;

@@ -159,15 +159,37 @@ def test_auto_plan(fmt, n, k, fused):
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])
 def test_auto_plan_other_modes_and_columns_use_knob_sets(mode, m):
     for fmt, n, k in ((0, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912)):
+        if fmt == 1 and mode == 2:
+            continue  # TQ2_0 in dp4a mode: one workgroup per CU at 1-3 columns (test_auto_plan_bitnet_shapes)
         for fused in (False, True):
             bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, m, n, k, fused, mode)
             assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and lanes == 64 // min(bn // nw, 16)
 
 
-def test_auto_plan_bitnet_shapes():
-    # the headline shapes: one workgroup per CU (256 CUs), fused and unfused alike
-    assert _abi.auto_plan(1, 1, 2560, 6912, True) == _abi.auto_plan(1, 1, 2560, 6912, False) == (10, 2, 10, 64, 1)
-    assert _abi.auto_plan(1, 1, 6912, 2560, True) == _abi.auto_plan(1, 1, 6912, 2560, False) == (27, 4, 7, 16, 1)
+@pytest.mark.parametrize("m,w1,w2", [(1, (27, 4, 7, 16, 1), (10, 2, 10, 64, 1)),
+                                     (2, (27, 4, 7, 16, 1), (10, 2, 10, 64, 1)),
+                                     # 3 x 10 blocks x 16 = 480 staging threads: 8 waves of 4 rows, one staging pass
+                                     (3, (32, 4, 8, 16, 1), (10, 2, 10, 64, 1))])
+def test_auto_plan_bitnet_shapes(m, w1, w2):
+    # the BitNet-2B shapes, 1-3 columns: one workgroup per CU (256 CUs), fused and unfused alike
+    assert _abi.auto_plan(1, m, 6912, 2560, True) == _abi.auto_plan(1, m, 6912, 2560, False) == w1
+    assert _abi.auto_plan(1, m, 2560, 6912, True) == _abi.auto_plan(1, m, 2560, 6912, False) == w2
+
+
+def test_auto_plan_tq2_columns_few_rows_use_knob_sets():
+    # 2-3 columns need at least 7 waves of the one-workgroup-per-CU plan; fewer rows take the 8-wave knob-set plans
+    for n, k in ((127, 2816), (4097, 2816)):
+        for m in (2, 3):
+            bn, nb, nw, lanes, passes = _abi.auto_plan(1, m, n, k, True)
+            assert bn in (8, 16, 32, 64, 128) and nw == 8 and lanes == 64 // min(bn // nw, 16)
+    assert _abi.auto_plan(1, 3, 6913, 2816, True)[2] == 7  # 28 rows per CU: 7 waves of 4 rows
+
+
+def test_auto_plan_tq2_columns_fall_back_when_the_lean_kernel_cannot_take_them():
+    # a row of 256 blocks at 3 columns needs more than 160 KB of staged activations: the 8-wave knob-set plan, which
+    # the general kernel runs
+    bn, nb, nw, lanes, passes = _abi.auto_plan(1, 3, 4096, 65536, True)
+    assert nw <= 8 and bn in (8, 16, 32, 64, 128) and lanes == 64 // min(bn // nw, 16)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
