@@ -65,13 +65,14 @@ TimingState g_timing;
 //   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): nb 4, 8 waves, 16 lanes per row, or 8
 //   (8 rows per wave, K in steps of 8 blocks) from 128 chunks per row: 8% faster than nb 2 at 32768 x 8192 and
 //   16384 x 2816.
-//   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode, fused launches of one column
-//   and TQ2_0 with 1-3 columns: one workgroup per CU with ceil(N / CUs) rows, one row group per wave, one K step.  A grid of at most
+//   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode, fused launches of one column,
+//   TQ2_0 with 1-3 columns and Q4_0 with 2-3: one workgroup per CU with ceil(N / CUs) rows, one row group per wave,
+//   one K step where nb allows.  A grid of at most
 //   one workgroup per CU is spread one to a CU, so no CU stages (and, fused, quantizes) the activations twice or runs
 //   two workgroups' dots on the same SIMDs; 9-24% faster at the BitNet-2B and Llama-3-8B shapes than 8-wave
 //   workgroups of 8-16 rows.  Lanes per row start at 64 and halve while the rows would need more than 16 waves or a
 //   lane would get fewer than 1.5 of the row's 16-byte chunks.
-//   Otherwise (unfused Q4_0, other modes, 2-3 columns of the other formats): 8 waves per workgroup, as many lanes per row as the row has
+//   Otherwise (one unfused Q4_0 column, other modes, 2-3 columns of the other formats): 8 waves per workgroup, as many lanes per row as the row has
 //   16-byte chunks (at most 64; the fused launch halves that, since every workgroup pays for quantizing the input),
 //   and nb just large enough for one K step (Q4_0 caps it at 4), because each extra step adds a full HBM round trip to
 //   a wave's critical path.
@@ -124,7 +125,7 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
     return plan_of(4 * (64 / lpr) * 2, nb, 4, lpr, 2);  // 4 waves, two passes each
   }
-  if (mode == KOMP_MODE_DP4A && ((m == 1 && fused) || (fmt == FMT_TQ2_0 && m <= 3))) {
+  if (mode == KOMP_MODE_DP4A && m <= 3 && (fmt == FMT_TQ2_0 || (m == 1 && fused) || (fmt == FMT_Q4_0 && m > 1))) {
     const int cus = device_cus();
     const int64_t rows = n < 1 ? 1 : (n + cus - 1) / cus;
     const int lpr_min = bpb > 4 ? bpb : 4;  // a row group holds whole blocks
@@ -143,7 +144,9 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       wg_rows = waves * rpp;  // fewer, fuller workgroups
     }
     // two or three columns only with two waves on most SIMDs: with fewer, the 8-wave plans below, two workgroups
-    // a CU, stage and dot faster (4097 x 2816, 3 columns: 4.16 against 4.32 us; 127 x 2816: 3.0 against 4.8)
+    // a CU, stage and dot faster (TQ2_0 4097 x 2816, 3 columns: 4.16 against 4.32 us; 127 x 2816: 3.0 against 4.8).
+    // Q4_0 at Llama-3-8B shapes, 2-3 columns: 8-36% faster than those plans, the fused launches most (4096 x 14336,
+    // 3 columns: 15.8 against 24.7 us fused, 9.3 against 10.2 with q8 in).
     if (waves <= 16 && (m == 1 || waves >= 7)) {
       const int64_t blocks_per_slot = lpr / bpb;
       // the 16-wave instantiations: nb up to 8 for one column, 4 for two and three (Q4_K: 4, 4 VGPRs of scales per
@@ -151,9 +154,10 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       const int nb_max = fmt == FMT_Q4_K || m > 1 ? 4 : 8;
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
       nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
-      // two or three columns run this plan on the lean kernel only (the general kernel takes at most 8 waves there)
-      if (m == 1 || waves <= 8 ||
-          tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k)) <= kLdsMax)
+      // two or three columns run this plan on the lean kernels only (the general kernel takes at most 8 waves there)
+      const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k))
+                                               : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k));
+      if (m == 1 || waves <= 8 || lean_lds <= kLdsMax)
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);
     }
   }

@@ -159,8 +159,8 @@ def test_auto_plan(fmt, n, k, fused):
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])
 def test_auto_plan_other_modes_and_columns_use_knob_sets(mode, m):
     for fmt, n, k in ((0, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912)):
-        if fmt == 1 and mode == 2:
-            continue  # TQ2_0 in dp4a mode: one workgroup per CU at 1-3 columns (test_auto_plan_bitnet_shapes)
+        if mode == 2 and (fmt == 1 or m > 1):
+            continue  # one workgroup per CU: TQ2_0 at 1-3 columns, Q4_0 at 2-3 (the tests below)
         for fused in (False, True):
             bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, m, n, k, fused, mode)
             assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and lanes == 64 // min(bn // nw, 16)
@@ -174,6 +174,14 @@ def test_auto_plan_bitnet_shapes(m, w1, w2):
     # the BitNet-2B shapes, 1-3 columns: one workgroup per CU (256 CUs), fused and unfused alike
     assert _abi.auto_plan(1, m, 6912, 2560, True) == _abi.auto_plan(1, m, 6912, 2560, False) == w1
     assert _abi.auto_plan(1, m, 2560, 6912, True) == _abi.auto_plan(1, m, 2560, 6912, False) == w2
+
+
+@pytest.mark.parametrize("n,k,plan", [(4096, 4096, (16, 2, 16, 64, 1)), (6144, 4096, (24, 4, 12, 32, 1)),
+                                      (4096, 14336, (16, 4, 16, 64, 1))])  # nb 4 at most for 2-3 columns
+def test_auto_plan_q4_0_columns_llama_shapes(n, k, plan):
+    for m in (2, 3):
+        assert _abi.auto_plan(0, m, n, k, True) == _abi.auto_plan(0, m, n, k, False) == plan
+    assert _abi.auto_plan(0, 1, n, k, False)[2] == 8  # one unfused column keeps the 8-wave plan
 
 
 def test_auto_plan_tq2_columns_few_rows_use_knob_sets():
