@@ -247,12 +247,23 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
   GemmPlan q = {8, 1, 1, cn, 2};
   if (r > 8.0)
     q = cn == 1 ? GemmPlan{1, 8, m > 8 && fmt != FMT_Q8_0 ? 2 : 1, 1, 2} : GemmPlan{1, 8, 1, cn, cn == 2 ? 2 : 1};
+  else if (r > 2.0 && cn == 1)
+    q = GemmPlan{4, 2, 2, 1, 4};
+  else if (r > 2.0 && fmt == FMT_Q8_0)  // Q8_0's two row tiles a wave would need more than 256 VGPRs
+    q = GemmPlan{2, 4, 1, cn, 2};
   else if (r > 2.0)
-    q = cn == 1 ? GemmPlan{4, 2, 2, 1, 4} : GemmPlan{2, 4, 1, cn, 2};
+    // two row tiles a wave: each activation load feeds twice the MFMAs (the activations are re-read for every row
+    // tile, 8x the weight bytes a step at 64 columns); 4 waves from 4 row tiles a CU.  Q4_0 14336 x 4096 at 32 / 48 /
+    // 64 columns: 32.0 / 44.2 / 56.1 -> 23.7 / 30.3 / 37.7 us; 28672 x 4096 at 64: 108 -> 67 us; TQ2_0 14336 x 4096
+    // at 64: 44.6 -> 27.2 us
+    q = r > 4.0 ? GemmPlan{2, 2, 2, cn, 2} : GemmPlan{4, 2, 2, cn, 2};
   else if (r > 1.25 && cn > 1)
     q = GemmPlan{4, 2, 1, cn, 2};
   while (gemm_lds_bytes(fmt, q, static_cast<int>(k)) > kLdsMax && q.wn * q.wr > 1) {  // long rows: fewer rows a group
-    if (q.wn > 1) q.wn = 1; else q = GemmPlan{8, 1, 1, cn, 2};
+    if (q.wn > 1 && (q.wk == 1 || (q.wk == 4 && q.cn > 1)))
+      q.wn = 1;  // (1, 8, 2, 1, 2) -> (1, 8, 1, 1, 2); (4, 2, 2, cn, 2) -> (4, 2, 1, cn, 2)
+    else
+      q = GemmPlan{8, 1, 1, cn, 2};
   }
   *p = q;
   return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;

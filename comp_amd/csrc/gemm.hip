@@ -555,6 +555,14 @@ hipError_t launch_fmt(const GemmCall& c, const GemmPlan& p, hipStream_t stream) 
   KOMP_GEMM_PLAN(1, 8, 1, 2, 2)
   KOMP_GEMM_PLAN(1, 8, 1, 3, 1)
   KOMP_GEMM_PLAN(1, 8, 1, 4, 1)
+  if constexpr (FMT != FMT_Q8_0) {  // two row tiles a wave with 2-4 column tiles (208 VGPRs at 4)
+    KOMP_GEMM_PLAN(4, 2, 2, 2, 2)
+    KOMP_GEMM_PLAN(4, 2, 2, 3, 2)
+    KOMP_GEMM_PLAN(4, 2, 2, 4, 2)
+    KOMP_GEMM_PLAN(2, 2, 2, 2, 2)
+    KOMP_GEMM_PLAN(2, 2, 2, 3, 2)
+    KOMP_GEMM_PLAN(2, 2, 2, 4, 2)
+  }
 #undef KOMP_GEMM_PLAN
   return hipErrorInvalidConfiguration;
 }

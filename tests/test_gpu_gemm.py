@@ -71,7 +71,8 @@ FAMILIES = [
     (4000, 512, 20, 16, 32),    # ~1 row tile per CU: K split over 8 waves
     (6144, 512, 20, 32, 32),    # 1.5 per CU, 2 column tiles: 4 x 2 waves
     (9600 + 7, 512, 12, 64, 16),  # 2..8 per CU, 1 column tile: 4 x 2 waves, 2 row tiles each
-    (9600, 256, 20, 64, 32),    # 2..8 per CU, 2 column tiles: 2 x 4 waves
+    (9600, 256, 20, 64, 32),    # 2..4 per CU, 2 column tiles: 4 x 2 waves, 2 row tiles each (Q8_0: 2 x 4 waves)
+    (20000 + 3, 256, 40, 64, 48),  # 4..8 per CU, 3 column tiles: 2 x 2 waves, 2 row tiles each (Q8_0: 2 x 4)
     (33600, 256, 4, 128, 16),   # > 8 per CU: 8 waves, each its own rows
     (33600 - 5, 256, 12, 256, 16),  # ... 2 row tiles each
     (16400, 256, 70, 128, 48),  # ... 3 column tiles, 2 column groups
