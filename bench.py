@@ -306,12 +306,16 @@ def headline(torch, host, abi, args):
 
 def cpu_baseline(args, step_bytes_m, seconds=10.0):
     """The C restatement of the reference path (oracle/oracle.c: ggml's q8_K quantizer, int32 block dots, f32 scale
-    and accumulate in block order), one thread, on whole steps of the same chain."""
+    and accumulate in block order) on whole steps of the same chain, each GEMV's rows split evenly over
+    args.cpu_threads host threads (the C calls run outside the GIL); the chain's order is kept, as in a decode."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
 
     from oracle import coracle as C
     from oracle import oracle as O
 
+    threads = max(1, args.cpu_threads or min(16, len(os.sched_getaffinity(0))))
     rng = np.random.default_rng(args.seed)
     m = args.m
     mats = []
@@ -323,22 +327,39 @@ def cpu_baseline(args, step_bytes_m, seconds=10.0):
         mats.append((n, k, wq, ws))
     x0 = rng.normal(size=(m, 2560)).astype(np.float32)
     C.lib()
+    pool = ThreadPoolExecutor(threads)
+
+    def gemv(n, k, wq, ws, xq, xd):
+        cuts = [n * t // threads for t in range(threads + 1)]
+        parts = pool.map(lambda t: C.gemv_f32("tq2_0", wq[cuts[t]:cuts[t + 1]], ws[cuts[t]:cuts[t + 1]], xq, xd,
+                                              cuts[t + 1] - cuts[t], k), range(threads))  # fmt: skip
+        return np.concatenate(list(parts), axis=1)
+
+    # the row-split chain equals the one-thread chain bit for bit (rows are independent)
+    x1 = x2 = x0
+    for n, k, wq, ws in mats:
+        q1, d1, _ = C.quant_q8_K(x1)
+        q2, d2, _ = C.quant_q8_K(x2)
+        x1, x2 = C.gemv_f32("tq2_0", wq, ws, q1, d1, n, k), gemv(n, k, wq, ws, q2, d2)
+    assert np.array_equal(x1, x2), "row-split CPU chain differs from the one-thread chain"
     steps = 0
     t0 = time.perf_counter()
     while True:
         x = x0
         for n, k, wq, ws in mats:
             xq, xd, _ = C.quant_q8_K(x)
-            x = C.gemv_f32("tq2_0", wq, ws, xq, xd, n, k)
+            x = gemv(n, k, wq, ws, xq, xd)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
+    pool.shutdown()
     value = step_bytes_m * steps / el / 1e9
-    return {"value": round(value, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{steps} whole steps of the same chain (m={m}, both matrices) through the C oracle "
                       f"(oracle/oracle.c: quant_q8_K, int32 block dots, f32 block-order accumulation), gcc -O2, "
-                      f"1 thread, {el:.1f} s; host has {len(os.sched_getaffinity(0))} cores"}  # fmt: skip
+                      f"each GEMV's rows split over {threads} threads, {el:.1f} s; host has "
+                      f"{len(os.sched_getaffinity(0))} cores"}  # fmt: skip
 
 
 DETAIL_SHAPES = (  # (fmt, n, k, m)
@@ -684,6 +705,8 @@ def main():
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="host threads for cpu_baseline (default: the usable cores, at most 16)")
     ap.add_argument("--batched-only", action="store_true",
                     help="only run the batched_gemm block (for profiling the GEMM by itself)")
     ap.add_argument("--batched-calls", type=int, default=0, metavar="N",

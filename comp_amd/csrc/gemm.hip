@@ -9,7 +9,8 @@
 // a K step is 64 contiguous bytes of each weight row (4 Q4_0 blocks or 1 TQ2_0 block) and wave w takes steps
 // w, w + W, w + 2W, ...; at the end the waves add their f32 partials in wave order.  Lane (r, g) (r = lane % 16,
 // g = lane / 16) loads bytes 16g..16g+15 of a step for row r, so one load instruction reads 64 bytes of each of 16
-// rows.  Each wave keeps D steps of loads in flight (a register ring).  Loads go through buffer descriptors whose
+// rows.  Each wave keeps D steps of activation loads and DW >= D steps of weight loads in flight (register rings;
+// the step loop has no branch, so each step waits for its own loads only).  Loads go through buffer descriptors whose
 // range ends at the tile's last valid row / column, with the whole offset of a load in its per-lane offset (no scalar
 // offset): a load past the range (a block past K in the tile's last row, every load of a step past the wave's last)
 // returns zeros without touching memory.
@@ -158,18 +159,24 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
     vd[u] = static_cast<unsigned>(c * nblk * 4 + (NIB4 ? 4 * g : (Q8 ? 4 * (g & 1) : 0)));
   }
 
-  struct Step {
+  struct WStep {  // a K step's weight loads
     u32x4 a[WN];
+  };
+  struct Step {  // a K step's activation loads
     u32x4 x[CN][XV];
     float dx[CN];  // 32-value blocks: d_x of row group g's block of the step; TQ2_0: d_x of block s; Q4_K: s / 2
   };
+  auto load_w = [&](WStep& w, int s) {
+    const unsigned sa = s < nsteps ? 64u * s : kOob;  // wave-uniform
+#pragma unroll
+    for (int t = 0; t < WN; ++t) w.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t] + sa, 0, 2);  // nt: read once
+  };
   auto load = [&](Step& st, int s) {
     const bool sv = s < nsteps;  // wave-uniform
-    const unsigned sa = sv ? 64u * s : kOob;
     const unsigned sx = sv ? (QK ? 128u : 32u * BPS * (TQ2 ? 8u : 1u)) * s : kOob;  // activation bytes per step
-    const unsigned sd = sv ? (QK ? 4u * (s >> 1) : 4u * BPS * s) : kOob;
-#pragma unroll
-    for (int t = 0; t < WN; ++t) st.a[t] = __builtin_amdgcn_raw_buffer_load_b128(wq, va[t] + sa, 0, 2);  // nt: read once
+    // d_x: 32-value blocks past K (the lanes of a partial last step) load zero, so such a block adds exact zeros
+    const unsigned sd = !sv || (BLK32 && BPS * s + (NIB4 ? g : (g & 1)) >= nblk)
+                            ? kOob : (QK ? 4u * (s >> 1) : 4u * BPS * s);  // fmt: skip
 #pragma unroll
     for (int u = 0; u < CN; ++u) {
 #pragma unroll
@@ -241,9 +248,27 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   auto step_of = [&](int i) { return QK ? 2 * (wk + WK * (i >> 1)) + (i & 1) : wk + WK * i; };
   const int my = QK ? 2 * (nblk > wk ? (nblk - wk + WK - 1) / WK : 0)
                     : (nsteps > wk ? (nsteps - wk + WK - 1) / WK : 0);  // this wave's steps (wave-uniform)
+  // Two rings: the activations (L2 hits) D steps ahead, the weights (HBM) DW steps ahead.  After step i's compute the
+  // wave loads step i + D's activations, then step i + DW's weights.  DW = 2D for TQ2_0's 8-wave plans with one row
+  // tile a wave (with two, the extra registers spill), whose steps (4 crumb MFMAs per tile, 16 activation loads)
+  // leave the weights' HBM latency exposed at D (TQ2_0 6912 x 2560 at 64 columns: 18.2 -> 15.1 us); elsewhere the
+  // deeper weight ring measured no faster (Q4_0 14336 x 4096 at 64 columns) or slower (at 4 and 16 columns).  The
+  // first loads go out after the slab's, in the order the step loop
+  // keeps (weights of steps 0..DW-D-1, then activations of step d with weights of step DW-D+d), so the compiler's wait
+  // counts at the loop's head see the same order on entry as on the back edge: each step waits for its own loads.
+  constexpr int DW = (TQ2 && WK * WR == 8 && WN == 1) ? 2 * D : D;
+  WStep wring[DW];
   Step ring[D];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < D; ++d) load(ring[d], step_of(d));  // past the wave's steps: zeros
+  for (int d = 0; d < DW - D; ++d) load_w(wring[d], step_of(d));  // past the wave's steps: zeros
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load(ring[d], step_of(d));
+    load_w(wring[DW - D + d], step_of(DW - D + d));
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   if constexpr (QK) {
     qk_slab_store(0);
@@ -282,7 +307,7 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
     }
   };
 
-  auto compute = [&](const Step& st, int s) {
+  auto compute = [&](const WStep& wt, const Step& st, int s) {
     if constexpr (QK) {
       // Q4_K step s = half s % 2 of block s / 2: 64 quant bytes = 32-byte groups j = 2 (s % 2) + {0, 1}, each the
       // low nibbles of sub-block 2j and the high nibbles of sub-block 2j + 1.  After the transpose ta[t][p] (row
@@ -291,7 +316,7 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
       // odd: the slots of Q4_0's block i, whose B operand the activation loads give unchanged.
       unsigned ta[WN][4], xt[CN][XV][4];
 #pragma unroll
-      for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
+      for (int t = 0; t < WN; ++t) transpose4(wt.a[t], ta[t]);
 #pragma unroll
       for (int u = 0; u < CN; ++u)
 #pragma unroll
@@ -364,7 +389,7 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
       unsigned ta[WN][4], xt[CN][XV][4];
       float dxb[CN][4];
 #pragma unroll
-      for (int t = 0; t < WN; ++t) transpose4(st.a[t], ta[t]);
+      for (int t = 0; t < WN; ++t) transpose4(wt.a[t], ta[t]);
 #pragma unroll
       for (int u = 0; u < CN; ++u) {
 #pragma unroll
@@ -390,7 +415,8 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
 #pragma unroll
       for (int j = 0; j < BPS; ++j) {
         const int b = BPS * s + j;
-        if (b >= nblk) break;  // wave-uniform: the step's last blocks past K
+        // the step's last blocks past K (wave-uniform): their d_x is zero, so only S needs the branch
+        if (STORE_S && b >= nblk) break;
         long bj[CN];
         i32x4 corr[CN];
 #pragma unroll
@@ -442,7 +468,7 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
         i32x4 aj[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const u32x4 cr = (st.a[t] >> (2u * v)) & CRUMB;
+          const u32x4 cr = (wt.a[t] >> (2u * v)) & CRUMB;
           aj[v] = reinterpret_cast<const i32x4&>(cr);
         }
 #pragma unroll
@@ -461,13 +487,40 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
     }
   };
 
-  for (int i0 = 0; i0 < my; i0 += D) {
+  // Whole groups of DW steps run with no wave-uniform branch in the loop (a branch there makes the compiler's wait
+  // counts conservative: a step would wait for the next steps' loads too); the last my % DW steps follow, unrolled.
+  // With S (whose stores branch anyway) every step is guarded instead.
+  if constexpr (!STORE_S) {
+    int i0 = 0;
+    for (; i0 + DW <= my; i0 += DW) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int i = i0 + d;
+      for (int d = 0; d < DW; ++d) {
+        const int i = i0 + d;
+        compute(wring[d], ring[d % D], step_of(i));
+        __builtin_amdgcn_sched_barrier(0);  // slot order kept: the other slots' loads stay in flight meanwhile
+        load(ring[d % D], i + D < my ? step_of(i + D) : nsteps);  // past the wave's last step: zeros, no traffic
+        load_w(wring[d], i + DW < my ? step_of(i + DW) : nsteps);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < ((QK && DW <= 2) ? 0 : DW - 1); ++d) {  // the tail (Q4_K: none, its step count is even)
+      const int i = i0 + d;  // every weight load of the tail is in flight already
       if (i < my) {
-        compute(ring[d], step_of(i));
-        load(ring[d], i + D < my ? step_of(i + D) : nsteps);  // past the wave's last step: zeros, no traffic
+        compute(wring[d], ring[d % D], step_of(i));
+        if (d < DW - D && i + D < my) load(ring[d % D], step_of(i + D));
+      }
+    }
+  } else {
+    for (int i0 = 0; i0 < my; i0 += DW) {
+#pragma unroll
+      for (int d = 0; d < DW; ++d) {
+        const int i = i0 + d;
+        if (i < my) {
+          compute(wring[d], ring[d % D], step_of(i));
+          load(ring[d % D], i + D < my ? step_of(i + D) : nsteps);
+          load_w(wring[d], i + DW < my ? step_of(i + DW) : nsteps);
+        }
       }
     }
   }

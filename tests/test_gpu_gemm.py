@@ -43,10 +43,15 @@ def check(fmt, n, k, m, seed, extreme=False, ws_offset=0, pad=0):
     else:
         ws_d = dev(ws)
     print(f"gemm {fmt} n={n} k={k} m={m} seed={seed} extreme={extreme} ws_offset={ws_offset} pad={pad}", flush=True)
-    y, s = host.gemm(fmt, wq_d, ws_d, dev(rq), dev(rd), n, k, store_s=True)
+    xq_d, xd_d = dev(rq), dev(rd)
+    y, s = host.gemm(fmt, wq_d, ws_d, xq_d, xd_d, n, k, store_s=True)
+    # the kernel without S (its own instantiation: blocks past K and slots past a wave's last step add exact zeros
+    # where the S kernel branches) gives the same Y bit for bit
+    y_plain, _ = host.gemm(fmt, wq_d, ws_d, xq_d, xd_d, n, k)
     torch.cuda.synchronize()
     assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
     assert outputs_ok(fmt, y.cpu().numpy(), ws, rd, rs, r)
+    assert torch.equal(y_plain, y)
     return y
 
 
