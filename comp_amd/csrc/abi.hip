@@ -62,9 +62,10 @@ TimingState g_timing;
 //   row x nb x 16 bytes covers it) and each wave walks two rows in sequence, nb 4 (8 past 256 chunks), lanes per row
 //   = chunks / nb within 16..64, 4 waves.  Reading whole rows keeps the DRAM accesses of the grid in long runs: with
 //   every workgroup resident, plans that read each row in 1 KB pieces over several steps ran 5-17% slower at
-//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): nb 4, 8 waves, 16 lanes per row, or 8
-//   (8 rows per wave, K in steps of 8 blocks) from 128 chunks per row: 8% faster than nb 2 at 32768 x 8192 and
-//   16384 x 2816.
+//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): 16 lanes per row (4 rows a wave), nb
+//   4, 8 waves, 32 rows a workgroup at every row length: 8% faster than nb 2 at 32768 x 8192 and 16384 x 2816.  32
+//   lanes per row with one K step (16 rows a workgroup) was within 3% at 32768 x 8192 and 16384 x 16384 with q8 in
+//   and 5-35% slower fused and at shorter rows (65536 x 2560).
 //   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode, fused launches of one column,
 //   TQ2_0 with 1-3 columns and Q4_0 with 2-3: one workgroup per CU with ceil(N / CUs) rows, one row group per wave,
 //   one K step where nb allows.  A grid of at most
