@@ -58,14 +58,16 @@ TimingState g_timing;
 
 // ---- auto plan ------------------------------------------------------------------------------------------------------
 // The plan gemv uses when block_n == 0.
-//   Throughput regime (N >= 16384 rows, several workgroups per CU).  Q4_0: each row is read in ONE K step (lanes per
-//   row x nb x 16 bytes covers it) and each wave walks two rows in sequence, nb 4 (8 past 256 chunks), lanes per row
-//   = chunks / nb within 16..64, 4 waves.  Reading whole rows keeps the DRAM accesses of the grid in long runs: with
-//   every workgroup resident, plans that read each row in 1 KB pieces over several steps ran 5-17% slower at
-//   Llama-3-8B shapes.  TQ2_0 (whose dot costs ~2.5x the VALU work per byte): 16 lanes per row (4 rows a wave), nb
-//   4, 8 waves, 32 rows a workgroup at every row length: 8% faster than nb 2 at 32768 x 8192 and 16384 x 2816.  32
-//   lanes per row with one K step (16 rows a workgroup) was within 3% at 32768 x 8192 and 16384 x 16384 with q8 in
-//   and 5-35% slower fused and at shorter rows (65536 x 2560).
+//   Throughput regime (N >= 16384 rows, several workgroups per CU; one unfused Q4_0 / IQ4_NL column from 12288).  Each
+//   row is read in ONE K step: the lean kernels then run their single-step form (a straight-line weight stream).
+//   One Q4_0 / IQ4_NL column: nb 4, lanes per row = chunks / 4 within 16..64, 8 rows a workgroup (4 waves of two rows
+//   at 32 lanes, 8 of one at 64); 2-7% faster than the earlier multi-step plans at Llama-3-8B shapes (gate+up 28672 x
+//   4096 11.84 -> 11.37 us, 28672 x 8192 21.4 -> 20.7, IQ4_NL 28672 x 8192 23.4 -> 22.9).  Other Q4_0 launches:
+//   whole rows in one K step, each wave walking two rows in sequence, nb 4 (8 past 256 chunks), lanes per row =
+//   chunks / nb within 16..64, 4 waves; reading whole rows keeps the DRAM accesses of the grid in long runs (plans
+//   that read each row in 1 KB pieces over several steps ran 5-17% slower).  TQ2_0: nb 4 and as many lanes per row
+//   (16..64) as give each lane quad one block per chunk slot, 8 waves: at 32768 x 8192, 32 lanes per row ran 12.0-12.4
+//   us against 16.2 for 16 lanes in two K steps (whose instance needs more than 64 VGPRs, 7 waves a SIMD).
 //   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode, fused launches of one column,
 //   TQ2_0 with 1-3 columns and Q4_0 with 2-3: one workgroup per CU with ceil(N / CUs) rows, one row group per wave,
 //   one K step where nb allows.  A grid of at most
@@ -114,12 +116,27 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   const int bpb = fmt_info(fmt).qbytes / (fmt == FMT_Q4_K ? 32 : 16);  // lane slots per block (Q4_K: 32-byte groups)
   const int64_t nblk = k / fmt_info(fmt).block;
   const int64_t chunks = nblk * bpb;                      // lane slots per row (16-byte chunks; Q4_K 32-byte groups)
+  // one unfused Q4_0 / IQ4_NL column (the lean kernel) over many rows: each row in one K step of nb 4, as few lanes
+  // per row as that allows (16..64), 8 rows a workgroup (4 waves at least); the lean kernel's single-step form
+  const bool lean_q4 = (fmt == FMT_Q4_0 || fmt == FMT_IQ4_NL) && m == 1 && mode == KOMP_MODE_DP4A;
+  if (lean_q4 && !fused && n >= 12288 && chunks <= 256) {
+    int lpr = pow2_ceil((chunks + 3) / 4);
+    lpr = lpr < 16 ? 16 : lpr;
+    const int rpw = 64 / lpr;
+    const int w = 8 / rpw < 4 ? 4 : 8 / rpw;
+    return plan_of(w * rpw, 4, w, lpr, 1);
+  }
   if (n >= 16384) {
-    if (fmt == FMT_TQ2_0)  // 16 lanes per row (4 rows per wave), nb 4, 8 waves: the fastest of a sweep over knob sets
-      return plan_of(32, 4, 8, 16, 1);                      // at 16400-32768 rows x 4096-8192 columns
-    if ((fmt == FMT_Q4_0 || fmt == FMT_IQ4_NL) && m == 1 && mode == KOMP_MODE_DP4A && chunks <= 128)
-      // one column of rows of up to 128 blocks (the lean kernel): 16 lanes per row, nb 2, 8 waves; 3-7%
-      // faster than the rule below at 28672-128256 rows x 4096 columns
+    if (fmt == FMT_TQ2_0) {
+      // nb 4, as many lanes per row as give every row one K step (16..64, lanes of a quad share a block), 8 waves;
+      // the single-step form of the lean kernel
+      int lpr = pow2_ceil(nblk);
+      lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
+      return plan_of(8 * (64 / lpr), 4, 8, lpr, 1);
+    }
+    if (lean_q4 && chunks <= 128)
+      // one fused column of rows of up to 128 blocks: 16 lanes per row, nb 2, 8 waves; 3-7% faster than the rule
+      // below at 28672-128256 rows x 4096 columns
       return plan_of(32, 2, 8, 16, 1);
     const int nb = chunks > 256 ? 8 : 4;
     int lpr = pow2_ceil((chunks + nb - 1) / nb);

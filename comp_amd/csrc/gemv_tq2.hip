@@ -1,7 +1,7 @@
 // TQ2_0 decode GEMV of 1-3 activation columns in dp4a mode (the BitNet decode step), unfused (q8_K in) and fused with
-// the q8_K quantizer.  Same plans, results and S as the general kernel in gemv_kernel.h (kernels.py:97-142 semantics);
-// the lanes per row group, the chunks per lane and the columns are template arguments here, which is what makes it
-// leaner:
+// the q8_K quantizer.  Same plans, block dots and S as the general kernel in gemv_kernel.h (kernels.py:97-142
+// semantics); the lanes per row group, the chunks per lane and the columns are template arguments here, which is what
+// makes it leaner:
 //   * weight and scale loads are buffer loads from loop-invariant per-lane offsets, the tile and chunk offsets being
 //     a scalar and an immediate.  A chunk past the row's last block, and every row past the matrix, reads zeros
 //     without touching memory (the buffer range check), so no load sits behind a branch and the compiler waits for
@@ -9,9 +9,10 @@
 //   * the activation columns lie in LDS in their natural order, 288 bytes per 256-value block (the 32-byte pad puts the
 //     four lane quads of a 16-lane row group on disjoint banks), so a chunk's four 16-byte activation pieces are one
 //     base address plus immediates;
-//   * the lane quad's partial dots are added (two DPP adds) into the block's exact dot, which one lane of the quad
-//     scales as d_x * d_w * f32(s) (kernels.py:141) and accumulates in f32; the row group's lanes are added at the
-//     end, in the general kernel's order, so Y is bit-identical to it;
+//   * the lane quad's partial dots are added (two DPP adds) into the block's exact dot, and each block is scaled once:
+//     chunk slot u of a quad belongs to lane u % 4, which alone loads the block's d_w and meta (d_x, -sum(x)),
+//     completes the dot and scales it as d_x * d_w * f32(s) (kernels.py:141).  The general kernel lets lane 0 scale
+//     every slot, so the lean kernel adds the same terms in another order (Y within the same f32 error bound; S equal);
 //   * the activation loads of the staging are issued before the weight loads, and the barrier that publishes the
 //     staged column waits for LDS writes only, so the weights stay in flight through the staging.
 #include <hip/hip_ext.h>
@@ -44,18 +45,55 @@ __device__ __forceinline__ CrumbMasks crumb_masks() {
   return k;
 }
 
-// The partial int32 dot of one 16-byte chunk with its four 16-byte activation pieces (piece j pairs with the crumbs
-// at bits 2j): three accumulators for the crumbs masked in place (x1, x4, x16) and one shift for the fourth.
-__device__ __forceinline__ int chunk_dot(const u32x4& w, const u32x4 (&x)[4], int init, const CrumbMasks& k) {
-  int a1 = init, a4 = 0, a16 = 0;
+// Sum of the four signed byte products of a and b: v_dot4_i32_i8 with a zero addend, the first dot of a chain (the
+// compiler otherwise clears a register for v_dot4c_i32_i8 to accumulate into).
+__device__ __forceinline__ int dot4_first(unsigned a, unsigned b) {
+  int r;
+  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// 16 x the partial int32 dot of one 16-byte chunk with its four 16-byte activation pieces (piece j pairs with the
+// crumbs at bits 2j): three accumulators for the crumbs masked in place (x1, x4, x16) and one shift for the fourth,
+// joined as (4 * (4 * a1 + a4) + a16) with two shift-adds.  Every term is a multiple of 16.
+__device__ __forceinline__ int chunk_dot16(const u32x4& w, const u32x4 (&x)[4], const CrumbMasks& k) {
+  int a1 = dot4_first(w[0] & k.m1, x[0][0]);
+  int a4 = dot4_first(w[0] & k.m4, x[1][0]);
+  int a16 = dot4_first(w[0] & k.m16, x[2][0]);
+  a16 = __builtin_amdgcn_sdot4(static_cast<int>((w[0] >> 2) & k.m16), static_cast<int>(x[3][0]), a16, false);
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
+  for (int d = 1; d < 4; ++d) {
     a1 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m1), static_cast<int>(x[0][d]), a1, false);
     a4 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m4), static_cast<int>(x[1][d]), a4, false);
     a16 = __builtin_amdgcn_sdot4(static_cast<int>(w[d] & k.m16), static_cast<int>(x[2][d]), a16, false);
     a16 = __builtin_amdgcn_sdot4(static_cast<int>((w[d] >> 2) & k.m16), static_cast<int>(x[3][d]), a16, false);
   }
-  return ((a1 << 4) + (a4 << 2) + a16) >> 4;
+  return (((a1 << 2) + a4) << 2) + a16;
+}
+
+// c ? a : b per lane, as one v_cndmask_b32 on a lane mask in SGPRs.  Written out because the compiler turns a chain
+// of such selects on the lane's quad position into an array indexed by it, which it keeps in scratch memory.
+__device__ __forceinline__ int lane_select(uint64_t c, int a, int b) {
+  int r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(c));
+  return r;
+}
+
+// Reduce-scatter over a lane quad: p0..p3 are the lane's partial dots of four chunk slots; lane q of the quad gets
+// the quad's sum for slot q.  odd / hi: the lanes whose quad position has bit 0 / bit 1 set.  Two exchanges of two
+// values and one of one (three DPP adds, six selects) instead of a full quad sum per slot (eight DPP adds).
+__device__ __forceinline__ int quad_scatter4(int p0, int p1, int p2, int p3, uint64_t odd, uint64_t hi) {
+  // lanes q, q ^ 1: keep the slots whose bit 0 is q's
+  const int t1 = lane_select(odd, p1, p0) + dpp_i<KOMP_DPP_XOR1>(lane_select(odd, p0, p1));  // slot q & 1
+  const int t2 = lane_select(odd, p3, p2) + dpp_i<KOMP_DPP_XOR1>(lane_select(odd, p2, p3));  // slot (q & 1) + 2
+  // lanes q, q ^ 2: keep the slot whose bit 1 is q's
+  return lane_select(hi, t2, t1) + dpp_i<KOMP_DPP_XOR2>(lane_select(hi, t1, t2));
+}
+
+// The same for two slots: lanes q and q + 2 of the quad both get the quad's sum for slot q & 1.
+__device__ __forceinline__ int quad_scatter2(int p0, int p1, uint64_t odd) {
+  const int t = lane_select(odd, p1, p0) + dpp_i<KOMP_DPP_XOR1>(lane_select(odd, p0, p1));
+  return t + dpp_i<KOMP_DPP_XOR2>(t);
 }
 
 // LPR lanes per row group (4 per block: lane q of a quad takes bytes 16q..16q+15 of the block), NB chunks per lane
@@ -130,9 +168,14 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + gblk) * 2);
 
 
-  // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk ----
+  // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk.  Chunk slot u of
+  // a quad is scaled by lane u % 4 alone, so a lane loads the scales of its own slots only: q, q + 4 (nb 8); lanes
+  // q >= nb own none (nb < 4) and read a zero scale ----
+  constexpr int NOWN = (NB + 3) / 4;
   u32x4 w[NB];
-  int16_t sc[NB];
+  int16_t sc[NOWN];
+  const bool owner = NB >= 4 || q < NB;
+  const unsigned vo_sq = vo_s + static_cast<unsigned>(q * BPG * 2);
   auto load = [&](int p, int st, bool first) {
     // a descriptor per pass, over the pass's rows inside the matrix: a row past the matrix lies past the range,
     // which the per-lane offset is checked against, and reads zeros; the step goes into the scalar offset, and the
@@ -144,22 +187,26 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 64);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
+    // The chunk's place in the step is wave-uniform and goes into the scalar offset too, so every chunk's load shares
+    // the one per-lane offset (a chunk past the row's end swaps it for the out-of-range one)
     if (!first && lim >= BSTEP) {
 #pragma unroll
-      for (int u = 0; u < NB; ++u)  // the scales first: a chunk's dot then waits for its own weight load only
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * BPG * 2, so_s, 0));
+      for (int i = 0; i < NOWN; ++i)  // the scales first: a chunk's dot then waits for its own weight load only
+        sc[i] = static_cast<int16_t>(
+            __builtin_amdgcn_raw_buffer_load_b16(srs, owner ? vo_sq : kOob, so_s + i * 4 * BPG * 2, 0));
 #pragma unroll
-      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * BPG * 64, so_w, 2);
+      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w, so_w + u * BPG * 64, 2);
     } else {  // the row's last, partial step, and the first tile
 #pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const bool ok = gblk + u * BPG < lim;
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_s + u * BPG * 2 : kOob, so_s, 0));
+      for (int i = 0; i < NOWN; ++i) {
+        const bool ok = owner && gblk + (q + 4 * i) * BPG < lim;
+        sc[i] = static_cast<int16_t>(
+            __builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_sq : kOob, so_s + i * 4 * BPG * 2, 0));
       }
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         const bool ok = gblk + u * BPG < lim;
-        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w + u * BPG * 64 : kOob, so_w, 2);
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w : kOob, so_w + u * BPG * 64, 2);
       }
     }
   };
@@ -231,7 +278,7 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   // ---- stream the weights ----
   const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
   const int2* ml = meta + gblk;
-  const int qmask = q == 0 ? -1 : 0;  // the block's -sum(x) joins one lane of the quad
+  const uint64_t odd = __builtin_amdgcn_ballot_w64((q & 1) != 0), hi = __builtin_amdgcn_ballot_w64((q & 2) != 0);
   const CrumbMasks km = crumb_masks();
   for (int p = 0; p < npass; ++p) {
     const int rl = p * RPW + grp;
@@ -244,40 +291,52 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
       if (p != 0 || st != 0) load(p, st, false);
       const int tb = st * BSTEP;
       const int lim = nblk - tb;  // blocks from the tile's first to the row's end (wave-uniform)
+      // 16 x the lane's partial dots of its chunks.  Slots past the row's end are skipped and hold arbitrary values:
+      // their scales and d_x are zero, so they add nothing
+      int pd[MC][NB];
+#pragma unroll
+      for (int m = 0; m < MC; ++m)
+#pragma unroll
+        for (int u = 0; u < NB; ++u) pd[m][u] = 0;
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         if (u * BPG >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
-        if constexpr (MC == 1) {  // one column: this form of the loop compiles ~10% faster at 32768 x 8192
-          const unsigned char* xp = xl + (tb + u * BPG) * XB;
-          u32x4 xv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
-          const int2 mt = ml[tb + u * BPG];
-          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask, km), 4);  // the block's exact dot, in every lane
-          if (__builtin_expect(S != nullptr, 0)) {
-            const int b = tb + u * BPG + gblk;
-            if (q == 0 && rv && b < nblk) S[static_cast<int64_t>(row) * nblk + b] = sb;
-          }
-          const float f = __int_as_float(mt.x) * f16_bits_to_f32(sc[u]) * static_cast<float>(sb);  // kernels.py:141
-          acc[0] += q == 0 ? f : 0.0f;
-          continue;
-        }
-        const float dw = f16_bits_to_f32(sc[u]);
 #pragma unroll
         for (int m = 0; m < MC; ++m) {
-          const int bo = m * nblk_pad + tb + u * BPG;
-          const unsigned char* xp = xl + bo * XB;
+          const unsigned char* xp = xl + (m * nblk_pad + tb + u * BPG) * XB;
           u32x4 xv[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
-          const int2 mt = ml[bo];
-          const int sb = group_sum(chunk_dot(w[u], xv, mt.y & qmask, km), 4);  // the block's exact dot, in every lane
+          pd[m][u] = chunk_dot16(w[u], xv, km);
+          // the dot is computed here, in the slot's own block: sunk to the scaling after the loop it would keep every
+          // slot's activation pieces live at once (16 VGPRs a slot and column)
+          asm volatile("" : "+v"(pd[m][u]));
+        }
+      }
+      // lane q completes and scales the blocks of slots q, q + 4: the exact dot s = the quad's sum / 16 - sum(x), then
+      // d_x * d_w * f32(s) (kernels.py:141 order)
+#pragma unroll
+      for (int i = 0; i < NOWN; ++i) {
+        if (4 * i * BPG >= lim) break;  // wave-uniform: every slot from 4i on lies past the row's end
+        const int u = NB >= 4 ? 4 * i + q : (owner ? q : 0);  // lanes q >= nb (nb < 4) own nothing: slot 0, d_w 0
+        const float dw = f16_bits_to_f32(sc[i]);
+#pragma unroll
+        for (int m = 0; m < MC; ++m) {
+          int v;  // the quad's sum for the lane's slot u
+          if constexpr (NB == 1)
+            v = group_sum(pd[m][0], 4);
+          else if constexpr (NB == 2)
+            v = quad_scatter2(pd[m][0], pd[m][1], odd);
+          else
+            v = quad_scatter4(pd[m][4 * i], pd[m][4 * i + 1], pd[m][4 * i + 2], pd[m][4 * i + 3], odd, hi);
+          const int2 mt = ml[m * nblk_pad + tb + u * BPG];
+          const int sb = (v >> 4) + mt.y;  // the block's exact dot
           if (__builtin_expect(S != nullptr, 0)) {
             const int b = tb + u * BPG + gblk;
-            if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
+            if (owner && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
           }
-          const float f = __int_as_float(mt.x) * dw * static_cast<float>(sb);  // kernels.py:141 order
-          acc[m] += q == 0 ? f : 0.0f;
+          const float f = __int_as_float(mt.x) * dw * static_cast<float>(sb);
+          acc[m] += owner ? f : 0.0f;
         }
       }
     }

@@ -148,12 +148,16 @@ def test_auto_plan(fmt, n, k, fused):
         assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and bn % nw == 0
         assert lanes == 64 // min(rpw, 16) and passes == rpw // min(rpw, 16)
         assert blocks_per_step >= nblk or nb == 4  # one K step unless the q4_0 nb cap applies
-    elif fmt == 0 and nblk <= 128:  # throughput regime, q4_0 rows of up to 128 blocks: 16 lanes per row, 8 waves
+    elif fmt == 0 and not fused and nblk <= 256:  # one q4_0 column, rows of up to 256 blocks: one K step of nb 4
+        assert nb == 4 and passes == 1 and lanes == max(16, 1 << (-(-nblk // 4) - 1).bit_length())
+        rpw = 64 // lanes  # 8 rows a workgroup, at least 4 waves
+        assert blocks_per_step >= nblk and (bn, nw) == (max(4, 8 // rpw) * rpw, max(4, 8 // rpw))
+    elif fmt == 0 and nblk <= 128:  # fused q4_0 rows of up to 128 blocks: 16 lanes per row, 8 waves
         assert (bn, nb, nw, lanes, passes) == (32, 2, 8, 16, 1)
     elif fmt == 0:  # throughput regime, q4_0: whole rows in one K step, two passes per wave
         assert passes == 2 and nw == 4 and bn == nw * (64 // lanes) * 2 and (blocks_per_step >= nblk or lanes == 64)
-    else:  # throughput regime, tq2_0: nb 4, 16 lanes per row, 8 waves
-        assert (bn, nb, nw, lanes, passes) == (32, 4, 8, 16, 1)
+    else:  # throughput regime, tq2_0: nb 4, one K step (a lane quad per block), 8 waves
+        assert (nb, nw, passes) == (4, 8, 1) and lanes == max(16, nblk) and bn == 8 * (64 // lanes)
 
 
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])

@@ -169,8 +169,8 @@ def test_gemv_every_legal_knob(fmt, block_n, nb, nw):
                                      ("q8_0", 20000, 1024), ("q4_k", 16400, 4352), ("tq2_0", 16400, 8192)])  # fmt: skip
 def test_gemv_auto_plan_throughput_shapes(fmt, n, k):
     # N >= 16384 (16400 and 20000 leave a partial last workgroup); q4_0 reads whole rows in one K step, two passes,
-    # except the single-column q4_0 / iq4_nl rows of up to 128 blocks (16 lanes per row, one pass) and tq2_0
-    single = fmt == "tq2_0" or (fmt in ("q4_0", "iq4_nl") and k // 32 <= 128)
+    # except the single-column q4_0 / iq4_nl rows of up to 256 blocks (one pass) and tq2_0
+    single = fmt == "tq2_0" or (fmt in ("q4_0", "iq4_nl") and k // 32 <= 256)
     assert host.auto_plan(fmt, 1, n, k)["passes"] == (1 if single else 2)
     y, s, r, rs, _, _, ws, rd = run_gemv(fmt, n, k, 1, 23, False, None, None, 2, None)
     assert np.array_equal(s.astype(np.int64), rs)
