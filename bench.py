@@ -42,7 +42,7 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
 # profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
-TRAFFIC_FUSED_BITNET_M1 = 4849972
+TRAFFIC_FUSED_BITNET_M1 = 4829499
 
 
 # (values per weight block, weight bytes per block, values per activation block) of each weight format
@@ -186,8 +186,8 @@ def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
 
 def read_floor_us(torch, host, nbytes):
     """Graph-replay us per call of the library's streaming-read probe (komp_stream_read: the bytes read once with
-    non-temporal 16-byte loads, nothing computed) over cold copies of nbytes, the same harness as the GEMVs: the time
-    of moving that many bytes alone, which a GEMV over them can at best reach."""
+    streaming 16-byte buffer loads, nothing computed) over cold copies of nbytes, the same harness as the GEMVs: the
+    time of moving that many bytes alone, which a GEMV over them can at best reach."""
     nb = -(-nbytes // 16) * 16
     ncopy = max(2, math.ceil((COLD_BYTES // 2) / nb))
     bufs = [torch.zeros(nb, dtype=torch.uint8, device="cuda") for _ in range(ncopy)]

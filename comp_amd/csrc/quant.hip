@@ -99,18 +99,21 @@ __global__ void tq2_0_decode_kernel(const uint8_t* __restrict__ WQ, int32_t* __r
   }
 }
 
-// Streaming-read probe: every 16 bytes of SRC read once with non-temporal 16-byte loads (4 per thread, 512 threads
-// per workgroup, all in flight together), XOR-folded per wave into OUT[wave]: the time of moving the bytes alone, the
-// floor a GEMV over as many bytes is measured against.
+// Streaming-read probe: every 16 bytes of SRC read once with 16-byte buffer loads (4 per thread, 512 threads per
+// workgroup, all in flight together; streaming cache policy: sc0 nt), XOR-folded per wave into OUT[wave]: the time of
+// moving the bytes alone, the floor a GEMV over as many bytes is measured against.  Each workgroup's 32 KB lie in
+// one buffer descriptor whose range ends at SRC's end, so the loads carry no bounds branches (bytes past the end
+// read as zeros).  Like a GEMV, it writes a result: a kernel that stores anything ends ~0.4 us later than one that
+// does not (the stores' completion before the kernel's end), at every size.
 __global__ void __launch_bounds__(512) stream_read_kernel(const u32x4* __restrict__ SRC, int64_t n16,
                                                           uint32_t* __restrict__ OUT) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * 2048 + threadIdx.x;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 2048;  // the workgroup's first 16-byte element
+  const int64_t left = (n16 - first) * 16;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(SRC + first), 0,
+                                                    static_cast<int>(left < 32768 ? left : 32768), 0x00020000);
   u32x4 v[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t j = base + u * 512;
-    v[u] = j < n16 ? __builtin_nontemporal_load(SRC + j) : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int u = 0; u < 4; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * 512 + threadIdx.x) * 16, 0, 3);
   unsigned acc = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];

@@ -203,7 +203,7 @@ int komp_tq2_0_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int6
 int komp_dp4a_probe(const int32_t* A, const int32_t* B, const int32_t* C, int32_t* OUT, int64_t n, int mode,
                     void* stream);
 
-/* Reads the BYTES of SRC once (non-temporal 16-byte loads, 2048 per 512-thread workgroup) and writes the XOR of each
+/* Reads the BYTES of SRC once (streaming 16-byte buffer loads, 2048 per 512-thread workgroup) and writes the XOR of each
  * wave's 512 dwords to OUT[wave], 8 * ceil(BYTES / 32768) words: the cost of moving the bytes alone, the floor a GEMV
  * over as many bytes is compared with.  BYTES % 16 == 0, SRC 16-byte and OUT 4-byte aligned.
  * No reference counterpart: a measurement probe (bench.py reports every GEMV shape against it). */
