@@ -173,7 +173,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
       nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
       // two or three columns run this plan on the lean kernels only (the general kernel takes at most 8 waves there)
-      const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k))
+      const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k), fused,
+                                                                    static_cast<int>(64 * waves))
                                                : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k));
       if (m == 1 || waves <= 8 || lean_lds <= kLdsMax)
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);

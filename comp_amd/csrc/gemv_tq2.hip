@@ -102,7 +102,7 @@ __device__ __forceinline__ int quad_scatter2(int p0, int p1, uint64_t odd) {
 // ONE: the plan has one pass and one K step (every decode shape whose rows fit one step), so the weight stream is
 // straight-line code with no loop and no reload: a launch starts with a cold instruction cache, and every 64-byte
 // line of code on the way to the first dot costs tens of nanoseconds of fetch.
-template <int LPR, int NB, int MC, bool FUSED, bool ONE>
+template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA>
 __global__ void __launch_bounds__(1024)
 tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes, const uint8_t* __restrict__ WQ1,
                 const int16_t* __restrict__ WS1, const void* __restrict__ XA, const float* __restrict__ XD,
@@ -117,9 +117,20 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
   // ---- the staging's first loads (16 threads per block), issued first: they need only preloaded arguments, so they
   // go out before anything else (the segment table of a multi-matrix launch included) and do not queue behind the
   // weights.  f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) of the flattened
-  // columns (X [MC][K], XQ [MC][K] and XD [MC][nblk] are dense) for thread i ----
+  // columns (X [MC][K], XQ [MC][K] and XD [MC][nblk] are dense) for thread i.  DMA (several q8 columns needing more
+  // than one staging pass, when LDS holds them): the columns are copied global -> LDS instead (global_load_lds: no
+  // registers held), every pass ahead of the weights, and staged from there; staged pass by pass from registers,
+  // each later pass waits for every weight load issued before it (the load counter retires in issue order).  A
+  // template flag, so that each form's wait counts are exact (behind a runtime branch the compiler makes the
+  // register staging wait for the weights) ----
   const int nstage = MC * nblk * 16;
-  const bool stg = tid < nstage;
+  const int nthreads = blockDim.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool stg = !DMA && tid < nstage;
+  const int nsteps = ONE ? 1 : (nblk + BSTEP - 1) / BSTEP;
+  const int nblk_pad = nsteps * BSTEP;
+  unsigned char* const raw = lds + ((MC * nblk_pad * (XB + 8) + 15) & ~15);  // past the staged columns and meta
   f32x4 xf[4];
   u32x4 x16;
   float xdv = 0.0f;
@@ -132,6 +143,23 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
       x16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + tid * 16);
       if ((tid & 15) == 0) xdv = XD[tid >> 4];
     }
+  }
+  if constexpr (DMA) {  // lane i's piece lands at the wave's LDS address + size * i
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    const int pieces = FUSED ? nstage * 4 : nstage;  // 16-byte pieces of X (f32) or XQ (q8)
+    const u32x4* src = static_cast<const u32x4*>(XA);
+    for (int c = wave * 64; c < pieces; c += nthreads)
+      if (c + lane < pieces)
+        __builtin_amdgcn_global_load_lds(src + c + lane, reinterpret_cast<lds_ptr>(reinterpret_cast<uintptr_t>(raw + c * 16)),
+                                         16, 0, 0);
+    if constexpr (!FUSED) {  // and d_x, one dword per block, after the q8 bytes
+      unsigned char* rawd = raw + nstage * 16;
+      for (int c = wave * 64; c < MC * nblk; c += nthreads)
+        if (c + lane < MC * nblk)
+          __builtin_amdgcn_global_load_lds(XD + c + lane, reinterpret_cast<lds_ptr>(reinterpret_cast<uintptr_t>(rawd + c * 4)),
+                                           4, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads
   }
   int N = N1;
   unsigned SW = static_cast<unsigned>(SW1);  // a row's bytes: one pass's rows span at most 0x7FFFFFF0 of them
@@ -151,15 +179,10 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
     Y = segs.y[sg];
     wg -= segs.first_wg[sg];
   }
-  const int nthreads = blockDim.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane & 3;
   const int gblk = (lane & (LPR - 1)) >> 2;
   const int grp = lane / LPR;
-  const int nsteps = ONE ? 1 : (nblk + BSTEP - 1) / BSTEP;
   const int npass = ONE ? 1 : passes;
-  const int nblk_pad = nsteps * BSTEP;
   const int rows_per_wave = RPW * npass;
   const int row_base = wg * rows_per_wg + wave * rows_per_wave;  // wave-uniform
   const int wave_rows = min(rows_per_wave, rows_per_wg - wave * rows_per_wave);
@@ -245,22 +268,46 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
       if (r == 0) meta[b] = make_int2(__float_as_int(dxv), -qsum);
     }
   };
-  if (stg) stage_one(tid, xf, x16, xdv);
-  // columns of more than 16 values per thread (none at the decode shapes: the loop sits out of line)
-  if (__builtin_expect(nstage > nthreads, 0)) {
-    for (int i = tid + nthreads; i < nstage; i += nthreads) {
+  if constexpr (DMA) {
+    // the copies are older than the first tile's NOWN + NB loads: wait for them only, then let every wave see them
+    constexpr int kN = NOWN + NB;
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((kN & 0xF) | 0x70 | 0xF00 | ((kN >> 4) << 14));  // vmcnt(NOWN + NB)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const float* rawd = reinterpret_cast<const float*>(raw + nstage * 16);
+    for (int i = tid; i < nstage; i += nthreads) {
       f32x4 v[4];
       u32x4 xq16;
       float dxv = 0.0f;
       if constexpr (FUSED) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 16);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = src[t];
+        for (int t = 0; t < 4; ++t) v[t] = *reinterpret_cast<const f32x4*>(raw + i * 64 + t * 16);
       } else {
-        xq16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 16);
-        if ((i & 15) == 0) dxv = XD[i >> 4];
+        xq16 = *reinterpret_cast<const u32x4*>(raw + i * 16);
+        if ((i & 15) == 0) dxv = rawd[i >> 4];
       }
       stage_one(i, v, xq16, dxv);
+    }
+  } else {
+    if (stg) stage_one(tid, xf, x16, xdv);
+    // one column longer than a staging pass of the workgroup (out of line: none at the decode shapes)
+    if (__builtin_expect(nstage > nthreads, 0)) {
+      for (int i = tid + nthreads; i < nstage; i += nthreads) {
+        f32x4 v[4];
+        u32x4 xq16;
+        float dxv = 0.0f;
+        if constexpr (FUSED) {
+          const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(XA) + i * 16);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = src[t];
+        } else {
+          xq16 = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(XA) + i * 16);
+          if ((i & 15) == 0) dxv = XD[i >> 4];
+        }
+        stage_one(i, v, xq16, dxv);
+      }
     }
   }
   for (int i = tid; i < MC * (nblk_pad - nblk); i += nthreads) {
@@ -351,7 +398,12 @@ tq2_lean_kernel(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes
 template <int LPR, int NB, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const bool one = p.passes == 1 && c.k / 256 <= (LPR / 4) * NB;
-  auto kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false>;
+  auto kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, false> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, false>;
+  bool dma = false;
+  if constexpr (MC > 1 && !FUSED) {
+    dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves);
+    if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
+  }
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -362,9 +414,9 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     }
   }
   const int nblk = c.k / 256;
-  const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k);
-  static std::atomic<unsigned> lds_limit[2][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
-  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[one ? 1 : 0]);
+  const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k, FUSED, 64 * p.waves);
+  static std::atomic<unsigned> lds_limit[4][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[(one ? 1 : 0) + (dma ? 2 : 0)]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));
@@ -417,11 +469,30 @@ hipError_t by_lpr(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
 
 }  // namespace gemv_tq2
 
-size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k) {
+namespace {
+size_t tq2_staged_bytes(int lpr, int nb, int mc, int k) {
   const int bstep = (lpr / 4) * nb;
   const int64_t nblk = k / 256;
   const int64_t pad = (nblk + bstep - 1) / bstep * bstep;
   return static_cast<size_t>(mc) * pad * (gemv_tq2::kBlockStride + 8);
+}
+size_t tq2_raw_bytes(int mc, int k, bool fused) {  // the columns as they are in memory (f32, or q8 bytes and d_x)
+  return fused ? static_cast<size_t>(mc) * k * 4 : static_cast<size_t>(mc) * k + static_cast<size_t>(mc) * (k / 256) * 4;
+}
+}  // namespace
+
+bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads) {
+  // q8 columns only: fused, the f32 columns are four times the bytes, and copying them all ahead of the weights
+  // delayed the weights more than the passes cost (BitNet-2B 2560x6912, 3 columns: 5.7 -> 6.8 us fused, against 4.8
+  // -> 4.6 with q8 in; 2 columns 4.5 -> 5.4 fused, 4.2 -> 3.9 with q8 in)
+  return !fused && mc > 1 && static_cast<int64_t>(mc) * (k / 256) * 16 > threads &&
+         ((tq2_staged_bytes(lpr, nb, mc, k) + 15) & ~size_t{15}) + tq2_raw_bytes(mc, k, fused) <= gemv_tq2::kLdsLimit;
+}
+
+size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k, bool fused, int threads) {
+  const size_t staged = tq2_staged_bytes(lpr, nb, mc, k);
+  if (!tq2_lean_dma(lpr, nb, mc, k, fused, threads)) return staged;
+  return ((staged + 15) & ~size_t{15}) + tq2_raw_bytes(mc, k, fused);  // the raw columns follow, 16-byte aligned
 }
 
 bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p) {
@@ -430,7 +501,7 @@ bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p) {
   return c.fmt == FMT_TQ2_0 && c.m >= 1 && c.m <= 3 && c.mode == MODE_DP4A && p.lpr_log2 >= 2 && p.lpr_log2 <= 6 &&
          nb_ok && p.waves >= 1 && p.waves <= 16 && p.rows_per_wave == (64 >> p.lpr_log2) * p.passes &&
          lean_strides_fit(c, 64 >> p.lpr_log2) &&
-         tq2_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k) <= gemv_tq2::kLdsLimit;
+         tq2_lean_lds_bytes(1 << p.lpr_log2, p.nb, c.m, c.k, c.x != nullptr, 64 * p.waves) <= gemv_tq2::kLdsLimit;
 }
 
 hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {

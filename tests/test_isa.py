@@ -28,25 +28,26 @@ def test_library_holds_gfx950_code_objects_with_every_kernel_family():
 
 
 @pytest.mark.parametrize("fmt,bn,nb,nw,name", [("q4_0", 64, 4, 4, "gemv_q4::q4_lean_kernel<0, 4, 4, 1, false, false>"),
-                                               ("tq2_0", 32, 2, 4, "gemv_tq2::tq2_lean_kernel<8, 2, 1, false, false>"),
+                                               ("tq2_0", 32, 2, 4, "gemv_tq2::tq2_lean_kernel<8, 2, 1, false, false, false>"),
                                                ("iq4_nl", 8, 2, 8, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>")])
 def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     # one column in dp4a mode runs the single-column kernel with 64 / min(block_n / num_warps, 16) lanes per row
     assert cli._gemv_kernel(fmt, 2, nb, 1, bn, nw) == name
     r = isa.summary(name, cli.VALUES_PER_LOAD[fmt])
     assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"] and r["loop"].get("dot4", 0) > 0
-    three = name.replace(", 1, false, false>", ", 3, false, false>")
+    three = name.replace(", 1, false, false", ", 3, false, false", 1)
     assert cli._gemv_kernel(fmt, 2, nb, 3, bn, nw) == three  # three columns
     assert cli._gemv_kernel(fmt, 2, 8, 3, bn, nw).startswith("gemv_impl::gemv_kernel<")  # nb 8 at three columns
     assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw).startswith("gemv_impl::gemv_kernel<")  # bytes mode
 
 
 @pytest.mark.parametrize("fmt,bn,nb,nw,k,m,name", [
-    ("tq2_0", 16, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, true>"),   # 10 blocks <= 4 x 4
-    ("tq2_0", 16, 4, 4, 6912, 1, "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, false>"),  # 27 blocks: two K steps
-    ("tq2_0", 16, 4, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 4, 3, false, true>"),
-    ("tq2_0", 16, 2, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 2, 3, false, false>"),  # 10 blocks > 4 x 2
-    ("tq2_0", 128, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_kernel<4, 4, 1, false, false>"),  # 32 rows a wave: two passes
+    ("tq2_0", 16, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, true, false>"),   # 10 blocks <= 4 x 4
+    ("tq2_0", 16, 4, 4, 6912, 1, "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, false, false>"),  # 27 blocks: two K steps
+    # 3 x 10 blocks x 16 threads > 4 waves: staged through an LDS copy
+    ("tq2_0", 16, 4, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 4, 3, false, true, true>"),
+    ("tq2_0", 16, 2, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 2, 3, false, false, true>"),  # 10 blocks > 4 x 2
+    ("tq2_0", 128, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_kernel<4, 4, 1, false, false, false>"),  # two passes a wave
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
     ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, false>"),  # one pass: one column only
     ("iq4_nl", 8, 2, 8, 8192, 1, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
