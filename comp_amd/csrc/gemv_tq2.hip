@@ -482,9 +482,10 @@ size_t tq2_raw_bytes(int mc, int k, bool fused) {  // the columns as they are in
 }  // namespace
 
 bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads) {
-  // q8 columns only: fused, the f32 columns are four times the bytes, and copying them all ahead of the weights
-  // delayed the weights more than the passes cost (BitNet-2B 2560x6912, 3 columns: 5.7 -> 6.8 us fused, against 4.8
-  // -> 4.6 with q8 in; 2 columns 4.5 -> 5.4 fused, 4.2 -> 3.9 with q8 in)
+  // q8 columns only.  Fused, every workgroup reads all of the f32 columns (21 MB from L2 over the chip at 2560x6912
+  // and 3 columns), and through LDS that cost more than the register passes, copied ahead of the weights (3 columns
+  // 5.7 -> 6.8 us, 2 columns 4.5 -> 5.4) or behind them (7.1, 5.6); with q8 in, 3 columns 4.8 -> 4.6, 2 columns
+  // 4.2 -> 3.9
   return !fused && mc > 1 && static_cast<int64_t>(mc) * (k / 256) * 16 > threads &&
          ((tq2_staged_bytes(lpr, nb, mc, k) + 15) & ~size_t{15}) + tq2_raw_bytes(mc, k, fused) <= gemv_tq2::kLdsLimit;
 }
