@@ -10,6 +10,9 @@
                                                instruction mix; -o writes the code object and the kernel's ISA
     python -m comp_amd mix    [--archs gfx950]  hot-loop instruction mixes of the GEMV configs (and the matrix-core
                                                GEMM plans) of this build
+    python -m comp_amd counters CSV... --cases CASES
+                                               per-weight instruction mix of the launches of a rocprofv3 --pmc run
+                                               of `bench.py --counter-calls N` (comp_amd.counters)
 
 `gen` and `mix` read the gfx950 code objects inside this build's own library (comp_amd.isa), where the reference
 compiles Triton to PTX/SASS and reads those (src/komp/cli.py:88-158).  `fork` (the Triton fork) has no counterpart and
@@ -227,6 +230,24 @@ def cmd_mix(args):
     return 1 if fails else 0
 
 
+def cmd_counters(args):
+    from . import counters
+
+    if "--cases" not in args or args.index("--cases") + 1 >= len(args):
+        print("komp counters: CSV... --cases CASES (the counter run's counter_calls JSON or a file holding it)",
+              file=sys.stderr)  # fmt: skip
+        return 2
+    i = args.index("--cases")
+    paths = [a for a in args[:i] + args[i + 2 :] if not a.startswith("--")]
+    try:
+        rows = counters.table(counters.merge([counters.read_pass(p) for p in paths]), counters.load_cases(args[i + 1]))
+    except (OSError, ValueError, KeyError) as e:
+        print(f"komp counters: {e}", file=sys.stderr)
+        return 2
+    print(counters.markdown(rows))
+    return 0
+
+
 def _unavailable(name):
     def cmd(_args):
         print(f"komp {name}: not available on the gfx950 build (it reports the Triton fork)", file=sys.stderr)
@@ -235,7 +256,8 @@ def _unavailable(name):
     return cmd
 
 
-COMMANDS = {"check": cmd_check, "verify": cmd_verify, "gen": cmd_gen, "mix": cmd_mix, "fork": _unavailable("fork")}
+COMMANDS = {"check": cmd_check, "verify": cmd_verify, "gen": cmd_gen, "mix": cmd_mix, "counters": cmd_counters,
+            "fork": _unavailable("fork")}
 
 
 def main(argv=None):
