@@ -68,17 +68,17 @@ TimingState g_timing;
 //   that read each row in 1 KB pieces over several steps ran 5-17% slower).  TQ2_0: nb 4 and as many lanes per row
 //   (16..64) as give each lane quad one block per chunk slot, 8 waves: at 32768 x 8192, 32 lanes per row ran 12.0-12.4
 //   us against 16.2 for 16 lanes in two K steps (whose instance needs more than 64 VGPRs, 7 waves a SIMD).
-//   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode, fused launches of one column,
-//   TQ2_0 with 1-3 columns and Q4_0 with 2-3: one workgroup per CU with ceil(N / CUs) rows, one row group per wave,
-//   one K step where nb allows.  A grid of at most
-//   one workgroup per CU is spread one to a CU, so no CU stages (and, fused, quantizes) the activations twice or runs
-//   two workgroups' dots on the same SIMDs; 9-24% faster at the BitNet-2B and Llama-3-8B shapes than 8-wave
-//   workgroups of 8-16 rows.  Lanes per row start at 64 and halve while the rows would need more than 16 waves or a
-//   lane would get fewer than 1.5 of the row's 16-byte chunks.
-//   Otherwise (one unfused Q4_0 column, other modes, 2-3 columns of the other formats): 8 waves per workgroup, as many lanes per row as the row has
-//   16-byte chunks (at most 64; the fused launch halves that, since every workgroup pays for quantizing the input),
-//   and nb just large enough for one K step (Q4_0 caps it at 4), because each extra step adds a full HBM round trip to
-//   a wave's critical path.
+//   Latency regime (fewer rows: every wave of the grid is resident at once), dp4a mode (TQ2_0: and bytes mode), fused
+//   launches of one column, TQ2_0 with 1-3 columns and Q4_0 with 2-3: one workgroup per CU with ceil(N / CUs) rows,
+//   one row group per wave, one K step where nb allows.  A grid of at most one workgroup per CU is spread one to a
+//   CU, so no CU stages (and, fused, quantizes) the activations twice or runs two workgroups' dots on the same SIMDs;
+//   9-24% faster at the BitNet-2B and Llama-3-8B shapes than 8-wave workgroups of 8-16 rows.  Lanes per row start at
+//   64 and halve while the rows would need more than 16 waves or a lane would get fewer than 1.5 of the row's 16-byte
+//   chunks.
+//   Otherwise (one unfused Q4_0 column, other modes, 2-3 columns of the other formats): 8 waves per workgroup, as
+//   many lanes per row as the row has 16-byte chunks (at most 64; the fused launch halves that, since every workgroup
+//   pays for quantizing the input), and nb just large enough for one K step (Q4_0 caps it at 4), because each extra
+//   step adds a full HBM round trip to a wave's critical path.
 // The knob-mapped plans are knob sets of the explicit tune space; the two-pass Q4_0 throughput plan and the
 // one-workgroup-per-CU plans are beyond the knob mapping.
 int pow2_ceil(int64_t v) {
@@ -143,7 +143,9 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
     return plan_of(4 * (64 / lpr) * 2, nb, 4, lpr, 2);  // 4 waves, two passes each
   }
-  if (mode == KOMP_MODE_DP4A && m <= 3 && (fmt == FMT_TQ2_0 || (m == 1 && fused) || (fmt == FMT_Q4_0 && m > 1))) {
+  // the lean kernels' modes: dp4a, and bytes for TQ2_0
+  const bool lean_mode = mode == KOMP_MODE_DP4A || (fmt == FMT_TQ2_0 && mode == KOMP_MODE_BYTES);
+  if (lean_mode && m <= 3 && (fmt == FMT_TQ2_0 || (m == 1 && fused) || (fmt == FMT_Q4_0 && m > 1))) {
     const int cus = device_cus();
     const int64_t rows = n < 1 ? 1 : (n + cus - 1) / cus;
     const int lpr_min = bpb > 4 ? bpb : 4;  // a row group holds whole blocks
@@ -172,11 +174,12 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       const int nb_max = fmt == FMT_Q4_K || m > 1 ? 4 : 8;
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
       nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
-      // two or three columns run this plan on the lean kernels only (the general kernel takes at most 8 waves there)
+      // past 8 waves, two or three columns (and bytes mode) run this plan on the lean kernels only: the general kernel
+      // takes at most 8 waves there
       const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k), fused,
-                                                                    static_cast<int>(64 * waves))
+                                                                    static_cast<int>(64 * waves), mode == KOMP_MODE_BYTES)
                                                : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k));
-      if (m == 1 || waves <= 8 || lean_lds <= kLdsMax)
+      if (waves <= 8 || (m == 1 && mode == KOMP_MODE_DP4A) || lean_lds <= kLdsMax)
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);
     }
   }

@@ -166,12 +166,14 @@ hipError_t launch_gemv_more(const GemvCall& c, const GemvPlan& p, hipStream_t st
 hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q4_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q4_k_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
-// TQ2_0, 1-3 columns in dp4a mode (gemv_tq2.hip): the plans it runs, its LDS bytes and its launch
+// TQ2_0, 1-3 columns in dp4a and bytes modes (gemv_tq2.hip, gemv_tq2_bytes.hip): the plans it runs, its LDS bytes
+// and its launch
 bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p);
-size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k, bool fused, int threads);
-// several columns staged in more than one pass of the workgroup's threads go through LDS as they are in memory
-bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads);
+size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k, bool fused, int threads, bool bytes);
+// several q8 columns staged in more than one pass of the workgroup's threads go through LDS as they are in memory
+bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads, bool bytes);
 hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_tq2_lean_bytes(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 // Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip)
 bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p);
 size_t q4_lean_lds_bytes(int g, int nb, int mc, int k);

@@ -163,8 +163,8 @@ def test_auto_plan(fmt, n, k, fused):
 @pytest.mark.parametrize("mode,m", [(0, 1), (1, 1), (2, 2), (2, 3)])
 def test_auto_plan_other_modes_and_columns_use_knob_sets(mode, m):
     for fmt, n, k in ((0, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912)):
-        if mode == 2 and (fmt == 1 or m > 1):
-            continue  # one workgroup per CU: TQ2_0 at 1-3 columns, Q4_0 at 2-3 (the tests below)
+        if (mode == 2 and (fmt == 1 or m > 1)) or (mode == 0 and fmt == 1):
+            continue  # one workgroup per CU: TQ2_0 at 1-3 columns (dp4a and bytes), Q4_0 at 2-3 (the tests below)
         for fused in (False, True):
             bn, nb, nw, lanes, passes = _abi.auto_plan(fmt, m, n, k, fused, mode)
             assert bn in (8, 16, 32, 64, 128) and nw in (1, 2, 4, 8) and lanes == 64 // min(bn // nw, 16)
@@ -175,9 +175,10 @@ def test_auto_plan_other_modes_and_columns_use_knob_sets(mode, m):
                                      # 3 x 10 blocks x 16 = 480 staging threads: 8 waves of 4 rows, one staging pass
                                      (3, (32, 4, 8, 16, 1), (10, 2, 10, 64, 1))])
 def test_auto_plan_bitnet_shapes(m, w1, w2):
-    # the BitNet-2B shapes, 1-3 columns: one workgroup per CU (256 CUs), fused and unfused alike
-    assert _abi.auto_plan(1, m, 6912, 2560, True) == _abi.auto_plan(1, m, 6912, 2560, False) == w1
-    assert _abi.auto_plan(1, m, 2560, 6912, True) == _abi.auto_plan(1, m, 2560, 6912, False) == w2
+    # the BitNet-2B shapes, 1-3 columns: one workgroup per CU (256 CUs), fused and unfused alike, dp4a and bytes
+    for mode in (2, 0):
+        assert _abi.auto_plan(1, m, 6912, 2560, True, mode) == _abi.auto_plan(1, m, 6912, 2560, False, mode) == w1
+        assert _abi.auto_plan(1, m, 2560, 6912, True, mode) == _abi.auto_plan(1, m, 2560, 6912, False, mode) == w2
 
 
 @pytest.mark.parametrize("n,k,plan", [(4096, 4096, (16, 2, 16, 64, 1)), (6144, 4096, (24, 4, 12, 32, 1)),

@@ -21,7 +21,8 @@ def run(*args):
 
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
-    for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_q4::q4_lean_kernel<",
+    for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_tq2::tq2_lean_bytes_kernel<",
+                   "gemv_q4::q4_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
         assert any(family in n for n in names), family
@@ -38,7 +39,15 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     three = name.replace(", 1, false, false", ", 3, false, false", 1)
     assert cli._gemv_kernel(fmt, 2, nb, 3, bn, nw) == three  # three columns
     assert cli._gemv_kernel(fmt, 2, 8, 3, bn, nw).startswith("gemv_impl::gemv_kernel<")  # nb 8 at three columns
-    assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw).startswith("gemv_impl::gemv_kernel<")  # bytes mode
+    if fmt == "tq2_0":  # bytes mode: the lean kernel's bytes form, with no dot instruction
+        bytes_name = name.replace("tq2_lean_kernel<", "tq2_lean_bytes_kernel<").replace(", false, false, false>",
+                                                                                        ", false, false>")
+        assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw) == bytes_name
+        r = isa.summary(bytes_name, cli.VALUES_PER_LOAD[fmt])
+        assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"] and r["dot4_total"] == 0
+        assert r["loop"].get("ld128", 0) > 0
+    else:
+        assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw).startswith("gemv_impl::gemv_kernel<")  # bytes mode
 
 
 @pytest.mark.parametrize("fmt,bn,nb,nw,k,m,name", [
