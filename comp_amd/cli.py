@@ -99,15 +99,16 @@ FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kern
 def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     """The kernel instantiation a launch of this config runs, the knobs giving lanes per row = 64 / min(block_n /
     num_warps, 16): in dp4a mode, q4_0 / iq4_nl / tq2_0 with 1-3 columns (nb <= 4, or 8 for one column) run the lean
-    kernel <(format,) lanes per row, nb, columns, fused, one pass(, tq2_0: staged through an LDS copy)>, and tq2_0 in
-    bytes mode its bytes form tq2_lean_bytes_kernel <lanes per row, nb, columns, fused, one pass> when LDS holds the
-    16-bit activations; everything else the general gemv_kernel <format, mode, columns, nb, fused>.  "One pass" is
+    kernel <(format,) lanes per row, nb, columns, fused, one pass(, tq2_0: staged through an LDS copy)>, and tq2_0 /
+    q4_0 in bytes mode its bytes form (tq2_lean_bytes_kernel / q4_lean_bytes_kernel <lanes per row, nb, columns, fused,
+    one pass>; tq2_0 when LDS holds the 16-bit activations); everything else the general gemv_kernel <format, mode,
+    columns, nb, fused>.  "One pass" is
     the lean kernel's single-pass, single-K-step form, which the launch picks when the rows per wave fit one pass and a
     row's K blocks one step (the single-column form only for q4_0 / iq4_nl); without k the loop form is named.  The
     LDS-copy form stages two or three tq2_0 columns that need more than one pass of the workgroup's threads, when LDS
     holds them."""
     cols = min(max(m, 1), 3)
-    lean_mode = mode == 2 or (mode == 0 and fmt == "tq2_0")
+    lean_mode = mode == 2 or (mode == 0 and fmt in ("tq2_0", "q4_0"))
     if lean_mode and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
         rpw = block_n // num_warps
         lanes = 64 // min(rpw, 16)
@@ -128,6 +129,8 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
                     f"{str(dma).lower()}>")
         elif fmt in ("q4_0", "iq4_nl"):
             one = one_pass and cols == 1 and k // 32 <= lanes * nb
+            if mode == 0:
+                return f"gemv_q4::q4_lean_bytes_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
             return f"gemv_q4::q4_lean_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, {cols}, false, {str(one).lower()}>"
     return f"gemv_impl::gemv_kernel<{FMT_NUM[fmt]}, {mode}, {min(max(m, 1), 3)}, {nb}, false>"
 

@@ -118,7 +118,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   const int64_t chunks = nblk * bpb;                      // lane slots per row (16-byte chunks; Q4_K 32-byte groups)
   // one unfused Q4_0 / IQ4_NL column (the lean kernel) over many rows: each row in one K step of nb 4, as few lanes
   // per row as that allows (16..64), 8 rows a workgroup (4 waves at least); the lean kernel's single-step form
-  const bool lean_q4 = (fmt == FMT_Q4_0 || fmt == FMT_IQ4_NL) && m == 1 && mode == KOMP_MODE_DP4A;
+  const bool lean_q4 = (fmt == FMT_Q4_0 || fmt == FMT_IQ4_NL) && m == 1 &&
+                       (mode == KOMP_MODE_DP4A || (fmt == FMT_Q4_0 && mode == KOMP_MODE_BYTES));
   if (lean_q4 && !fused && n >= 12288 && chunks <= 256) {
     int lpr = pow2_ceil((chunks + 3) / 4);
     lpr = lpr < 16 ? 16 : lpr;
@@ -143,8 +144,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     lpr = lpr < 16 ? 16 : (lpr > 64 ? 64 : lpr);
     return plan_of(4 * (64 / lpr) * 2, nb, 4, lpr, 2);  // 4 waves, two passes each
   }
-  // the lean kernels' modes: dp4a, and bytes for TQ2_0
-  const bool lean_mode = mode == KOMP_MODE_DP4A || (fmt == FMT_TQ2_0 && mode == KOMP_MODE_BYTES);
+  // the lean kernels' modes: dp4a, and bytes for TQ2_0 and Q4_0
+  const bool lean_mode = mode == KOMP_MODE_DP4A || ((fmt == FMT_TQ2_0 || fmt == FMT_Q4_0) && mode == KOMP_MODE_BYTES);
   if (lean_mode && m <= 3 && (fmt == FMT_TQ2_0 || (m == 1 && fused) || (fmt == FMT_Q4_0 && m > 1))) {
     const int cus = device_cus();
     const int64_t rows = n < 1 ? 1 : (n + cus - 1) / cus;
@@ -178,7 +179,8 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       // takes at most 8 waves there
       const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k), fused,
                                                                     static_cast<int>(64 * waves), mode == KOMP_MODE_BYTES)
-                                               : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k));
+                                               : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k),
+                                                                   mode == KOMP_MODE_BYTES);
       if (waves <= 8 || (m == 1 && mode == KOMP_MODE_DP4A) || lean_lds <= kLdsMax)
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);
     }

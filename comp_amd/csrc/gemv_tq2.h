@@ -77,16 +77,6 @@ __device__ __forceinline__ int chunk_dot16(const u32x4& w, const u32x4 (&x)[4], 
   return (((a1 << 2) + a4) << 2) + a16;
 }
 
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-
-// The signed bytes of q as 16-bit integers: bytes 0 and 2 (even) or 1 and 3 (odd) in the low and high half.
-__device__ __forceinline__ unsigned sext_even(unsigned q) {
-  return __builtin_bit_cast(unsigned, __builtin_bit_cast(s16x2, q << 8) >> 8);
-}
-__device__ __forceinline__ unsigned sext_odd(unsigned q) {
-  return __builtin_bit_cast(unsigned, __builtin_bit_cast(s16x2, q) >> 8);
-}
-
 // Bytes mode: the partial int32 dot of one 16-byte chunk with every weight and activation unpacked to an integer
 // first.  xe[j] / xo[j]: activation piece j's even / odd bytes as 16-bit integers (sext_even / sext_odd of each
 // dword); crumb j of weight byte e pairs with byte e of piece j.  Each crumb is isolated into a 16-bit half (bytes
@@ -101,10 +91,8 @@ __device__ __forceinline__ int chunk_dot_bytes(const u32x4& w, const u32x4 (&xe)
     for (int j = 0; j < 4; ++j) {
       const unsigned ce = (w[d] >> (2 * j)) & 0x00030003u;      // crumb j of bytes 0 and 2
       const unsigned co = (w[d] >> (2 * j + 8)) & 0x00030003u;  // crumb j of bytes 1 and 3
-      // the activation words as values: a bit cast of a vector element itself reads element 0
-      const unsigned ae = xe[j][d], ao = xo[j][d];
-      acc += __builtin_bit_cast(s16x2, ce) * __builtin_bit_cast(s16x2, ae);
-      acc += __builtin_bit_cast(s16x2, co) * __builtin_bit_cast(s16x2, ao);
+      acc += halves(ce) * halves(xe[j][d]);
+      acc += halves(co) * halves(xo[j][d]);
     }
   }
   return static_cast<int>(acc.x) + static_cast<int>(acc.y);
@@ -325,7 +313,7 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
         s16x2 t = {0, 0};
 #pragma unroll
         for (int d = 0; d < 4; ++d)
-          t += __builtin_bit_cast(s16x2, sext_even(xq16[d])) + __builtin_bit_cast(s16x2, sext_odd(xq16[d]));
+          t += halves(sext_even(xq16[d])) + halves(sext_odd(xq16[d]));
         s16 = static_cast<int>(t.x) + static_cast<int>(t.y);
       } else {
 #pragma unroll

@@ -15,6 +15,21 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Mode { MODE_BYTES = 0, MODE_DP4A_EMU = 1, MODE_DP4A = 2 };
 
+// Bytes mode's unpacked integers: two 16-bit values a register (v_pk_* arithmetic).
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// A register's two 16-bit halves.  Takes the word by value: a bit cast applied to a vector element itself reads
+// element 0 whatever the index.
+__device__ __forceinline__ s16x2 halves(unsigned v) { return __builtin_bit_cast(s16x2, v); }
+
+// The signed bytes of q as 16-bit integers: bytes 0 and 2 (even) or 1 and 3 (odd) in the low and high half.
+__device__ __forceinline__ unsigned sext_even(unsigned q) {
+  return __builtin_bit_cast(unsigned, halves(q << 8) >> 8);
+}
+__device__ __forceinline__ unsigned sext_odd(unsigned q) {
+  return __builtin_bit_cast(unsigned, halves(q) >> 8);
+}
+
 // f16 bit pattern -> f32, exact for every pattern (patch:33-36).
 __device__ __forceinline__ float f16_bits_to_f32(int16_t bits) {
   return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));

@@ -174,10 +174,11 @@ size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k, bool fused, int thread
 bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads, bool bytes);
 hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_tq2_lean_bytes(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
-// Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip)
+// Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip), and Q4_0 in bytes mode (gemv_q4_bytes.hip)
 bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p);
-size_t q4_lean_lds_bytes(int g, int nb, int mc, int k);
+size_t q4_lean_lds_bytes(int g, int nb, int mc, int k, bool bytes);
 hipError_t launch_gemv_q4_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_q4_lean_bytes(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 size_t gemm_lds_bytes(int fmt, const GemmPlan& p, int k);
 hipError_t launch_gemm(const GemmCall& c, const GemmPlan& p, hipStream_t stream);
 hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int64_t n, int64_t k, int64_t sw,

@@ -1,12 +1,12 @@
-"""The lean kernels (gemv_tq2.h: 1-3 TQ2_0 columns in dp4a and bytes modes; gemv_q4.hip: 1-3 Q4_0 / IQ4_NL columns in
-dp4a mode) vs the oracle, over every lanes-per-row / chunks-per-lane / column-count instantiation they are built for:
+"""The lean kernels (gemv_tq2.h: 1-3 TQ2_0 columns in dp4a and bytes modes; gemv_q4.h: 1-3 Q4_0 / IQ4_NL columns in
+dp4a mode, Q4_0 in bytes mode too) vs the oracle, over every lanes-per-row / chunks-per-lane / column-count instantiation they are built for:
 S exact, every output of Y within the f32 error bound of the f64 reference_dot, Y independent of whether S is stored,
 and the fused launch bit-identical to quantizer + GEMV.  The Q4_0 / IQ4_NL kernels keep the general kernel's
 accumulation order (whole block dots scaled in f32, lane sums in the same tree), so their Y is also bit-identical to
 the emulated-dp4a mode (which runs the general kernel); the TQ2_0 kernel scales each block in the lane that owns its
 chunk slot, another order of the same terms, so there both Y are checked against the bound and S against each other.
-TQ2_0's bytes mode (every crumb and activation unpacked to a 16-bit integer first) gives the dp4a form's S and Y bit
-for bit.  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
+Bytes mode (every crumb or nibble and activation unpacked to a 16-bit integer first) gives the dp4a form's S and Y
+bit for bit.  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
 wave; padded weight rows and multi-matrix launches too.  Everything goes through the C ABI."""
 
 import numpy as np
@@ -28,6 +28,7 @@ def dev(a):
 
 
 FORMATS = ["tq2_0", "q4_0", "iq4_nl"]
+BYTES_LEAN = ("tq2_0", "q4_0")  # the formats whose lean kernel has a bytes form
 K_TAIL = {"tq2_0": 2816, "q4_0": 2400, "iq4_nl": 2400}  # 11 / 75 blocks: a partial last K step for every layout, nb
 
 
@@ -48,7 +49,7 @@ def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme, m):
     xq, xd, *_ = host.quantize(fmt, x_d)
     y2, s2 = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 2, nw, store_s=True)
     y_emu, s_emu = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 1, nw, store_s=True)  # the general kernel
-    if fmt == "tq2_0":  # bytes mode: the lean kernel's bytes form, the same block dots in the same order
+    if fmt in BYTES_LEAN:  # bytes mode: the lean kernel's bytes form, the same block dots in the same order
         y_b, s_b = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, bn, nb, 0, nw, store_s=True)
         y_bf = host.gemv_f32(fmt, wq_d, ws_d, x_d, n, k, bn, nb, 0, nw)[0]
     torch.cuda.synchronize()
@@ -59,10 +60,11 @@ def test_every_instantiation_matches_oracle(fmt, layout, nb, extreme, m):
     assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
     if fmt == "tq2_0":
         assert outputs_ok(fmt, y_emu.cpu().numpy(), ws, rd, rs, r)
-        assert torch.equal(s_b, s) and torch.equal(y_b.view(torch.int32), y2.view(torch.int32))
-        assert torch.equal(y_bf.view(torch.int32), y.view(torch.int32))
     else:
         assert torch.equal(y.view(torch.int32), y_emu.view(torch.int32))
+    if fmt in BYTES_LEAN:
+        assert torch.equal(s_b, s) and torch.equal(y_b.view(torch.int32), y2.view(torch.int32))
+        assert torch.equal(y_bf.view(torch.int32), y.view(torch.int32))
     assert outputs_ok(fmt, y.cpu().numpy(), ws, rd, rs, r)
 
 
@@ -80,7 +82,7 @@ def test_auto_plans_padded_rows(fmt, shape, fused):
     wq, ws = host.split(fmt, W, n, k)
     wq_pad = dev(np.pad(wq, ((0, 0), (0, 64))))[:, : wq.shape[1]]  # a row stride 64 bytes past the row
     ys = []
-    for mode in (2, 0) if fmt == "tq2_0" else (2,):  # TQ2_0: dp4a and bytes, bit-identical
+    for mode in (2, 0) if fmt in BYTES_LEAN else (2,):  # dp4a and bytes, bit-identical
         if fused:
             y, s = host.gemv_f32(fmt, wq_pad, dev(ws), dev(x), n, k, mode=mode, store_s=True)
         else:
