@@ -1,7 +1,8 @@
 // Decode GEMVs for Q4_0 x q8_0 and TQ2_0 x q8_K on gfx950 (CDNA4), and for the ggml formats Q8_0 and IQ4_NL (x q8_0)
 // and Q4_K (x q8_K) with the same structure (their lanes and dots are described where they are computed).  In dp4a
-// mode, 1-3 Q4_0 / IQ4_NL columns run the lean kernel of gemv_q4.hip instead, and 1-3 TQ2_0 columns (dp4a and bytes
-// modes) that of gemv_tq2.h, which take the same plans and give the same S (and Y within the same bound).
+// mode, 1-3 Q4_0 / IQ4_NL columns run the lean kernel of gemv_q4.h instead (Q4_0 in bytes mode too), and 1-3 TQ2_0
+// columns (dp4a and bytes modes) that of gemv_tq2.h, which take the same plans and give the same S (and Y within the
+// same bound).
 //
 // Replaces the reference's Triton kernels src/komp/kernels.py:48-94 (q4_0_gemv) and :97-142 (tq2_0_gemv).
 //
