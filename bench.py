@@ -38,6 +38,7 @@ if ROOT not in sys.path:
 
 METRIC = "GEMV µs/call + achieved HBM GB/s (% of peak), Q4_0 & TQ2_0 decode shapes"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MODE_NAMES = {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}
 COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infinity Cache)
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
@@ -296,7 +297,7 @@ def headline(torch, host, abi, args):
                 "read_floor_us": round(read_floor_us(torch, host, int(launch_b)), 3)}  # fmt: skip
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
                           "activations quantized to q8_K inside each launch",  # fmt: skip
-              "shapes_nk": [list(s) for s in shapes], "m": m, "mode": {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}[args.mode],
+              "shapes_nk": [list(s) for s in shapes], "m": m, "mode": MODE_NAMES[args.mode],
               "plan_rows_nb_waves_lanes_passes": plans, "cold_copies": ncopies, "seed": args.seed,
               "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3), "us_per_step_graph": round(ms_per_step * 1e3, 3),
               "gemv_us_per_call_dispatch": round(g_us, 3),
@@ -470,7 +471,7 @@ def config_detail(torch, host, args):
                     us = ms_t * 1e3 / reps
                     gemm = knobs is None and host.uses_gemm(fmt, m, n, k, mode=mode)
                     rows.append({"config": cfg, "fmt": fmt, "n": n, "k": k, "m": m,
-                                 "mode": {0: "bytes", 2: "dp4a"}[mode],
+                                 "mode": MODE_NAMES[mode],
                                  "knobs": list(knobs) if knobs else "library plan",
                                  "path": "gemm" if gemm else "gemv", "outliers": outliers, "bytes": b,
                                  "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
@@ -655,22 +656,24 @@ def batched_calls(torch, host, args):
     return rows
 
 
-COUNTER_CASES = (  # (fmt, N, K, columns, launch): the kernels the hardware-counter tables cover
-    ("tq2_0", 6912, 2560, 1, "fused"), ("tq2_0", 2560, 6912, 1, "fused"),
-    ("tq2_0", 6912, 2560, 3, "fused"), ("tq2_0", 2560, 6912, 3, "fused"),
-    ("tq2_0", 32768, 8192, 1, "gemv"), ("q4_0", 4096, 14336, 1, "gemv"), ("q4_0", 4096, 14336, 3, "gemv"),
-    ("q4_0", 128256, 4096, 1, "gemv"), ("q4_0", 14336, 4096, 64, "gemm"),
+COUNTER_CASES = (  # (fmt, N, K, columns, launch, mode): the kernels the hardware-counter tables cover
+    ("tq2_0", 6912, 2560, 1, "fused", 2), ("tq2_0", 2560, 6912, 1, "fused", 2),
+    ("tq2_0", 6912, 2560, 3, "fused", 2), ("tq2_0", 2560, 6912, 3, "fused", 2),
+    ("tq2_0", 32768, 8192, 1, "gemv", 2), ("q4_0", 4096, 14336, 1, "gemv", 2), ("q4_0", 4096, 14336, 3, "gemv", 2),
+    ("q4_0", 128256, 4096, 1, "gemv", 2), ("q4_0", 14336, 4096, 64, "gemm", 2),
+    # bytes mode (every value unpacked to an integer, no dot instruction) beside dp4a
+    ("tq2_0", 6912, 2560, 1, "fused", 0), ("tq2_0", 32768, 8192, 1, "gemv", 0), ("q4_0", 4096, 14336, 1, "gemv", 0),
 )  # fmt: skip
 
 
 def counter_calls(torch, host, args):
-    """COUNTER_CASES, args.counter_calls eager launches each over cold weight copies, untimed (library plans, dp4a;
-    fused = f32 activations quantized inside the launch, gemv / gemm = q8 activations in): the dispatches one
-    rocprofv3 --pmc pass reads."""
+    """COUNTER_CASES, args.counter_calls eager launches each over cold weight copies, untimed (library plans, the
+    case's mode; fused = f32 activations quantized inside the launch, gemv / gemm = q8 activations in): the dispatches
+    one rocprofv3 --pmc pass reads."""
     rows = []
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed + 6)
-    for fmt, n, k, m, launch in COUNTER_CASES:
+    for fmt, n, k, m, launch, mode in COUNTER_CASES:
         copies = weight_copies(fmt, n, k, gen, torch, COLD_BYTES // 2)
         x = torch.randn((m, k), generator=gen, device="cuda")
         xq, xd = host.quantize(fmt, x)
@@ -678,13 +681,14 @@ def counter_calls(torch, host, args):
         for i in range(args.counter_calls):
             wq, ws = copies[i % len(copies)]
             if launch == "fused":
-                host.gemv_f32_into(fmt, wq, ws, x, y, n, k)
+                host.gemv_f32_into(fmt, wq, ws, x, y, n, k, None, 0, mode, 0)
             elif launch == "gemm":
                 host.gemm_into(fmt, wq, ws, xq, xd, y, n, k)
             else:
-                host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, 2, 0)
+                host.gemv_into(fmt, wq, ws, xq, xd, y, n, k, None, 0, mode, 0)
         torch.cuda.synchronize()
-        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "launch": launch, "calls": args.counter_calls,
+        rows.append({"fmt": fmt, "n": n, "k": k, "m": m, "launch": launch, "mode": MODE_NAMES[mode],
+                     "calls": args.counter_calls,
                      "bytes": step_bytes_fused(fmt, n, k, m) if launch == "fused" else gemv_bytes(fmt, n, k, m)})
         del copies
         torch.cuda.empty_cache()

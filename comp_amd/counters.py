@@ -10,7 +10,8 @@ order) or a file holding it.  The GEMV and GEMM dispatches of every pass are tak
 (the quantizer dispatches of the q8 launches are skipped), the passes zipped dispatch by dispatch, and each counter
 averaged over a case's dispatches.  Per weight = instructions x 64 lanes / (N x K): the whole kernel's instructions,
 staging, reductions and stores included.  `dot4` is the exact integer work the format defines: 0.25 v_dot4 per weight
-and column (4 products an instruction), the floor of the dp4a path; the VALU figure includes it.
+and column (4 products an instruction), the floor of the dp4a path; the VALU figure includes it.  A case may name its
+mode ("dp4a", the default, or "bytes": no dot instruction, so 0 there).
 """
 
 from __future__ import annotations
@@ -20,7 +21,8 @@ import json
 import os
 
 # kernel families that make one GEMV / GEMM call (the quantizer and the copies of the weight rotation are not counted)
-FAMILIES = ("tq2_lean_kernel", "q4_lean_kernel", "gemv_kernel", "gemm_kernel")
+FAMILIES = ("tq2_lean_kernel", "tq2_lean_bytes_kernel", "q4_lean_kernel", "q4_lean_bytes_kernel", "gemv_kernel",
+            "gemm_kernel")
 
 
 def _family(name):
@@ -70,9 +72,11 @@ def table(dispatches, cases):
         keys = sorted({k for d in ds for k in d["counters"]})
         avg = {k: sum(d["counters"].get(k, 0.0) for d in ds) / len(ds) for k in keys}
         weights = case["n"] * case["k"]
+        mode = case.get("mode", "dp4a")
+        dots = case["launch"] != "gemm" and mode != "bytes"
         row = {"fmt": case["fmt"], "n": case["n"], "k": case["k"], "m": case["m"], "launch": case["launch"],
-               "kernel": ds[0]["kernel"], "grid": ds[0]["grid"], "wg": ds[0]["wg"], "dispatches": len(ds),
-               "dot4_per_weight": 0.25 * case["m"] if case["launch"] != "gemm" else 0.0}  # fmt: skip
+               "mode": mode, "kernel": ds[0]["kernel"], "grid": ds[0]["grid"], "wg": ds[0]["wg"],
+               "dispatches": len(ds), "dot4_per_weight": 0.25 * case["m"] if dots else 0.0}  # fmt: skip
         waves = avg.get("SQ_WAVES")
         for name, key in (("valu", "SQ_INSTS_VALU"), ("salu", "SQ_INSTS_SALU"), ("vmem", "SQ_INSTS_VMEM_RD"),
                           ("lds", "SQ_INSTS_LDS"), ("mfma", "SQ_INSTS_MFMA")):  # fmt: skip
@@ -102,7 +106,7 @@ def markdown(rows):
         return fmt.format(r[k]) if k in r else "-"
 
     for r in rows:
-        label = f"{r['fmt']} {r['n']}x{r['k']}, m={r['m']}, {r['launch']}"
+        label = f"{r['fmt']} {r['n']}x{r['k']}, m={r['m']}, {r['launch']}" + (", bytes" if r["mode"] == "bytes" else "")
         out.append(f"| {label} | `{r['kernel']}` | {f(r, 'waves', '{:.0f}')} | {f(r, 'valu_per_wave', '{:.1f}')} | "
                    f"{f(r, 'valu_per_weight')} | {r['dot4_per_weight']:.2f} | {f(r, 'salu_per_weight')} | "
                    f"{f(r, 'vmem_per_weight', '{:.3f}')} | {f(r, 'lds_per_weight', '{:.3f}')} | "

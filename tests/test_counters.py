@@ -67,3 +67,16 @@ def test_cli_prints_the_table(tmp_path, capsys):
     out = capsys.readouterr().out
     assert "tq2_0 256x2560, m=1, fused" in out and "| 6.4 |" in out
     assert cli.main(["counters", str(a)]) == 2
+
+
+def test_bytes_mode_case_names_its_kernel_and_has_no_dot4(tmp_path):
+    a = tmp_path / "a.csv"
+    name = "void komp::gemv_tq2::tq2_lean_bytes_kernel<16, 4, 1, true, true>(int, int)"
+    with open(a, "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Grid_Size", "Workgroup_Size", "Counter_Name", "Counter_Value"])
+        w.writerow([1, name, 16384, 448, "SQ_INSTS_VALU", 3200])
+    case = {"fmt": "tq2_0", "n": 256, "k": 2560, "m": 1, "launch": "fused", "mode": "bytes", "calls": 1}
+    (r,) = counters.table(counters.read_pass(a), [case])
+    assert r["kernel"] == "tq2_lean_bytes_kernel<16, 4, 1, true, true>" and r["dot4_per_weight"] == 0.0
+    assert "m=1, fused, bytes" in counters.markdown([r])
