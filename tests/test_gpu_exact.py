@@ -127,3 +127,35 @@ def test_gemm_bit_exact(fmt):
     torch.cuda.synchronize()
     assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
     assert bits_equal(y.cpu().numpy(), r), f"{fmt}: GEMM Y differs from the exact value"
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
+@pytest.mark.parametrize("act", [-128, 127])
+@pytest.mark.parametrize("m", [1, 3])
+def test_bytes_mode_sums_at_their_largest(fmt, act, m):
+    """The largest integer dots the formats allow: every nibble 15 (Q4_0 value +7) or every crumb 3 (TQ2_0 value
+    +2) against activations all -128 or all 127, q8 bytes given directly (the quantizers never produce -128; the C ABI
+    takes any bytes).  Bytes mode keeps 16-bit partial sums (at most 16 Q4_0 products of 15 x 128 or 32 TQ2_0 products
+    of 3 x 128 in a half), so this is where they would overflow: S must equal the exact dots in every mode, on the lean
+    and general kernels, and Y the exact reference."""
+    n, k = 300, K[fmt]
+    blk, qb = (32, 16) if fmt == "q4_0" else (256, 64)
+    nb = k // blk
+    wq = np.full((n, nb * qb), 0xFF, np.uint8)
+    ws = np.full((n, nb), 0x3C00, np.uint16).view(np.int16)  # d_w = 1
+    xq = np.full((m, k), act, np.int8)
+    xd = np.full((m, nb), 0.5, np.float32)
+    r, rs = O.gemv(fmt, wq, ws, xq, xd, n, k)
+    assert (rs == (7 if fmt == "q4_0" else 2) * act * blk).all()  # the oracle's decode: nibble 15 -> 7, crumb 3 -> 2
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    wq_d, ws_d, xq_d, xd_d = dev(wq), dev(ws), dev(xq), dev(xd)
+    runs = []
+    for mode in (0, 1, 2):  # bytes, emulated dp4a (the general kernel), dp4a
+        for bn, nb_, nw in ((None, 4, 4), (64, 1, 4), (16, 4, 4)):  # auto (lean), knob sets (lean / general)
+            print(f"{fmt} act={act} m={m} mode={mode} block_n={bn} nb={nb_} num_warps={nw}", flush=True)
+            runs.append((mode, host.gemv(fmt, wq_d, ws_d, xq_d, xd_d, n, k, bn, nb_, mode, nw, store_s=True)))
+    torch.cuda.synchronize()
+    for mode, (y, s) in runs:
+        assert np.array_equal(s.cpu().numpy().astype(np.int64), rs), mode
+        # every term and partial sum is an integer below 2**24, exact in f32: Y equals the reference in any order
+        assert np.array_equal(y.cpu().numpy().astype(np.float64), r), mode
