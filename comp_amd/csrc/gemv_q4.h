@@ -313,7 +313,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   // the single-pass, single-step form for one column (the decode case; two and three columns keep the general one)
   const bool one = MC == 1 && p.passes == 1 && c.k / 32 <= G * NB;
   auto kern = one ? q4_lean_kernel<FMT, G, NB, MC, FUSED, MC == 1> : q4_lean_kernel<FMT, G, NB, MC, FUSED, false>;
-  if constexpr (BYTES) kern = one ? q4_lean_bytes_kernel<G, NB, MC, FUSED, MC == 1> : q4_lean_bytes_kernel<G, NB, MC, FUSED, false>;
+  if constexpr (BYTES)
+    kern = one ? q4_lean_bytes_kernel<G, NB, MC, FUSED, MC == 1> : q4_lean_bytes_kernel<G, NB, MC, FUSED, false>;
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {

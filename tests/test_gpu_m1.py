@@ -1,13 +1,14 @@
 """The lean kernels (gemv_tq2.h: 1-3 TQ2_0 columns in dp4a and bytes modes; gemv_q4.h: 1-3 Q4_0 / IQ4_NL columns in
-dp4a mode, Q4_0 in bytes mode too) vs the oracle, over every lanes-per-row / chunks-per-lane / column-count instantiation they are built for:
-S exact, every output of Y within the f32 error bound of the f64 reference_dot, Y independent of whether S is stored,
-and the fused launch bit-identical to quantizer + GEMV.  The Q4_0 / IQ4_NL kernels keep the general kernel's
-accumulation order (whole block dots scaled in f32, lane sums in the same tree), so their Y is also bit-identical to
-the emulated-dp4a mode (which runs the general kernel); the TQ2_0 kernel scales each block in the lane that owns its
-chunk slot, another order of the same terms, so there both Y are checked against the bound and S against each other.
-Bytes mode (every crumb or nibble and activation unpacked to a 16-bit integer first) gives the dp4a form's S and Y
-bit for bit.  Shapes leave a partial last workgroup, a partial last K step and (with 128 rows over 4 waves) two passes per
-wave; padded weight rows and multi-matrix launches too.  Everything goes through the C ABI."""
+dp4a mode, Q4_0 in bytes mode too) vs the oracle, over every lanes-per-row / chunks-per-lane / column-count
+instantiation they are built for: S exact, every output of Y within the f32 error bound of the f64 reference_dot, Y
+independent of whether S is stored, and the fused launch bit-identical to quantizer + GEMV.  The Q4_0 / IQ4_NL
+kernels keep the general kernel's accumulation order (whole block dots scaled in f32, lane sums in the same tree), so
+their Y is also bit-identical to the emulated-dp4a mode (which runs the general kernel); the TQ2_0 kernel scales each
+block in the lane that owns its chunk slot, another order of the same terms, so there both Y are checked against the
+bound and S against each other.  Bytes mode (every crumb or nibble and activation unpacked to a 16-bit integer first)
+gives the dp4a form's S and Y bit for bit.  Shapes leave a partial last workgroup, a partial last K step and (with 128
+rows over 4 waves) two passes per wave; padded weight rows and multi-matrix launches too.  Everything goes through the
+C ABI."""
 
 import numpy as np
 import pytest

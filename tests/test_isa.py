@@ -40,8 +40,9 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     assert cli._gemv_kernel(fmt, 2, nb, 3, bn, nw) == three  # three columns
     assert cli._gemv_kernel(fmt, 2, 8, 3, bn, nw).startswith("gemv_impl::gemv_kernel<")  # nb 8 at three columns
     if fmt in ("tq2_0", "q4_0"):  # bytes mode: the lean kernel's bytes form, with no dot instruction
-        bytes_name = (name.replace("tq2_lean_kernel<", "tq2_lean_bytes_kernel<").replace(", false, false, false>", ", false, false>")
-                      .replace("q4_lean_kernel<0, ", "q4_lean_bytes_kernel<"))  # fmt: skip
+        bytes_name = (name.replace("tq2_lean_kernel<", "tq2_lean_bytes_kernel<")
+                      .replace(", false, false, false>", ", false, false>")
+                      .replace("q4_lean_kernel<0, ", "q4_lean_bytes_kernel<"))
         assert cli._gemv_kernel(fmt, 0, nb, 1, bn, nw) == bytes_name
         r = isa.summary(bytes_name, cli.VALUES_PER_LOAD[fmt])
         assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"] and r["dot4_total"] == 0
