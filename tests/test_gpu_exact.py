@@ -129,6 +129,7 @@ def test_gemm_bit_exact(fmt):
     assert bits_equal(y.cpu().numpy(), r), f"{fmt}: GEMM Y differs from the exact value"
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "tq2_0"])
 @pytest.mark.parametrize("act", [-128, 127])
 @pytest.mark.parametrize("m", [1, 3])
