@@ -11,16 +11,21 @@ p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), the input N(0, 1), all resident in HBM be
 served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-graph replays, so the host launch rate
 does not bound them.
 
-Printed: one JSON line.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in + f32 outputs)
-/ their wall time (GB/s); roofline = the fused tq2_0_gemv launches' algorithmic bytes / their average duration over the
-timed region (events around the graph replays / launches; dispatch_us beside it is each dispatch timed alone with
-hipExtLaunchKernel events, the clock rocprofv3 --kernel-trace reads); cpu_baseline = the C oracle (the reference's arithmetic restated) on a bounded
-sample of the same steps on this host; detail = per-shape GEMV us/call and GB/s for the Q4_0 / TQ2_0 shape list and
-Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs); configs = every configuration of the workload
-list in the modes (dp4a, bytes) and knob sets it names; multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one
-gemv_multi launch against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B
-(Q4_0, and 14336 x 4096 in Q8_0, IQ4_NL and Q4_K) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against
-GEMV launches of 3 columns; ingest = ggml block bytes split into the planes on the device.
+Printed: one JSON line of a few KB.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in +
+f32 outputs) / their wall time (GB/s); roofline = the fused tq2_0_gemv launches' algorithmic bytes / their average
+in-graph span (first wave's entry to last wave's stored outputs, from the library's wave stamps over a graph of the same
+steps; events_us beside it is the events around the timed replays / the launches, gaps between dispatches included,
+and dispatch_us each dispatch timed alone with hipExtLaunchKernel events); cpu_baseline = the C oracle (the
+reference's arithmetic restated) on a bounded sample of the same steps on this host; configs = every configuration of
+the workload list in the modes (dp4a, bytes) and knob sets it names, one compact row each (us/call, GB/s, % of peak,
+streaming-read floor / GEMV).
+
+Written to --detail-out (default gpurun_out/bench_detail.json): the same line plus detail = per-shape GEMV us/call and
+GB/s for the Q4_0 / TQ2_0 shape list and Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs);
+configs in full; multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one gemv_multi launch
+against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B (Q4_0, and 14336 x
+4096 in Q8_0, IQ4_NL and Q4_K) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3
+columns; ingest = ggml block bytes split into the planes on the device.
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ if ROOT not in sys.path:
 METRIC = "GEMV µs/call + achieved HBM GB/s (% of peak), Q4_0 & TQ2_0 decode shapes"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
 MODE_NAMES = {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}
+SUBMIT_COVER_CYCLES = 2_000_000  # torch.cuda._sleep length (~1 ms): covers the host's submission of the timed replays
 COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infinity Cache)
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
@@ -173,6 +179,9 @@ def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
         g_full.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # a bounded spin kernel ahead of the start event keeps the GPU busy while the host submits the replays, so the
+    # timed region holds the K steps back to back and not the host's submission of the first graph
+    torch.cuda._sleep(SUBMIT_COVER_CYCLES)
     t0 = time.perf_counter()
     e0.record()
     for _ in range(steps // per_graph):
@@ -213,6 +222,60 @@ def dispatch_times(abi, torch, step, count):
         step(i)
     torch.cuda.synchronize()
     return abi.timing_end()
+
+
+PHASES = ("entry", "staged", "dots", "stored")
+
+
+def stamped_spans(torch, abi, step, ncopies, replays=4):
+    """In-graph kernel spans from the library's wave stamps (komp_stamps_begin / komp_stamps_end): one graph of
+    ncopies steps is captured with stamping on (the TQ2_0 dp4a one-pass launches then run their stamped
+    instantiation, which reads the real-time counter in every wave on entry, once the staged activations are
+    published, after its last weight chunk's dot and once its outputs are stored), replayed `replays` times after one
+    warm replay, and the last replay's records read back.  -> (per-shape summary, us per step of the stamped replays)
+    with, per (N, K): launches, span_us (mean of last stored - first entry), and each phase's median and 95th
+    percentile over the waves (ns from the launch's first entry), averaged over the launches."""
+    import numpy as np
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(ncopies, 2)):
+            step(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    buf = torch.zeros(8 << 20, dtype=torch.int32, device="cuda")  # 32 MiB of records
+    g = torch.cuda.CUDAGraph()
+    abi.stamps_begin(buf)
+    try:
+        with torch.cuda.graph(g):
+            for i in range(ncopies):
+                step(i)
+    finally:
+        used, khz = abi.stamps_end()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_step = e0.elapsed_time(e1) * 1e3 / (replays * ncopies)
+    recs = abi.parse_stamps(buf[:used].cpu().numpy().view(np.uint32), khz)
+    del g, buf
+    shapes = {}
+    for r in recs:
+        shapes.setdefault((r["n"], r["k"]), []).append(r)
+    out = {}
+    for (n, k), rs in shapes.items():
+        row = {"launches": len(rs), "waves": rs[0]["waves"],
+               "span_us": round(float(np.mean([r["span_ns"] for r in rs])) / 1e3, 3)}  # fmt: skip
+        for ph in PHASES:
+            row[ph + "_ns_median_p95"] = [round(float(np.mean([np.median(r[ph]) for r in rs]))),
+                                          round(float(np.mean([np.percentile(r[ph], 95) for r in rs])))]  # fmt: skip
+        out[f"{n}x{k}"] = row
+    return out, us_step
 
 
 def step_bytes_fused(fmt, n, k, m):
@@ -284,15 +347,25 @@ def headline(torch, host, abi, args):
     g_ms, g_n = disp["tq2_0_gemv"]
     launch_b = step_bytes / len(shapes)
     g_us = g_ms * 1e3 / g_n
-    # the kernel's average launch duration over the timed region: torch events around the graph replays (on the stream
-    # the kernels are launched on) / the launches in them; the eager per-dispatch events beside it (dispatch_us) read
-    # 4.5-5.4 us from run to run, since an eager launch leaves the GPU idle in between
-    launch_us = ms_per_step * 1e3 / len(shapes)
+    # The kernel's average duration: its in-graph span (first wave's entry to last wave's stored outputs, from the
+    # wave stamps of a graph of the same steps), averaged over both shapes' launches.  Beside it: the events around
+    # the timed replays / the launches in them (gaps between dispatches included), and each dispatch timed alone
+    # with hipExtLaunchKernel events (an eager launch leaves the GPU idle in between).
+    spans, us_step_stamped = stamped_spans(torch, abi, step, ncopies)
+    events_us = ms_per_step * 1e3 / len(shapes)
+    if len(spans) == len(shapes):
+        launch_us, timing = sum(v["span_us"] for v in spans.values()) / len(spans), "wave stamps (in-graph span)"
+    else:  # no stamped instantiation for this mode / plan: the events' share of the step
+        launch_us, timing = events_us, "events over the timed replays / launches"
     achieved = launch_b / (launch_us * 1e-6) / 1e9
     default_cfg = m == 1 and args.mode == 2 and args.block_n is None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": TRAFFIC_FUSED_BITNET_M1 if default_cfg else None,
-                "kernel": "tq2_0_gemv (fused quantize)", "launch_us": round(launch_us, 3),
+                "traffic_source": "profiles/tq2_0_gemv_bitnet2b_decode_chain.md (rocprofv3 --pmc FETCH_SIZE + "
+                                  "WRITE_SIZE, scaled by a copy kernel's readings; not measured in this run)",
+                "kernel": "tq2_0_gemv (fused quantize)", "launch_us": round(launch_us, 3), "launch_timing": timing,
+                "stamps": spans,
+                "events_us": round(events_us, 3), "stamped_us_per_step": round(us_step_stamped, 3),
                 "dispatch_us": round(g_us, 3), "bytes_per_launch": int(launch_b),
                 "read_floor_us": round(read_floor_us(torch, host, int(launch_b)), 3)}  # fmt: skip
     config = {"workload": "tq2_0 decode chain at BitNet-2B FFN shapes: x[m][2560] -> W1[6912x2560] -> W2[2560x6912], "
@@ -480,6 +553,18 @@ def config_detail(torch, host, args):
         del copies
         torch.cuda.empty_cache()
     return rows
+
+
+def config_summary(rows):
+    """The configs rows in compact form for the result line: {"<config> <fmt> <N>x<K>": {"m<M> <mode> <knobs>":
+    [us/call, GB/s, % of 8 TB/s, read floor / GEMV]}}, knobs "lib" for the library's plan, else block_n/nb/waves."""
+    out = {}
+    for r in rows:
+        key = f"{r['config']} {r['fmt']} {r['n']}x{r['k']}"
+        knobs = "lib" if r["knobs"] == "library plan" else "/".join(str(v) for v in r["knobs"])
+        out.setdefault(key, {})[f"m{r['m']} {r['mode']} {knobs}"] = [
+            round(r["us_per_call"], 2), round(r["gbs"]), round(r["pct_peak"], 1), round(r["of_read_floor"], 2)]
+    return out
 
 
 MULTI_CASES = (  # (name, fmt, [rows per matrix], K): projections stored as separate tensors that share one input
@@ -707,6 +792,9 @@ def main():
     ap.add_argument("--num-warps", type=int, default=4)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--detail-out", default=os.path.join("gpurun_out", "bench_detail.json"), metavar="PATH",
+                    help="where the full per-shape tables (detail, configs, multi_matrix, batched_gemm, ingest) go "
+                         "(empty: not written); the result line carries a compact row per workload configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0,
@@ -765,12 +853,17 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args, step_bytes, args.cpu_seconds)
     if not args.no_detail:
-        out["detail"] = detail(torch, host, _abi, args)
-        out["configs"] = config_detail(torch, host, args)
-        out["multi_matrix"] = multi_detail(torch, host, args)
-        out["batched_gemm"] = batched_detail(torch, host, args)
-        out["ingest"] = ingest_detail(torch, host, args)
-    print(json.dumps(out), flush=True)
+        full = {"detail": detail(torch, host, _abi, args), "configs": config_detail(torch, host, args),
+                "multi_matrix": multi_detail(torch, host, args), "batched_gemm": batched_detail(torch, host, args),
+                "ingest": ingest_detail(torch, host, args)}  # fmt: skip
+        out["configs"] = config_summary(full["configs"])
+        if args.detail_out:
+            os.makedirs(os.path.dirname(os.path.abspath(args.detail_out)), exist_ok=True)
+            with open(args.detail_out, "w") as f:
+                json.dump({**out, **full, "configs_summary": out["configs"]}, f, indent=1)
+            out["detail_file"] = args.detail_out
+    # the result line stays a few KB (the per-shape tables go to the detail file)
+    print(json.dumps(out, separators=(",", ":")), flush=True)
     return 0
 
 

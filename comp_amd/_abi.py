@@ -70,6 +70,8 @@ SIGNATURES = {
     "komp_tq2_0_decode": (_INT, [_P, _P, _I64, _P]),
     "komp_timing_begin": (_INT, [_I64]),
     "komp_timing_end": (_INT, [_P, _P]),
+    "komp_stamps_begin": (_INT, [_P, _I64]),
+    "komp_stamps_end": (_INT, [_P, _P]),
 }
 ABI_VERSION = 1
 
@@ -144,3 +146,41 @@ def timing_end():
     cnt = (ctypes.c_int64 * len(TIMING_KINDS))()
     call("komp_timing_end", ms, cnt)
     return {k: (ms[i], cnt[i]) for i, k in enumerate(TIMING_KINDS)}
+
+
+STAMP_MAGIC = 0x4B535450
+
+
+def stamps_begin(buf):
+    """Start recording wave stamps into `buf`, a 16-byte aligned int32 / uint32 device tensor (komp_stamps_begin)."""
+    call("komp_stamps_begin", ctypes.c_void_p(buf.data_ptr()), buf.numel())
+
+
+def stamps_end():
+    """-> (words used, counter rate in kHz) (komp_stamps_end)."""
+    used, khz = ctypes.c_int64(0), ctypes.c_int(0)
+    call("komp_stamps_end", ctypes.byref(used), ctypes.byref(khz))
+    return used.value, khz.value
+
+
+def parse_stamps(words, clock_khz):
+    """Records of a stamp buffer (uint32 numpy array, the words komp_stamps_end reported) -> one dict per launch:
+    n, k, waves, and for each of entry / staged / dots / stored the per-wave times in ns from the launch's first
+    entry (int64 arrays), plus span_ns = last stored - first entry."""
+    import numpy as np
+
+    words = np.asarray(words, dtype=np.uint32)
+    ns_per_tick = 1e6 / clock_khz
+    out, off = [], 0
+    while off + 4 <= words.size:
+        magic, waves, n, k = (int(v) for v in words[off:off + 4])
+        if magic != STAMP_MAGIC:
+            raise KompError(f"stamp buffer: no launch header at word {off}")
+        rec = words[off + 4:off + 4 + 4 * waves].reshape(waves, 4).astype(np.int64)
+        rel = (rec - rec[0, 0] + (1 << 31)) % (1 << 32) - (1 << 31)  # the counter's low words, wrap-safe
+        rel -= rel[:, 0].min()
+        t = rel * ns_per_tick
+        out.append({"n": n, "k": k, "waves": waves, "entry": t[:, 0], "staged": t[:, 1], "dots": t[:, 2],
+                    "stored": t[:, 3], "span_ns": float(t[:, 3].max())})
+        off += (4 + 4 * waves + 3) & ~3
+    return out

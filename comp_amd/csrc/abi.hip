@@ -56,6 +56,16 @@ struct TimingState {
 };
 TimingState g_timing;
 
+// ---- in-kernel wave stamps ------------------------------------------------------------------------------------------
+struct StampState {
+  std::mutex mu;
+  std::atomic<bool> on{false};
+  uint32_t* buf = nullptr;
+  int64_t words = 0;
+  int64_t used = 0;
+};
+StampState g_stamps;
+
 // ---- auto plan ------------------------------------------------------------------------------------------------------
 // The plan gemv uses when block_n == 0.
 //   Throughput regime (N >= 16384 rows, several workgroups per CU; one unfused Q4_0 / IQ4_NL column from 12288).  Each
@@ -482,6 +492,17 @@ Timing timing_slot(int kind) {
   return t;
 }
 
+bool stamps_on() { return g_stamps.on.load(std::memory_order_relaxed); }
+
+uint32_t* stamp_slot(int64_t words) {
+  if (!stamps_on()) return nullptr;
+  std::lock_guard<std::mutex> lock(g_stamps.mu);
+  if (!g_stamps.on || words <= 0 || g_stamps.used + words > g_stamps.words) return nullptr;
+  uint32_t* p = g_stamps.buf + g_stamps.used;
+  g_stamps.used += (words + 3) & ~int64_t{3};  // the next launch's header stays 16-byte aligned
+  return p;
+}
+
 }  // namespace komp
 
 using namespace komp;
@@ -761,6 +782,32 @@ int komp_timing_end(double* ms, int64_t* count) {
     if (count) count[kd] += 1;
   }
   g_timing.used = 0;
+  return KOMP_OK;
+}
+
+int komp_stamps_begin(uint32_t* buf, int64_t words) {
+  if (words < 0 || (words > 0 && (buf == nullptr || !aligned(buf, 16))))
+    return fail(KOMP_EINVAL, "komp_stamps_begin: buf must be 16-byte aligned and words >= 0");
+  std::lock_guard<std::mutex> lock(g_stamps.mu);
+  g_stamps.buf = buf;
+  g_stamps.words = words;
+  g_stamps.used = 0;
+  g_stamps.on = true;
+  return KOMP_OK;
+}
+
+int komp_stamps_end(int64_t* words_used, int* clock_khz) {
+  std::lock_guard<std::mutex> lock(g_stamps.mu);
+  g_stamps.on = false;
+  if (words_used) *words_used = g_stamps.used;
+  g_stamps.buf = nullptr;
+  g_stamps.words = g_stamps.used = 0;
+  if (clock_khz) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(clock_khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess) return hip_status(e, "komp_stamps_end");
+  }
   return KOMP_OK;
 }
 

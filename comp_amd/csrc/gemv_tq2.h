@@ -130,7 +130,11 @@ __device__ __forceinline__ int quad_scatter2(int p0, int p1, uint64_t odd) {
 // straight-line code with no loop and no reload: a launch starts with a cold instruction cache, and every 64-byte
 // line of code on the way to the first dot costs tens of nanoseconds of fetch.
 // BYTES: bytes mode (the activations staged as 16-bit integers, chunk_dot_bytes); otherwise dp4a (chunk_dot16).
-template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES>
+// STAMP: the measurement instantiation.  Each wave reads the real-time counter on entry, once the staged columns are
+// published, after its last weight chunk's dot and after its outputs are stored (their stores complete), and lane 0
+// writes the four low words to segs.stamps[4 + 4 * (blockIdx.x * waves + wave)]; thread 0 of workgroup 0 writes the
+// header {kStampMagic, waves of the grid, N, K}.  Scheduling barriers keep each reading in its place.
+template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES, bool STAMP = false>
 __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
                                               const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
                                               const void* __restrict__ XA, const float* __restrict__ XD,
@@ -143,6 +147,11 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
   constexpr int XB = kBlockStride;
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x;
+  uint64_t t_entry = 0, t_staged = 0, t_dots = 0;
+  if constexpr (STAMP) {
+    t_entry = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // ---- the staging's first loads (16 threads per block), issued first: they need only preloaded arguments, so they
   // go out before anything else (the segment table of a multi-matrix launch included) and do not queue behind the
   // weights.  f32 values 16i .. 16i + 15 (fused) or q8 bytes 16i .. 16i + 15 and d_x (unfused) of the flattened
@@ -377,6 +386,11 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left as they are
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  if constexpr (STAMP) {
+    __builtin_amdgcn_sched_barrier(0);
+    t_staged = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // ---- stream the weights ----
   const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
@@ -423,6 +437,11 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
           asm volatile("" : "+v"(pd[m][u]));
         }
       }
+      if constexpr (STAMP) {  // the last step's dots issued
+        __builtin_amdgcn_sched_barrier(0);
+        t_dots = __builtin_amdgcn_s_memrealtime();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       // lane q completes and scales the blocks of slots q, q + 4: the exact dot s = the quad's sum (/ 16) - sum(x), then
       // d_x * d_w * f32(s) (kernels.py:141 order)
 #pragma unroll
@@ -456,6 +475,22 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
       if ((lane & (LPR - 1)) == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
     }
   }
+  if constexpr (STAMP) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the wave's stores have completed
+    __builtin_amdgcn_sched_barrier(0);
+    const uint64_t t_stored = __builtin_amdgcn_s_memrealtime();
+    u32x4* rec = reinterpret_cast<u32x4*>(segs.stamps);
+    const unsigned wpg = static_cast<unsigned>(nthreads) >> 6;
+    if (lane == 0) {
+      const u32x4 v = {static_cast<unsigned>(t_entry), static_cast<unsigned>(t_staged), static_cast<unsigned>(t_dots),
+                       static_cast<unsigned>(t_stored)};
+      rec[1 + blockIdx.x * wpg + static_cast<unsigned>(wave)] = v;
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+      const u32x4 h = {kStampMagic, gridDim.x * wpg, static_cast<unsigned>(N1), static_cast<unsigned>(nblk) * 256u};
+      rec[0] = h;
+    }
+  }
 }
 
 #define KOMP_TQ2_LEAN_ARGS                                                                                        \
@@ -470,6 +505,12 @@ __global__ void __launch_bounds__(1024) tq2_lean_kernel(KOMP_TQ2_LEAN_ARGS) {
   tq2_lean_body<LPR, NB, MC, FUSED, ONE, DMA, false>(KOMP_TQ2_LEAN_PASS);
 }
 
+// The stamped single-pass, single-step dp4a form (STAMP above): the measurement instantiation of the tuning harness.
+template <int LPR, int NB, int MC, bool FUSED>
+__global__ void __launch_bounds__(1024) tq2_lean_stamped_kernel(KOMP_TQ2_LEAN_ARGS) {
+  tq2_lean_body<LPR, NB, MC, FUSED, true, false, false, true>(KOMP_TQ2_LEAN_PASS);
+}
+
 template <int LPR, int NB, int MC, bool FUSED, bool ONE>
 __global__ void __launch_bounds__(1024) tq2_lean_bytes_kernel(KOMP_TQ2_LEAN_ARGS) {
   tq2_lean_body<LPR, NB, MC, FUSED, ONE, false, true>(KOMP_TQ2_LEAN_PASS);
@@ -478,16 +519,25 @@ __global__ void __launch_bounds__(1024) tq2_lean_bytes_kernel(KOMP_TQ2_LEAN_ARGS
 #undef KOMP_TQ2_LEAN_ARGS
 #undef KOMP_TQ2_LEAN_PASS
 
-template <int LPR, int NB, int MC, bool FUSED, bool BYTES>
+// STAMP: the stamped instantiation (dp4a, one pass and one K step, no global -> LDS copy: tq2_lean_stampable), with
+// c.segs.stamps holding the launch's records; only it is instantiated, in its own translation unit.
+template <int LPR, int NB, int MC, bool FUSED, bool BYTES, bool STAMP = false>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const bool one = p.passes == 1 && c.k / 256 <= (LPR / 4) * NB;
-  auto kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, false> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, false>;
+  decltype(&tq2_lean_kernel<LPR, NB, MC, FUSED, true, false>) kern;
   bool dma = false;
-  if constexpr (BYTES) {
+  if constexpr (STAMP) {
+    if (BYTES || !one || tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) || c.segs.stamps == nullptr)
+      return hipErrorInvalidConfiguration;
+    kern = tq2_lean_stamped_kernel<LPR, NB, MC, FUSED>;
+  } else if constexpr (BYTES) {
     kern = one ? tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, false>;
-  } else if constexpr (MC > 1 && !FUSED) {
-    dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false);
-    if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
+  } else {
+    kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, false> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, false>;
+    if constexpr (MC > 1 && !FUSED) {
+      dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false);
+      if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
+    }
   }
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
@@ -518,38 +568,39 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int LPR, int MC, bool FUSED, bool BYTES>
+template <int LPR, int MC, bool FUSED, bool BYTES, bool STAMP>
 hipError_t by_nb(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (p.nb) {
-    case 1: return launch_k<LPR, 1, MC, FUSED, BYTES>(c, p, s);
-    case 2: return launch_k<LPR, 2, MC, FUSED, BYTES>(c, p, s);
-    case 4: return launch_k<LPR, 4, MC, FUSED, BYTES>(c, p, s);
+    case 1: return launch_k<LPR, 1, MC, FUSED, BYTES, STAMP>(c, p, s);
+    case 2: return launch_k<LPR, 2, MC, FUSED, BYTES, STAMP>(c, p, s);
+    case 4: return launch_k<LPR, 4, MC, FUSED, BYTES, STAMP>(c, p, s);
     case 8:
-      if constexpr (MC == 1) return launch_k<LPR, 8, MC, FUSED, BYTES>(c, p, s);
+      if constexpr (MC == 1) return launch_k<LPR, 8, MC, FUSED, BYTES, STAMP>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
 
-template <int LPR, bool FUSED, bool BYTES>
+template <int LPR, bool FUSED, bool BYTES, bool STAMP>
 hipError_t by_mc(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   switch (c.m) {
-    case 1: return by_nb<LPR, 1, FUSED, BYTES>(c, p, s);
-    case 2: return by_nb<LPR, 2, FUSED, BYTES>(c, p, s);
-    case 3: return by_nb<LPR, 3, FUSED, BYTES>(c, p, s);
+    case 1: return by_nb<LPR, 1, FUSED, BYTES, STAMP>(c, p, s);
+    case 2: return by_nb<LPR, 2, FUSED, BYTES, STAMP>(c, p, s);
+    case 3: return by_nb<LPR, 3, FUSED, BYTES, STAMP>(c, p, s);
   }
   return hipErrorInvalidValue;
 }
 
-// The lean kernels of one mode (dp4a: gemv_tq2.hip, bytes: gemv_tq2_bytes.hip, each its own translation unit).
-template <bool BYTES>
+// The lean kernels of one mode (dp4a: gemv_tq2.hip, bytes: gemv_tq2_bytes.hip, the stamped dp4a instantiations:
+// gemv_tq2_stamp.hip, each its own translation unit).
+template <bool BYTES, bool STAMP = false>
 hipError_t launch_mode(const GemvCall& c, const GemvPlan& p, hipStream_t s) {
   const bool fused = c.x != nullptr;
   switch (p.lpr_log2) {
-    case 2: return fused ? by_mc<4, true, BYTES>(c, p, s) : by_mc<4, false, BYTES>(c, p, s);
-    case 3: return fused ? by_mc<8, true, BYTES>(c, p, s) : by_mc<8, false, BYTES>(c, p, s);
-    case 4: return fused ? by_mc<16, true, BYTES>(c, p, s) : by_mc<16, false, BYTES>(c, p, s);
-    case 5: return fused ? by_mc<32, true, BYTES>(c, p, s) : by_mc<32, false, BYTES>(c, p, s);
-    case 6: return fused ? by_mc<64, true, BYTES>(c, p, s) : by_mc<64, false, BYTES>(c, p, s);
+    case 2: return fused ? by_mc<4, true, BYTES, STAMP>(c, p, s) : by_mc<4, false, BYTES, STAMP>(c, p, s);
+    case 3: return fused ? by_mc<8, true, BYTES, STAMP>(c, p, s) : by_mc<8, false, BYTES, STAMP>(c, p, s);
+    case 4: return fused ? by_mc<16, true, BYTES, STAMP>(c, p, s) : by_mc<16, false, BYTES, STAMP>(c, p, s);
+    case 5: return fused ? by_mc<32, true, BYTES, STAMP>(c, p, s) : by_mc<32, false, BYTES, STAMP>(c, p, s);
+    case 6: return fused ? by_mc<64, true, BYTES, STAMP>(c, p, s) : by_mc<64, false, BYTES, STAMP>(c, p, s);
   }
   return hipErrorInvalidValue;
 }

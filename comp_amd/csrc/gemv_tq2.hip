@@ -41,8 +41,22 @@ bool tq2_lean_eligible(const GemvCall& c, const GemvPlan& p) {
              gemv_tq2::kLdsLimit;
 }
 
+bool tq2_lean_stampable(const GemvCall& c, const GemvPlan& p) {
+  const int lpr = 1 << p.lpr_log2;
+  return c.mode == MODE_DP4A && c.nseg <= 1 && p.passes == 1 && c.k / 256 <= (lpr / 4) * p.nb &&
+         !tq2_lean_dma(lpr, p.nb, c.m, c.k, c.x != nullptr, 64 * p.waves, false);
+}
+
 hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   if (p.waves * p.rows_per_wave < p.block_n) return hipErrorInvalidConfiguration;
+  if (stamps_on() && tq2_lean_stampable(c, p)) {  // the tuning harness's wave stamps, while there is room for them
+    const int64_t groups = (c.n + p.block_n - 1) / p.block_n;
+    if (uint32_t* slot = stamp_slot(4 + 4 * groups * p.waves)) {
+      GemvCall cs = c;
+      cs.segs.stamps = slot;
+      return launch_gemv_tq2_lean_stamped(cs, p, stream);
+    }
+  }
   return c.mode == MODE_BYTES ? launch_gemv_tq2_lean_bytes(c, p, stream) : gemv_tq2::launch_mode<false>(c, p, stream);
 }
 

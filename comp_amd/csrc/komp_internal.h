@@ -71,6 +71,7 @@ struct GemvSegs {
   int64_t sw[kMaxSegs];
   int n[kMaxSegs];
   int first_wg[kMaxSegs];
+  uint32_t* stamps;  // the stamped TQ2_0 lean instantiations only: this launch's wave-stamp records (stamp_slot)
 };
 
 struct GemvCall {
@@ -159,6 +160,14 @@ struct Timing {
 };
 Timing timing_slot(int kind);   // defined in abi.hip
 
+// In-kernel wave stamps of the tuning harness (komp_stamps_begin / komp_stamps_end in abi.hip): whether stamping is
+// on, and a launch's records, `words` words of the caller's stamp buffer (nullptr when stamping is off or the buffer
+// has no room left; the launch then runs unstamped).  Record layout: a header {kStampMagic, waves, N, K}, then
+// {entry, staged, dots, stored} per wave, each the low 32 bits of the real-time counter.
+constexpr uint32_t kStampMagic = 0x4B535450u;
+bool stamps_on();
+uint32_t* stamp_slot(int64_t words);
+
 size_t gemv_lds_bytes(int fmt, int m, int k);
 hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
@@ -174,6 +183,9 @@ size_t tq2_lean_lds_bytes(int lpr, int nb, int mc, int k, bool fused, int thread
 bool tq2_lean_dma(int lpr, int nb, int mc, int k, bool fused, int threads, bool bytes);
 hipError_t launch_gemv_tq2_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_tq2_lean_bytes(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+// the stamped instantiations (gemv_tq2_stamp.hip): dp4a plans with one pass and one K step, no global -> LDS copy
+bool tq2_lean_stampable(const GemvCall& c, const GemvPlan& p);
+hipError_t launch_gemv_tq2_lean_stamped(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 // Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip), and Q4_0 in bytes mode (gemv_q4_bytes.hip)
 bool q4_lean_eligible(const GemvCall& c, const GemvPlan& p);
 size_t q4_lean_lds_bytes(int g, int nb, int mc, int k, bool bytes);

@@ -6,7 +6,7 @@
  * (NULL = the default stream).  Every call is asynchronous on `stream` and allocates nothing.  Each entry validates
  * shapes, strides and alignment first and returns a nonzero status without touching the GPU when they are wrong;
  * komp_last_error() then describes the problem.  Nothing aborts.  The library keeps no state between calls except
- * the optional dispatch timing of the tuning harness (komp_timing_*).
+ * the optional dispatch timing and wave stamps of the tuning harness (komp_timing_*, komp_stamps_*).
  *
  * Layouts are the reference's split planes (src/komp/kernels.py:3-7, src/komp/host.py:16-31):
  *   Q4_0 weights   WQ uint8 [N][SW] (row r at WQ + r*SW; 16 quant bytes per block of 32, ggml order),
@@ -225,6 +225,21 @@ int komp_tq2_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t nblk, void* strea
 #define KOMP_TIMING_KINDS 8
 int komp_timing_begin(int64_t max_dispatches);
 int komp_timing_end(double* ms, int64_t* count);
+
+/* In-kernel wave stamps for the tuning harness (no reference counterpart; the reference was never timed): the span of
+ * a kernel inside a HIP graph, from its first wave's entry to its last wave's stored outputs, which no event can see.
+ * Between komp_stamps_begin() and komp_stamps_end(), every TQ2_0 GEMV launch in dp4a mode (fused or not) whose plan
+ * reads its rows in one pass and one K step, from a single matrix (the decode shapes' plans), runs an instantiation
+ * of the same kernel that reads the device's constant-rate real-time counter in every wave at four points: entry,
+ * the staged activations published to the workgroup, the last weight chunk's dot issued, and the wave's outputs
+ * stored (the stores complete).  Other launches run as usual and record nothing, and so does a launch that no longer
+ * fits in BUF.  BUF (device memory, 16-byte aligned, WORDS uint32 words) receives per stamped launch, at the next
+ * 16-byte boundary: a header {0x4B535450, waves of the grid, N, K}, then {entry, staged, dots, stored} per wave (the
+ * counter's low 32 bits), wave w of workgroup g at index g * (waves per workgroup) + w.  A launch captured into a HIP
+ * graph keeps its records' place, and each replay rewrites them.  komp_stamps_end() returns the words used and the
+ * counter's rate in kHz (hipDeviceAttributeWallClockRate). */
+int komp_stamps_begin(uint32_t* buf, int64_t words);
+int komp_stamps_end(int64_t* words_used, int* clock_khz);
 
 #ifdef __cplusplus
 }

@@ -245,3 +245,27 @@ def test_gemm_rejects_bad_arguments():
         assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 4096, None, None, None) == 0
     for fmt in (-1, 5):
         assert lib.komp_gemm_plan(fmt, 16, 4096, 4096, 2048, None, None, None) == _abi.KOMP_EINVAL
+
+
+def test_stamps_begin_rejects_bad_buffers():
+    lib = _abi.lib()
+    assert lib.komp_stamps_begin(ctypes.c_void_p(8), 64) == _abi.KOMP_EINVAL and "16-byte" in _abi.last_error()
+    assert lib.komp_stamps_begin(None, 64) == _abi.KOMP_EINVAL
+    assert lib.komp_stamps_begin(ctypes.c_void_p(16), -1) == _abi.KOMP_EINVAL
+    used = ctypes.c_int64(-1)
+    assert lib.komp_stamps_end(ctypes.byref(used), None) == _abi.KOMP_OK and used.value == 0
+
+
+def test_parse_stamps_walks_records_across_a_counter_wrap():
+    import numpy as np
+
+    # two launches: 2 waves (counter wrapping past 2^32 inside the launch), then 3 waves; 100 MHz = 10 ns a tick
+    a = [_abi.STAMP_MAGIC, 2, 6912, 2560, 0xFFFFFFF0, 0xFFFFFFF8, 2, 20, 0xFFFFFFF4, 0, 5, 30]
+    b = [_abi.STAMP_MAGIC, 3, 2560, 6912] + [100, 110, 120, 130] * 2 + [90, 111, 121, 200]
+    words = np.array(a + b, dtype=np.uint64).astype(np.uint32)
+    recs = _abi.parse_stamps(words, 100_000)
+    assert [(r["n"], r["k"], r["waves"]) for r in recs] == [(6912, 2560, 2), (2560, 6912, 3)]
+    assert list(recs[0]["entry"]) == [0, 40] and list(recs[0]["stored"]) == [360, 460] and recs[0]["span_ns"] == 460
+    assert list(recs[1]["entry"]) == [100, 100, 0] and recs[1]["span_ns"] == 1100
+    with pytest.raises(_abi.KompError, match="header"):
+        _abi.parse_stamps(np.array([1, 2, 3, 4], dtype=np.uint32), 100_000)

@@ -5,10 +5,14 @@ stay within the bound; plausible mistakes of a kernel (a shifted scale index, a 
 flushed to zero, a flipped sign, another column's d_x) must break it.  The evaluations below are f32 simulations in
 numpy, where every operation rounds to nearest-even as the GPU's do."""
 
+import functools
+
 import numpy as np
 import pytest
 
+from oracle import coracle as C
 from oracle import oracle as O
+from tests.checks import gate
 
 FORMATS = ("q4_0", "tq2_0", "q8_0", "iq4_nl", "q4_k")
 SHAPES = {"q4_0": (37, 416, 3), "q8_0": (37, 416, 3), "iq4_nl": (37, 416, 3), "tq2_0": (29, 1792, 3),
@@ -186,3 +190,64 @@ def test_zero_terms_need_exact_zero():
     assert not O.output_check("q4_0", y, ws, xd, s, r)[0]
     y[0, 0] = np.nan
     assert not O.output_check("q4_0", y, ws, xd, s, r)[0]
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the combined gate (tests/checks.py: per-output bound and relerr <= 1e-5) at the workloads' long rows
+
+
+@functools.lru_cache(maxsize=4)
+def _long_row_problem(n, k, seed):
+    """Q4_0 W [n][k] ~ N(0, 0.02) by ggml's q4_0 rule and one column x ~ N(0, 1) with 1% of entries x20 (the
+    Llama-3-8B layer's activations), from the C oracle: (ws, xd, s [1][n][k/32], r)."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    wq, ws = O.split("q4_0", C.quantize_q4_0_weights(w), n, k)
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    x = np.where(rng.random((1, k)) < 0.01, x * np.float32(20), x).astype(np.float32)
+    xq, xd = C.quant_q8_0(x)
+    s = C.block_dots("q4_0", wq, xq, n, k)
+    return ws, xd, s, C.reference_dot("q4_0", ws, xd, s)
+
+
+def _round_mantissa(p, bits):
+    """f32 p rounded to nearest (ties away) at `bits` fraction bits: a kernel keeping a short scale product."""
+    u = np.ascontiguousarray(p, np.float32).view(np.uint32).astype(np.uint64)
+    shift = 23 - bits
+    u = ((u + (1 << (shift - 1))) >> shift) << shift
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("k", [4096, 8192, 14336])
+def test_gate_is_tight_at_long_rows(k):
+    """Not vacuous at 128-448 blocks a row, where the per-output bound alone admits 1e-4 of |r| and more: the f32
+    evaluations pass the combined gate, and an error of 1e-4 of |r| in one output at or above the median fails it."""
+    ws, xd, s, r = _long_row_problem(512, k, 31)
+    t = _f32_terms("q4_0", ws, xd, s)
+    for name, y in (("sequential", _sum_sequential(t)), ("lanes", _sum_lanes(t)), ("fma", _sum_fma("q4_0", ws, xd, s))):
+        ok, msg = gate("q4_0", y, ws, xd, s, r)
+        assert ok, f"k={k} {name}: {msg}"
+    y = _sum_sequential(t).astype(np.float64)
+    big = np.flatnonzero((np.abs(r) >= np.median(np.abs(r))).reshape(-1))
+    for i in big[:: max(1, big.size // 16)]:
+        yp = y.copy()
+        yp.reshape(-1)[i] += 1e-4 * abs(r.reshape(-1)[i])
+        assert not gate("q4_0", yp, ws, xd, s, r)[0], f"k={k}: an error of 1e-4 |r| at output {i} passes"
+
+
+@pytest.mark.parametrize("bits", [12, 13, 14])
+def test_short_scale_product_fails_the_gate_at_4096x14336(bits):
+    """A kernel that keeps only 12-14 fraction bits of each block's scale product d_w * d_x, summing in f32, stays
+    within the per-output bound at the Llama-3-8B down projection (448 Q4_0 blocks a row), so only the relerr half of
+    the gate catches it; the full-precision f32 evaluation passes both halves."""
+    ws, xd, s, r = _long_row_problem(4096, 14336, 37)
+    dw = O.f16_bits_to_f32(ws)
+    dx = np.asarray(xd, np.float32)
+    good = _sum_sequential((s.astype(np.float32) * dw[None]) * dx[:, None, :])
+    assert gate("q4_0", good, ws, xd, s, r)[0]
+    short = _sum_sequential(s.astype(np.float32) * _round_mantissa(dw[None] * dx[:, None, :], bits))
+    bound_ok, _ = O.output_check("q4_0", short, ws, xd, s, r)
+    ok, msg = gate("q4_0", short, ws, xd, s, r)
+    assert not ok and "relerr" in msg, f"{bits} bits: {msg}"
+    if bits == 12:
+        assert bound_ok, "the per-output bound alone was expected to admit the 12-bit scale product here"
