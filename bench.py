@@ -44,7 +44,6 @@ if ROOT not in sys.path:
 METRIC = "GEMV µs/call + achieved HBM GB/s (% of peak), Q4_0 & TQ2_0 decode shapes"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
 MODE_NAMES = {0: "bytes", 1: "dp4a-emulated", 2: "dp4a"}
-SUBMIT_COVER_CYCLES = 2_000_000  # torch.cuda._sleep length (~1 ms): covers the host's submission of the timed replays
 COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infinity Cache)
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
@@ -179,9 +178,6 @@ def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
         g_full.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # a bounded spin kernel ahead of the start event keeps the GPU busy while the host submits the replays, so the
-    # timed region holds the K steps back to back and not the host's submission of the first graph
-    torch.cuda._sleep(SUBMIT_COVER_CYCLES)
     t0 = time.perf_counter()
     e0.record()
     for _ in range(steps // per_graph):
@@ -192,6 +188,49 @@ def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
     return e0.elapsed_time(e1), wall
+
+
+def timed_one_graph(torch, abi, step, ncopies, steps, warmup):
+    """The headline's timing: `warmup` untimed steps (graph replays), then ONE graph holding a lead step, a clock mark,
+    exactly `steps` steps and a second clock mark, replayed once.  The marks are the library's one-lane komp_clock
+    kernel writing the device's real-time counter, since the runtime records no events inside a graph; the graph's
+    own start latency on the GPU (about 11 us a replay) falls on the lead step, outside the interval, which holds the
+    K steps back to back (and the first mark's own end, a fraction of a microsecond).  -> (ms of the K steps, host wall
+    ms of the replay, events ms around the whole replay: lead step and start latency included)."""
+    marks = torch.zeros(2, dtype=torch.int64, device="cuda")
+    khz = abi.clock_khz()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(ncopies, 2)):
+            step(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(0)
+        abi.clock_into(marks[0:1])
+        for i in range(steps):
+            step(1 + i)
+        abi.clock_into(marks[1:2])
+    if warmup > 0:
+        per_graph = ncopies * max(1, math.ceil(64 / ncopies))
+        g_warm = run_graph(torch, step, min(per_graph, warmup), 1)
+        for _ in range(math.ceil(warmup / per_graph)):
+            g_warm.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    t = marks.cpu().tolist()
+    ms = (t[1] - t[0]) / khz
+    if not ms > 0.0:
+        raise RuntimeError(f"clock marks {t} at {khz} kHz give no interval")
+    return ms, wall, e0.elapsed_time(e1)
 
 
 def read_floor_us(torch, host, nbytes):
@@ -322,10 +361,10 @@ def headline(torch, host, abi, args):
         host.quantize_into("tq2_0", u1, *q2)
         host.gemv_into("tq2_0", w2, s2, *q2, u2, n2, k2, *knobs[1][:2], args.mode, knobs[1][2])
 
-    ms, wall_ms = timed_steps(torch, step, ncopies, args.steps, args.warmup)
+    ms, wall_ms, replay_ms = timed_one_graph(torch, abi, step, ncopies, args.steps, args.warmup)
+    last = args.steps % ncopies  # the timed graph's last step
     # the graph must reproduce the eager result of the same (last) step bit for bit, and the fused and two-launch
     # paths must agree bit for bit
-    last = (args.steps - 1) % ncopies
     got = (y1.clone(), y2.clone())
     step(last)
     step_two_launch(last)
@@ -337,7 +376,7 @@ def headline(torch, host, abi, args):
     rel = max(float((a - b).abs().max() / b.abs().max()) for a, b in ((y1, u1), (y2, u2)))
     if rel > 1e-6:
         raise RuntimeError(f"fused and two-launch outputs differ by {rel:.2e} (relative)")
-    ms2, _ = timed_steps(torch, step_two_launch, ncopies, args.steps, args.warmup)
+    ms2, _, _ = timed_one_graph(torch, abi, step_two_launch, ncopies, args.steps, args.warmup)
 
     step_bytes = sum(step_bytes_fused("tq2_0", n, k, m) for n, k in shapes)
     ms_per_step = ms / args.steps
@@ -372,7 +411,10 @@ def headline(torch, host, abi, args):
                           "activations quantized to q8_K inside each launch",  # fmt: skip
               "shapes_nk": [list(s) for s in shapes], "m": m, "mode": MODE_NAMES[args.mode],
               "plan_rows_nb_waves_lanes_passes": plans, "cold_copies": ncopies, "seed": args.seed,
-              "step_bytes": step_bytes, "wall_ms_host": round(wall_ms, 3), "us_per_step_graph": round(ms_per_step * 1e3, 3),
+              "step_bytes": step_bytes,
+              "step_timing": "device clock marks (komp_clock) around the K steps inside one graph, after a lead step",
+              "replay_events_ms": round(replay_ms, 4), "wall_ms_host": round(wall_ms, 3),
+              "us_per_step_graph": round(ms_per_step * 1e3, 3),
               "gemv_us_per_call_dispatch": round(g_us, 3),
               "two_launch_us_per_step_graph": round(ms2 / args.steps * 1e3, 3)}  # fmt: skip
     return value, ms_per_step, roofline, config, step_bytes

@@ -72,6 +72,8 @@ SIGNATURES = {
     "komp_timing_end": (_INT, [_P, _P]),
     "komp_stamps_begin": (_INT, [_P, _I64]),
     "komp_stamps_end": (_INT, [_P, _P]),
+    "komp_clock": (_INT, [_P, _P]),
+    "komp_clock_khz": (_INT, [_P]),
 }
 ABI_VERSION = 1
 
@@ -184,3 +186,17 @@ def parse_stamps(words, clock_khz):
                     "stored": t[:, 3], "span_ns": float(t[:, 3].max())})
         off += (4 + 4 * waves + 3) & ~3
     return out
+
+
+def clock_into(out, stream=None):
+    """Write the device's real-time counter to out[0] (an int64 device tensor) when the stream gets there (komp_clock;
+    inside a graph capture too).  stream: a torch stream (default: the current one)."""
+    st = (stream or torch.cuda.current_stream()).cuda_stream
+    call("komp_clock", ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st))
+
+
+def clock_khz():
+    """The rate of komp_clock's counter in kHz."""
+    khz = ctypes.c_int(0)
+    call("komp_clock_khz", ctypes.byref(khz))
+    return khz.value

@@ -106,20 +106,30 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     the lean kernel's single-pass, single-K-step form, which the launch picks when the rows per wave fit one pass and a
     row's K blocks one step (the single-column form only for q4_0 / iq4_nl); without k the loop form is named.  The
     LDS-copy form stages two or three tq2_0 columns that need more than one pass of the workgroup's threads, when LDS
-    holds them."""
+    holds them.  One column with nb < 8 whose waves walk 3 tiles or more (passes x K steps; k given) runs the
+    pipelined loop form instead (q4_lean_pipe_kernel <format, lanes, nb, fused>, q4_lean_bytes_pipe_kernel <lanes, nb,
+    fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>)."""
     cols = min(max(m, 1), 3)
     lean_mode = mode == 2 or (mode == 0 and fmt in ("tq2_0", "q4_0"))
     if lean_mode and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
         rpw = block_n // num_warps
         lanes = 64 // min(rpw, 16)
         one_pass = rpw <= 16 and k is not None
+        passes = rpw // min(rpw, 16)
+        vals = 256 if fmt == "tq2_0" else 32
+        step = (lanes // 4 if fmt == "tq2_0" else lanes) * nb  # blocks a K step covers
+        pipe = k is not None and cols == 1 and nb < 8 and passes * -(-(k // vals) // step) >= 3
         if fmt == "tq2_0" and mode == 0:
             one = one_pass and k // 256 <= (lanes // 4) * nb
             bstep = (lanes // 4) * nb
             if k is None or cols * -(-(k // 256) // bstep) * bstep * (2 * 288 + 8) <= 160 * 1024:
+                if pipe and not one:
+                    return f"gemv_tq2::tq2_lean_pipe_kernel<{lanes}, {nb}, false, true>"
                 return f"gemv_tq2::tq2_lean_bytes_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
         elif fmt == "tq2_0":
             one = one_pass and k // 256 <= (lanes // 4) * nb
+            if pipe and not one:
+                return f"gemv_tq2::tq2_lean_pipe_kernel<{lanes}, {nb}, false, false>"
             dma = False
             if k is not None and cols > 1 and cols * (k // 256) * 16 > 64 * num_warps:
                 bstep = (lanes // 4) * nb
@@ -129,6 +139,10 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
                     f"{str(dma).lower()}>")
         elif fmt in ("q4_0", "iq4_nl"):
             one = one_pass and cols == 1 and k // 32 <= lanes * nb
+            if pipe and not one:
+                if mode == 0:
+                    return f"gemv_q4::q4_lean_bytes_pipe_kernel<{lanes}, {nb}, false>"
+                return f"gemv_q4::q4_lean_pipe_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, false>"
             if mode == 0:
                 return f"gemv_q4::q4_lean_bytes_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
             return f"gemv_q4::q4_lean_kernel<{FMT_NUM[fmt]}, {lanes}, {nb}, {cols}, false, {str(one).lower()}>"

@@ -122,7 +122,9 @@ int device_cus() {
   return c;
 }
 
-GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t k) {
+// sw: the largest row stride of the launch's matrices (bytes; 0: dense rows), which decides whether the lean kernels
+// can take a plan of more than 8 waves (their 32-bit per-pass buffer ranges, lean_strides_fit).
+GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t k, int64_t sw = 0) {
   const int bpb = fmt_info(fmt).qbytes / (fmt == FMT_Q4_K ? 32 : 16);  // lane slots per block (Q4_K: 32-byte groups)
   const int64_t nblk = k / fmt_info(fmt).block;
   const int64_t chunks = nblk * bpb;                      // lane slots per row (16-byte chunks; Q4_K 32-byte groups)
@@ -191,7 +193,10 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
                                                                     static_cast<int>(64 * waves), mode == KOMP_MODE_BYTES)
                                                : q4_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k),
                                                                    mode == KOMP_MODE_BYTES);
-      if (waves <= 8 || (m == 1 && mode == KOMP_MODE_DP4A) || lean_lds <= kLdsMax)
+      // and only where the lean kernels' 32-bit per-pass buffer ranges hold a pass's rows (else the 8-wave plans)
+      const int64_t row_bytes = sw > 0 ? sw : nblk * fmt_info(fmt).qbytes;
+      const bool lean_fit = rpp * row_bytes <= 0x7FFFFFF0;
+      if (waves <= 8 || (lean_fit && ((m == 1 && mode == KOMP_MODE_DP4A) || lean_lds <= kLdsMax)))
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);
     }
   }
@@ -418,8 +423,10 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
   if (gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax)
     return fail(KOMP_EINVAL, "%s: K=%lld needs more than 160 KiB of LDS for one activation column", name, (long long)K);
 
+  int64_t sw_max = 0;
+  for (int i = 0; i < count; ++i) sw_max = mats[i].sw > sw_max ? mats[i].sw : sw_max;
   const GemvPlan plan =
-      block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K) : knob_plan(block_n, nb, num_warps);
+      block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K, sw_max) : knob_plan(block_n, nb, num_warps);
 
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
     GemvCall c = {};
@@ -738,6 +745,19 @@ int komp_stream_read(const void* SRC, int64_t bytes, uint32_t* OUT, void* stream
   if (!SRC || !OUT) return fail(KOMP_EINVAL, "komp_stream_read: NULL pointer");
   if (!aligned(SRC, 16) || !aligned(OUT, 4)) return fail(KOMP_EINVAL, "komp_stream_read: SRC must be 16-byte and OUT 4-byte aligned");
   return hip_status(launch_stream_read(SRC, bytes, OUT, static_cast<hipStream_t>(stream)), "komp_stream_read");
+}
+
+int komp_clock(uint64_t* OUT, void* stream) {
+  if (!OUT || !aligned(OUT, 8)) return fail(KOMP_EINVAL, "komp_clock: OUT must be an 8-byte aligned device pointer");
+  return hip_status(launch_clock(OUT, static_cast<hipStream_t>(stream)), "komp_clock");
+}
+
+int komp_clock_khz(int* khz) {
+  if (!khz) return fail(KOMP_EINVAL, "komp_clock_khz: NULL pointer");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev);
+  return hip_status(e, "komp_clock_khz");
 }
 
 int komp_q4_0_decode(const uint8_t* WQ, int32_t* OUT, int64_t R, void* stream) {

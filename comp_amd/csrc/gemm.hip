@@ -581,8 +581,16 @@ hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
 
 template <int FMT, int WK, int WR, int WN, int CN, int D>
 hipError_t launch_t(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
-  return c.s != nullptr ? launch_s<FMT, WK, WR, WN, CN, D, true>(c, p, stream)
-                        : launch_s<FMT, WK, WR, WN, CN, D, false>(c, p, stream);
+  if (c.s == nullptr) return launch_s<FMT, WK, WR, WN, CN, D, false>(c, p, stream);
+  if constexpr (WN == 2 && CN == 4) {
+    // storing S as well, two row tiles a wave with four column tiles would hold more than 256 VGPRs (spilled to
+    // scratch): one row tile a wave, twice the workgroups; each output's sums run in the same order, so Y is the same
+    GemmPlan q = p;
+    q.wn = 1;
+    return launch_s<FMT, WK, WR, 1, CN, D, true>(c, q, stream);
+  } else {
+    return launch_s<FMT, WK, WR, WN, CN, D, true>(c, p, stream);
+  }
 }
 
 // The instantiated plans (gemm_plan in abi.hip picks one): (wk, wr, wn, cn, d).

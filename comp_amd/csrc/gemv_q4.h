@@ -51,7 +51,8 @@ __device__ __forceinline__ int q4_0_block_dot_bytes(const u32x4& w, const u32x4&
 // code with no loop and no reload (a launch starts with a cold instruction cache, and every 64-byte line of code on
 // the way to the first dot costs tens of nanoseconds of fetch).
 // BYTES: Q4_0 in bytes mode (q4_0_block_dot_bytes on 16-bit activations); otherwise dp4a.
-template <int FMT, int G, int NB, int MC, bool FUSED, bool ONE, bool BYTES>
+// PIPE: the loop form with the weight loads software-pipelined, for waves of many tiles (the reference's knob plans).
+template <int FMT, int G, int NB, int MC, bool FUSED, bool ONE, bool BYTES, bool PIPE = false>
 __device__ __forceinline__ void q4_lean_body(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
                                              const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
                                              const void* __restrict__ XA, const float* __restrict__ XD,
@@ -113,10 +114,20 @@ __device__ __forceinline__ void q4_lean_body(int N1, int nblk, int SW1, int nseg
   const unsigned vo_w = grp * SW + g * 16;
   const unsigned vo_s = static_cast<unsigned>((grp * nblk + g) * 2);
 
-  // ---- weights: step (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * G + g ----
-  u32x4 w[NB];
-  int16_t sc[NB];
-  auto load = [&](int p, int st, bool first) {
+  // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * G + g.  The pipelined form
+  // keeps D tiles in flight, 8 chunks a lane: tile t is loaded into buffer t % D while tile t - D + 1 is being dotted,
+  // so a K step waits for its own loads only instead of a memory round trip per step (nb 8 keeps one buffer: two
+  // would take the kernel past 128 VGPRs; 16 chunks a lane measured slower, 7.5 -> 8.3 us at Q4_0 4096 x 4096 with
+  // block_n 64, nb 4, 4 waves).  The other forms keep one buffer, which holds fewer registers: with two tiles a wave
+  // or several workgroups a CU that is faster ----
+  constexpr int D = (!PIPE || NB >= 8) ? 1 : 8 / NB;
+  u32x4 w[D][NB];
+  int16_t sc[D][NB];
+  // One form for every tile, with no branch: a block past the row's end swaps its per-lane offset for the
+  // out-of-range one, and a tile past the wave's last (p = npass) has a descriptor of no rows, so every load of the
+  // loop is issued whatever the tile and the compiler counts the loads in flight exactly (behind a branch it waits
+  // for all of them at the join).
+  auto load = [&](u32x4 (&wb)[NB], int16_t (&sb)[NB], int p, int st) {
     // a descriptor per pass, over the pass's rows inside the matrix: a row past the matrix lies past the range,
     // which the per-lane offset is checked against, and reads zeros; the step goes into the scalar offset, and the
     // per-lane offsets stay the same in every pass
@@ -127,28 +138,26 @@ __device__ __forceinline__ void q4_lean_body(int N1, int nblk, int SW1, int nseg
     const unsigned so_w = static_cast<unsigned>(st * BSTEP * 16);
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the step's first to the row's end (wave-uniform)
-    if (!first && lim >= BSTEP) {
 #pragma unroll
-      for (int u = 0; u < NB; ++u)  // the scales first: a block's dot then waits for its own weight load only
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, vo_s + u * G * 2, so_s, 0));
+    for (int u = 0; u < NB; ++u) {  // the scales first: a block's dot then waits for its own weight load only
+      const bool ok = g + u * G < lim;
+      sb[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_s + u * G * 2 : kOob, so_s, 0));
+    }
 #pragma unroll
-      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w + u * G * 16, so_w, 2);
-    } else {  // the row's last, partial step, and the first tile
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const bool ok = g + u * G < lim;
-        sc[u] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_s + u * G * 2 : kOob, so_s, 0));
-      }
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const bool ok = g + u * G < lim;
-        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w + u * G * 16 : kOob, so_w, 2);
-      }
+    for (int u = 0; u < NB; ++u) {
+      const bool ok = g + u * G < lim;
+      wb[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w + u * G * 16 : kOob, so_w, 2);
     }
   };
-  // The first tile's loads take the selecting form whatever the step: behind an if / else the compiler's wait
-  // counting loses their place after the staging loads, and the staging then waits for the weights as well.
-  load(0, 0, true);
+  load(w[0], sc[0], 0, 0);
+  int lp = 0, lst = 0;  // the next tile to load
+  auto advance = [&](int& p, int& st) {
+    if (++st == nsteps) {
+      st = 0;
+      ++p;
+    }
+  };
+  advance(lp, lst);
 
   // ---- stage the columns: xl[m][b] = activations 0..15 of block b of column m, xh[m][b] = 16..31, meta[m][b] =
   // {d_x bits, -8 * sum(x) (Q4_0; IQ4_NL 0)} for b < nblk_pad (zeros past nblk, so a block past the row's end adds 0);
@@ -242,49 +251,84 @@ __device__ __forceinline__ void q4_lean_body(int N1, int nblk, int SW1, int nseg
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
+  // the loop form's next tiles, issued once the staging is done: a staging pass that loads after them would wait for
+  // them too (loads retire in issue order)
+#pragma unroll
+  for (int d = 1; d < D; ++d) {
+    load(w[d], sc[d], lp, lst);
+    advance(lp, lst);
+  }
+
   // ---- stream the weights ----
   const u32x4* xlg = xl + g;
   const u32x4* xhg = xh + g;
   const u32x4* xlog = xlo + g;
   const u32x4* xhog = xho + g;
   const int2* mg = meta + g;
-  for (int p = 0; p < npass; ++p) {
+  float acc[MC];
+  int p = 0, st = 0;  // the tile being dotted: pass p, K step st
+  // Dot the tile in buffer (wb, sb), then (next) load tile t + D into it, past the wave's last tile a load of no rows
+  // (zeros, no memory touched); the pass's outputs are stored after its last step.
+  auto tile = [&](u32x4 (&wb)[NB], int16_t (&sb)[NB], bool next) {
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
-    float acc[MC];
+    if (st == 0) {
 #pragma unroll
-    for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
-    for (int st = 0; st < nsteps; ++st) {
-      if (p != 0 || st != 0) load(p, st, false);
-      const int tb = st * BSTEP;
-      const int lim = nblk - tb;  // blocks from the step's first to the row's end (wave-uniform)
+      for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
+    }
+    const int tb = st * BSTEP;
+    const int lim = nblk - tb;  // blocks from the step's first to the row's end (wave-uniform)
 #pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        if (u * G >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
-        const int bo = tb + u * G;
-        const float dw = f16_bits_to_f32(sc[u]);
+    for (int u = 0; u < NB; ++u) {
+      // no lane of the wave has a block in this slot or the next (the row's last step): skipped, except in the
+      // pipelined form, which dots them (zero weights and activations), since a branch here would make the compiler
+      // wait for every load in flight
+      if (D == 1 && u * G >= lim) break;
+      const int bo = tb + u * G;
+      const float dw = f16_bits_to_f32(sb[u]);
 #pragma unroll
-        for (int m = 0; m < MC; ++m) {
-          const int bm = m * nblk_pad + bo;
-          const int2 mt = mg[bm];
-          int s;
-          if constexpr (BYTES)
-            s = q4_0_block_dot_bytes(w[u], xlg[bm], xlog[bm], xhg[bm], xhog[bm], mt.y);
-          else if constexpr (FMT == FMT_Q4_0)
-            s = gemv_impl::q4_0_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm], mt.y);
-          else
-            s = gemv_impl::iq4_nl_block_dot<MODE_DP4A>(w[u], xlg[bm], xhg[bm]);
-          if (__builtin_expect(S != nullptr, 0) && rv && bo + g < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + bo + g] = s;
-          acc[m] += static_cast<float>(s) * dw * __int_as_float(mt.x);  // kernels.py:93 order
-        }
+      for (int m = 0; m < MC; ++m) {
+        const int bm = m * nblk_pad + bo;
+        const int2 mt = mg[bm];
+        int s;
+        if constexpr (BYTES)
+          s = q4_0_block_dot_bytes(wb[u], xlg[bm], xlog[bm], xhg[bm], xhog[bm], mt.y);
+        else if constexpr (FMT == FMT_Q4_0)
+          s = gemv_impl::q4_0_block_dot<MODE_DP4A>(wb[u], xlg[bm], xhg[bm], mt.y);
+        else
+          s = gemv_impl::iq4_nl_block_dot<MODE_DP4A>(wb[u], xlg[bm], xhg[bm]);
+        if (__builtin_expect(S != nullptr, 0) && rv && bo + g < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + bo + g] = s;
+        acc[m] += static_cast<float>(s) * dw * __int_as_float(mt.x);  // kernels.py:93 order
       }
     }
-#pragma unroll
-    for (int m = 0; m < MC; ++m) {
-      const float v = group_sum(acc[m], G);
-      if (g == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+    if (next && (D > 1 || lp < npass)) {  // one buffer: nothing to pipeline, no load past the wave's last tile
+      load(wb, sb, lp, lst);
+      advance(lp, lst);
     }
+    if (st == nsteps - 1) {
+#pragma unroll
+      for (int m = 0; m < MC; ++m) {
+        const float v = group_sum(acc[m], G);
+        if (g == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+      }
+    }
+    advance(p, st);
+  };
+  // Whole rounds of D tiles in the loop, with no branch that leaves a round midway (behind one, the loads in flight
+  // would reach the loop's head in two orders, and the compiler would wait for the stricter of them), then the last
+  // T mod D tiles straight-line, with nothing left to load
+  const int ntiles = npass * nsteps;
+  const int rounds = ONE ? 1 : ntiles / D;
+  for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) tile(w[d], sc[d], !ONE);
+  }
+  if constexpr (D > 1) {
+    const int rest = ntiles - rounds * D;  // wave-uniform
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (d < rest) tile(w[d], sc[d], false);
   }
 }
 
@@ -305,16 +349,31 @@ __global__ void __launch_bounds__(1024) q4_lean_bytes_kernel(KOMP_Q4_LEAN_ARGS) 
   q4_lean_body<FMT_Q4_0, G, NB, MC, FUSED, ONE, true>(KOMP_Q4_LEAN_PASS);
 }
 
+// The pipelined loop forms (PIPE above) of one column, dp4a and bytes mode.
+template <int FMT, int G, int NB, bool FUSED>
+__global__ void __launch_bounds__(1024) q4_lean_pipe_kernel(KOMP_Q4_LEAN_ARGS) {
+  q4_lean_body<FMT, G, NB, 1, FUSED, false, false, true>(KOMP_Q4_LEAN_PASS);
+}
+template <int G, int NB, bool FUSED>
+__global__ void __launch_bounds__(1024) q4_lean_bytes_pipe_kernel(KOMP_Q4_LEAN_ARGS) {
+  q4_lean_body<FMT_Q4_0, G, NB, 1, FUSED, false, true, true>(KOMP_Q4_LEAN_PASS);
+}
+
 #undef KOMP_Q4_LEAN_ARGS
 #undef KOMP_Q4_LEAN_PASS
 
 template <int FMT, int G, int NB, int MC, bool FUSED, bool BYTES>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  // the single-pass, single-step form for one column (the decode case; two and three columns keep the general one)
+  // the single-pass, single-step form for one column (the decode case; two and three columns keep the general one);
+  // the pipelined loop form for one column whose waves walk kPipeMinTiles tiles or more
   const bool one = MC == 1 && p.passes == 1 && c.k / 32 <= G * NB;
+  const bool pipe = MC == 1 && !one && NB < 8 && p.passes * ((c.k / 32 + G * NB - 1) / (G * NB)) >= kPipeMinTiles;
   auto kern = one ? q4_lean_kernel<FMT, G, NB, MC, FUSED, MC == 1> : q4_lean_kernel<FMT, G, NB, MC, FUSED, false>;
   if constexpr (BYTES)
     kern = one ? q4_lean_bytes_kernel<G, NB, MC, FUSED, MC == 1> : q4_lean_bytes_kernel<G, NB, MC, FUSED, false>;
+  if constexpr (MC == 1 && NB < 8) {
+    if (pipe) kern = BYTES ? q4_lean_bytes_pipe_kernel<G, NB, FUSED> : q4_lean_pipe_kernel<FMT, G, NB, FUSED>;
+  }
   GemvSegs segs = c.segs;
   int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
@@ -326,8 +385,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 32;
   const size_t lds = q4_lean_lds_bytes(G, NB, MC, c.k, BYTES);
-  static std::atomic<unsigned> lds_limit[2][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
-  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[one ? 1 : 0]);
+  static std::atomic<unsigned> lds_limit[3][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[one ? 1 : pipe ? 2 : 0]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));

@@ -134,7 +134,8 @@ __device__ __forceinline__ int quad_scatter2(int p0, int p1, uint64_t odd) {
 // published, after its last weight chunk's dot and after its outputs are stored (their stores complete), and lane 0
 // writes the four low words to segs.stamps[4 + 4 * (blockIdx.x * waves + wave)]; thread 0 of workgroup 0 writes the
 // header {kStampMagic, waves of the grid, N, K}.  Scheduling barriers keep each reading in its place.
-template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES, bool STAMP = false>
+// PIPE: the loop form with the weight loads software-pipelined, for waves of many tiles (the reference's knob plans).
+template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES, bool STAMP = false, bool PIPE = false>
 __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
                                               const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
                                               const void* __restrict__ XA, const float* __restrict__ XD,
@@ -233,12 +234,21 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
   // ---- weights: tile (p, st) = rows p * RPW + grp of the wave, blocks st * BSTEP + u * BPG + gblk.  Chunk slot u of
   // a quad is scaled by lane u % 4 alone, so a lane loads the scales of its own slots only: q, q + 4 (nb 8); lanes
   // q >= nb own none (nb < 4) and read a zero scale ----
+  // The pipelined form keeps D tiles in flight, 8 chunks a lane: tile t is loaded into buffer t % D while tile t - D + 1
+  // is being dotted, so a K step waits for its own loads only instead of a memory round trip per step (nb 8 keeps one
+  // buffer; 16 chunks a lane measured slower, 5.0 -> 5.7 us at 6912 x 2560 with block_n 64, nb 1, 4 waves).  The
+  // other forms keep one buffer, which holds fewer registers.
   constexpr int NOWN = (NB + 3) / 4;
-  u32x4 w[NB];
-  int16_t sc[NOWN];
+  constexpr int D = (!PIPE || NB >= 8) ? 1 : 8 / NB;
+  u32x4 w[D][NB];
+  int16_t sc[D][NOWN];
   const bool owner = NB >= 4 || q < NB;
   const unsigned vo_sq = vo_s + static_cast<unsigned>(q * BPG * 2);
-  auto load = [&](int p, int st, bool first) {
+  // One form for every tile, with no branch: a chunk past the row's end swaps its per-lane offset for the out-of-range
+  // one, and a tile past the wave's last (p = npass) has a descriptor of no rows, so every load of the loop is issued
+  // whatever the tile and the compiler counts the loads in flight exactly (behind a branch it waits for all of them at
+  // the join).
+  auto load = [&](u32x4 (&wb)[NB], int16_t (&sb)[NOWN], int p, int st) {
     // a descriptor per pass, over the pass's rows inside the matrix: a row past the matrix lies past the range,
     // which the per-lane offset is checked against, and reads zeros; the step goes into the scalar offset, and the
     // per-lane offsets stay the same in every pass
@@ -250,31 +260,27 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
     const unsigned so_s = static_cast<unsigned>(st * BSTEP * 2);
     const int lim = nblk - st * BSTEP;  // blocks from the tile's first to the row's end (wave-uniform)
     // The chunk's place in the step is wave-uniform and goes into the scalar offset too, so every chunk's load shares
-    // the one per-lane offset (a chunk past the row's end swaps it for the out-of-range one)
-    if (!first && lim >= BSTEP) {
+    // the one per-lane offset
 #pragma unroll
-      for (int i = 0; i < NOWN; ++i)  // the scales first: a chunk's dot then waits for its own weight load only
-        sc[i] = static_cast<int16_t>(
-            __builtin_amdgcn_raw_buffer_load_b16(srs, owner ? vo_sq : kOob, so_s + i * 4 * BPG * 2, 0));
+    for (int i = 0; i < NOWN; ++i) {  // the scales first: a chunk's dot then waits for its own weight load only
+      const bool ok = owner && gblk + (q + 4 * i) * BPG < lim;
+      sb[i] = static_cast<int16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_sq : kOob, so_s + i * 4 * BPG * 2, 0));
+    }
 #pragma unroll
-      for (int u = 0; u < NB; ++u) w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, vo_w, so_w + u * BPG * 64, 2);
-    } else {  // the row's last, partial step, and the first tile
-#pragma unroll
-      for (int i = 0; i < NOWN; ++i) {
-        const bool ok = owner && gblk + (q + 4 * i) * BPG < lim;
-        sc[i] = static_cast<int16_t>(
-            __builtin_amdgcn_raw_buffer_load_b16(srs, ok ? vo_sq : kOob, so_s + i * 4 * BPG * 2, 0));
-      }
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const bool ok = gblk + u * BPG < lim;
-        w[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w : kOob, so_w + u * BPG * 64, 2);
-      }
+    for (int u = 0; u < NB; ++u) {
+      const bool ok = gblk + u * BPG < lim;
+      wb[u] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? vo_w : kOob, so_w + u * BPG * 64, 2);
     }
   };
-  // The first tile's loads take the selecting form whatever the step: behind an if / else the compiler's wait
-  // counting loses their place after the staging loads, and the staging then waits for the weights as well.
-  load(0, 0, true);
+  load(w[0], sc[0], 0, 0);
+  int lp = 0, lst = 0;  // the next tile to load
+  auto advance = [&](int& p, int& st) {
+    if (++st == nsteps) {
+      st = 0;
+      ++p;
+    }
+  };
+  advance(lp, lst);
 
   // ---- stage the columns: LDS block b of column m = its 256 q8 values in order at (m * nblk_pad + b) * XB, then
   // meta[m * nblk_pad + b] = {d_x bits, -sum(x of the block)} for b < nblk_pad (zeros past nblk, so a chunk past the
@@ -392,88 +398,122 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  // the loop form's next tiles, issued once the staging is done: a staging pass that loads after them would wait for
+  // them too (loads retire in issue order)
+#pragma unroll
+  for (int d = 1; d < D; ++d) {
+    load(w[d], sc[d], lp, lst);
+    advance(lp, lst);
+  }
+
   // ---- stream the weights ----
   const unsigned char* xl = xs + gblk * XB + (q >> 1) * 128 + (q & 1) * 16;  // bytes 16q.. pair with x[(q/2)*128 + 32j + 16(q%2) ..]
   const int2* ml = meta + gblk;
   const uint64_t odd = __builtin_amdgcn_ballot_w64((q & 1) != 0), hi = __builtin_amdgcn_ballot_w64((q & 2) != 0);
   const CrumbMasks km = crumb_masks();
-  for (int p = 0; p < npass; ++p) {
+  float acc[MC];
+  int p = 0, st = 0;  // the tile being dotted: pass p, K step st
+  // Dot the tile in buffer (wb, sb), then (next) load tile t + D into it, past the wave's last tile a load of no rows
+  // (zeros, no memory touched); the pass's outputs are stored after its last step.
+  auto tile = [&](u32x4 (&wb)[NB], int16_t (&sb)[NOWN], bool next) {
     const int rl = p * RPW + grp;
     const int row = row_base + rl;
     const bool rv = rl < wave_rows && row < N;
-    float acc[MC];
+    if (st == 0) {
 #pragma unroll
-    for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
-    for (int st = 0; st < nsteps; ++st) {
-      if (p != 0 || st != 0) load(p, st, false);
-      const int tb = st * BSTEP;
-      const int lim = nblk - tb;  // blocks from the tile's first to the row's end (wave-uniform)
-      // the lane's partial dots of its chunks (16 x them in dp4a mode).  Slots past the row's end are skipped and hold
-      // arbitrary values: their scales and d_x are zero, so they add nothing
-      int pd[MC][NB];
+      for (int m = 0; m < MC; ++m) acc[m] = 0.0f;
+    }
+    const int tb = st * BSTEP;
+    const int lim = nblk - tb;  // blocks from the tile's first to the row's end (wave-uniform)
+    // the lane's partial dots of its chunks (16 x them in dp4a mode).  Slots past the row's end hold zero weights and
+    // zero scales and d_x, so they add nothing; the slots no lane of the wave has a block in (the row's last step) are
+    // skipped, except in the pipelined form, which dots them, since a branch there would make the compiler wait for
+    // every load in flight
+    int pd[MC][NB];
 #pragma unroll
-      for (int m = 0; m < MC; ++m)
+    for (int m = 0; m < MC; ++m)
 #pragma unroll
-        for (int u = 0; u < NB; ++u) pd[m][u] = 0;
+      for (int u = 0; u < NB; ++u) pd[m][u] = 0;
 #pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        if (u * BPG >= lim) break;  // no lane of the wave has a block in this slot or the next (the row's last step)
+    for (int u = 0; u < NB; ++u) {
+      if (D == 1 && u * BPG >= lim) break;
 #pragma unroll
-        for (int m = 0; m < MC; ++m) {
-          const unsigned char* xp = xl + (m * nblk_pad + tb + u * BPG) * XB;
-          u32x4 xv[4];
+      for (int m = 0; m < MC; ++m) {
+        const unsigned char* xp = xl + (m * nblk_pad + tb + u * BPG) * XB;
+        u32x4 xv[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
-          if constexpr (BYTES) {
-            u32x4 xo[4];
+        for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
+        if constexpr (BYTES) {
+          u32x4 xo[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xo[j] = *reinterpret_cast<const u32x4*>(xp + opl + 32 * j);
-            pd[m][u] = chunk_dot_bytes(w[u], xv, xo);
-          } else {
-            pd[m][u] = chunk_dot16(w[u], xv, km);
-          }
-          // the dot is computed here, in the slot's own block: sunk to the scaling after the loop it would keep every
-          // slot's activation pieces live at once (16 VGPRs a slot and column)
-          asm volatile("" : "+v"(pd[m][u]));
+          for (int j = 0; j < 4; ++j) xo[j] = *reinterpret_cast<const u32x4*>(xp + opl + 32 * j);
+          pd[m][u] = chunk_dot_bytes(wb[u], xv, xo);
+        } else {
+          pd[m][u] = chunk_dot16(wb[u], xv, km);
         }
-      }
-      if constexpr (STAMP) {  // the last step's dots issued
-        __builtin_amdgcn_sched_barrier(0);
-        t_dots = __builtin_amdgcn_s_memrealtime();
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // lane q completes and scales the blocks of slots q, q + 4: the exact dot s = the quad's sum (/ 16) - sum(x), then
-      // d_x * d_w * f32(s) (kernels.py:141 order)
-#pragma unroll
-      for (int i = 0; i < NOWN; ++i) {
-        if (4 * i * BPG >= lim) break;  // wave-uniform: every slot from 4i on lies past the row's end
-        const int u = NB >= 4 ? 4 * i + q : (owner ? q : 0);  // lanes q >= nb (nb < 4) own nothing: slot 0, d_w 0
-        const float dw = f16_bits_to_f32(sc[i]);
-#pragma unroll
-        for (int m = 0; m < MC; ++m) {
-          int v;  // the quad's sum for the lane's slot u
-          if constexpr (NB == 1)
-            v = group_sum(pd[m][0], 4);
-          else if constexpr (NB == 2)
-            v = quad_scatter2(pd[m][0], pd[m][1], odd);
-          else
-            v = quad_scatter4(pd[m][4 * i], pd[m][4 * i + 1], pd[m][4 * i + 2], pd[m][4 * i + 3], odd, hi);
-          const int2 mt = ml[m * nblk_pad + tb + u * BPG];
-          const int sb = (BYTES ? v : v >> 4) + mt.y;  // the block's exact dot
-          if (__builtin_expect(S != nullptr, 0)) {
-            const int b = tb + u * BPG + gblk;
-            if (owner && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = sb;
-          }
-          const float f = __int_as_float(mt.x) * dw * static_cast<float>(sb);
-          acc[m] += owner ? f : 0.0f;
-        }
+        // the dot is computed here, in the slot's own block: sunk to the scaling after the loop it would keep every
+        // slot's activation pieces live at once (16 VGPRs a slot and column)
+        asm volatile("" : "+v"(pd[m][u]));
       }
     }
-#pragma unroll
-    for (int m = 0; m < MC; ++m) {
-      const float v = group_sum(acc[m], LPR);
-      if ((lane & (LPR - 1)) == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+    if constexpr (STAMP) {  // the last step's dots issued
+      __builtin_amdgcn_sched_barrier(0);
+      t_dots = __builtin_amdgcn_s_memrealtime();
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // lane q completes and scales the blocks of slots q, q + 4: the exact dot s = the quad's sum (/ 16) - sum(x), then
+    // d_x * d_w * f32(s) (kernels.py:141 order)
+#pragma unroll
+    for (int i = 0; i < NOWN; ++i) {
+      if (D == 1 && 4 * i * BPG >= lim) break;  // wave-uniform: every slot from 4i on lies past the row's end
+      const int u = NB >= 4 ? 4 * i + q : (owner ? q : 0);  // lanes q >= nb (nb < 4) own nothing: slot 0, d_w 0
+      const float dw = f16_bits_to_f32(sb[i]);
+#pragma unroll
+      for (int m = 0; m < MC; ++m) {
+        int v;  // the quad's sum for the lane's slot u
+        if constexpr (NB == 1)
+          v = group_sum(pd[m][0], 4);
+        else if constexpr (NB == 2)
+          v = quad_scatter2(pd[m][0], pd[m][1], odd);
+        else
+          v = quad_scatter4(pd[m][4 * i], pd[m][4 * i + 1], pd[m][4 * i + 2], pd[m][4 * i + 3], odd, hi);
+        const int2 mt = ml[m * nblk_pad + tb + u * BPG];
+        const int s = (BYTES ? v : v >> 4) + mt.y;  // the block's exact dot
+        if (__builtin_expect(S != nullptr, 0)) {
+          const int b = tb + u * BPG + gblk;
+          if (owner && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
+        }
+        const float f = __int_as_float(mt.x) * dw * static_cast<float>(s);
+        acc[m] += owner ? f : 0.0f;
+      }
+    }
+    if (next && (D > 1 || lp < npass)) {  // one buffer: nothing to pipeline, no load past the wave's last tile
+      load(wb, sb, lp, lst);
+      advance(lp, lst);
+    }
+    if (st == nsteps - 1) {
+#pragma unroll
+      for (int m = 0; m < MC; ++m) {
+        const float v = group_sum(acc[m], LPR);
+        if ((lane & (LPR - 1)) == 0 && rv) Y[static_cast<int64_t>(m) * N + row] = v;
+      }
+    }
+    advance(p, st);
+  };
+  // Whole rounds of D tiles in the loop, with no branch that leaves a round midway (behind one, the loads in flight
+  // would reach the loop's head in two orders, and the compiler would wait for the stricter of them), then the last
+  // T mod D tiles straight-line, with nothing left to load
+  const int ntiles = npass * nsteps;
+  const int rounds = ONE ? 1 : ntiles / D;
+  for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) tile(w[d], sc[d], !ONE);
+  }
+  if constexpr (D > 1) {
+    const int rest = ntiles - rounds * D;  // wave-uniform
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (d < rest) tile(w[d], sc[d], false);
   }
   if constexpr (STAMP) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the wave's stores have completed
@@ -516,6 +556,12 @@ __global__ void __launch_bounds__(1024) tq2_lean_bytes_kernel(KOMP_TQ2_LEAN_ARGS
   tq2_lean_body<LPR, NB, MC, FUSED, ONE, false, true>(KOMP_TQ2_LEAN_PASS);
 }
 
+// The pipelined loop forms (PIPE above) of one column, dp4a and bytes mode.
+template <int LPR, int NB, bool FUSED, bool BYTES>
+__global__ void __launch_bounds__(1024) tq2_lean_pipe_kernel(KOMP_TQ2_LEAN_ARGS) {
+  tq2_lean_body<LPR, NB, 1, FUSED, false, false, BYTES, false, true>(KOMP_TQ2_LEAN_PASS);
+}
+
 #undef KOMP_TQ2_LEAN_ARGS
 #undef KOMP_TQ2_LEAN_PASS
 
@@ -524,6 +570,9 @@ __global__ void __launch_bounds__(1024) tq2_lean_bytes_kernel(KOMP_TQ2_LEAN_ARGS
 template <int LPR, int NB, int MC, bool FUSED, bool BYTES, bool STAMP = false>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   const bool one = p.passes == 1 && c.k / 256 <= (LPR / 4) * NB;
+  // the pipelined loop form for one column whose waves walk kPipeMinTiles tiles or more
+  const bool pipe = !STAMP && MC == 1 && !one && NB < 8 &&
+                    p.passes * ((c.k / 256 + (LPR / 4) * NB - 1) / ((LPR / 4) * NB)) >= kPipeMinTiles;
   decltype(&tq2_lean_kernel<LPR, NB, MC, FUSED, true, false>) kern;
   bool dma = false;
   if constexpr (STAMP) {
@@ -532,8 +581,14 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     kern = tq2_lean_stamped_kernel<LPR, NB, MC, FUSED>;
   } else if constexpr (BYTES) {
     kern = one ? tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, false>;
+    if constexpr (MC == 1 && NB < 8) {
+      if (pipe) kern = tq2_lean_pipe_kernel<LPR, NB, FUSED, true>;
+    }
   } else {
     kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, false> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, false>;
+    if constexpr (MC == 1 && NB < 8) {
+      if (pipe) kern = tq2_lean_pipe_kernel<LPR, NB, FUSED, false>;
+    }
     if constexpr (MC > 1 && !FUSED) {
       dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false);
       if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
@@ -550,8 +605,9 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   }
   const int nblk = c.k / 256;
   const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k, FUSED, 64 * p.waves, BYTES);
-  static std::atomic<unsigned> lds_limit[4][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
-  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[(one ? 1 : 0) + (dma ? 2 : 0)]);
+  static std::atomic<unsigned> lds_limit[5][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le =
+      allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[pipe ? 4 : (one ? 1 : 0) + (dma ? 2 : 0)]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));

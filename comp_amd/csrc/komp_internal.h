@@ -119,6 +119,11 @@ struct GemmCall {
   int64_t sw;
 };
 
+// The lean kernels' loop forms pipeline their weight loads (a second kernel form) for one column when a wave walks this
+// many tiles (passes x K steps) or more: the reference's knob plans, whose small workgroups walk whole rows in narrow
+// steps.  With fewer, the second buffer's registers cost more occupancy than the prefetch saves.
+constexpr int kPipeMinTiles = 3;
+
 // The lean kernels address one pass of a wave's rows with 32-bit per-lane offsets inside a buffer descriptor whose
 // range is capped at 0x7FFFFFF0 bytes, so every matrix's `rows_per_pass` row strides must fit below the cap; other
 // strides take the general kernel, which addresses rows in 64 bits.
@@ -198,6 +203,7 @@ hipError_t launch_split(int fmt, const uint8_t* w, uint8_t* wq, int16_t* ws, int
 hipError_t launch_quant_q8_0(const float* x, int8_t* xq, float* xd, int64_t nblocks, hipStream_t stream);
 hipError_t launch_quant_q8_K(const float* x, int8_t* xq, float* xd, int16_t* xb, int64_t nblocks, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream);
+hipError_t launch_clock(uint64_t* out, hipStream_t stream);
 hipError_t launch_dp4a_probe(const int32_t* a, const int32_t* b, const int32_t* c, int32_t* out, int64_t n, int mode,
                              hipStream_t stream);
 hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream);

@@ -122,6 +122,13 @@ __global__ void __launch_bounds__(512) stream_read_kernel(const u32x4* __restric
   if ((threadIdx.x & 63) == 0) OUT[static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6)] = acc;
 }
 
+// One lane writes the device's constant-rate real-time counter (the wave stamps' clock) to OUT[0] with a vector store:
+// where the stream reaches it, e.g. around a stretch of work inside a HIP graph.
+__global__ void __launch_bounds__(64) clock_kernel(uint64_t* __restrict__ OUT) {
+  const uint64_t t = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) OUT[0] = t;
+}
+
 template <typename F, typename... Args>
 hipError_t launch(int kind, F kern, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
   const Timing tm = timing_slot(kind);
@@ -156,6 +163,10 @@ hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* out, hip
   const int64_t n16 = bytes / 16;
   return launch(KIND_PROBE, stream_read_kernel, dim3(blocks_for(n16, 2048)), dim3(512), stream,
                 static_cast<const u32x4*>(src), n16, out);
+}
+
+hipError_t launch_clock(uint64_t* out, hipStream_t stream) {
+  return launch(KIND_PROBE, clock_kernel, dim3(1), dim3(64), stream, out);
 }
 
 hipError_t launch_q4_0_decode(const uint8_t* wq, int32_t* out, int64_t rows, hipStream_t stream) {

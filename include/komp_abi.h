@@ -241,6 +241,13 @@ int komp_timing_end(double* ms, int64_t* count);
 int komp_stamps_begin(uint32_t* buf, int64_t words);
 int komp_stamps_end(int64_t* words_used, int* clock_khz);
 
+/* Writes the same real-time counter (64 bits) to OUT[0] (device, 8-byte aligned) when `stream` reaches the call: a
+ * one-lane kernel that marks a point of the stream's work, where events cannot be recorded (inside a HIP graph; the
+ * benchmark times its K decode steps between two such marks of one graph).  komp_clock_khz gives the counter's rate.
+ * No reference counterpart (a measurement probe). */
+int komp_clock(uint64_t* OUT, void* stream);
+int komp_clock_khz(int* khz);
+
 #ifdef __cplusplus
 }
 #endif

@@ -269,3 +269,10 @@ def test_parse_stamps_walks_records_across_a_counter_wrap():
     assert list(recs[1]["entry"]) == [100, 100, 0] and recs[1]["span_ns"] == 1100
     with pytest.raises(_abi.KompError, match="header"):
         _abi.parse_stamps(np.array([1, 2, 3, 4], dtype=np.uint32), 100_000)
+
+
+def test_clock_rejects_bad_pointers():
+    lib = _abi.lib()
+    assert lib.komp_clock(None, None) == _abi.KOMP_EINVAL and "8-byte" in _abi.last_error()
+    assert lib.komp_clock(ctypes.c_void_p(12), None) == _abi.KOMP_EINVAL
+    assert lib.komp_clock_khz(None) == _abi.KOMP_EINVAL

@@ -82,3 +82,39 @@ def test_uncovered_and_overflowing_launches_run_unstamped():
     torch.cuda.synchronize()
     assert used == 0 and torch.equal(y_small, y_ref) and torch.equal(y_bytes, y_ref)
     assert int(small.abs().sum()) == 0
+
+
+def test_clock_marks_order_work_in_a_graph():
+    """komp_clock marks around the stream's work read increasing counter values, eager and inside a HIP graph, at a
+    rate the device reports (the benchmark's headline timing rests on them)."""
+    n, k = 6912, 2560
+    wq, ws, x = _problem(n, k, 1, 47)
+    wq_d, ws_d, x_d = dev(wq), dev(ws), dev(x)
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    marks = torch.zeros(3, dtype=torch.int64, device="cuda")
+    khz = _abi.clock_khz()
+    assert 1_000 <= khz <= 10_000_000
+    _abi.clock_into(marks[0:1])
+    host.gemv_f32_into("tq2_0", wq_d, ws_d, x_d, y, n, k)
+    _abi.clock_into(marks[1:2])
+    torch.cuda.synchronize()
+    t = marks.cpu().tolist()
+    assert t[1] > t[0] and (t[1] - t[0]) / khz < 100.0  # ms
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _abi.clock_into(marks[0:1])
+        for _ in range(4):
+            host.gemv_f32_into("tq2_0", wq_d, ws_d, x_d, y, n, k)
+        _abi.clock_into(marks[1:2])
+    for _ in range(3):
+        marks.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        t = marks.cpu().tolist()
+        assert t[1] > t[0] > 0 and t[2] == 0
+    y_ref, _ = host.gemv_f32("tq2_0", wq_d, ws_d, x_d, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)

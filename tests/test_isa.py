@@ -57,7 +57,11 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     # 3 x 10 blocks x 16 threads > 4 waves: staged through an LDS copy
     ("tq2_0", 16, 4, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 4, 3, false, true, true>"),
     ("tq2_0", 16, 2, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 2, 3, false, false, true>"),  # 10 blocks > 4 x 2
-    ("tq2_0", 128, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_kernel<4, 4, 1, false, false, false>"),  # two passes a wave
+    # two passes of 3 K steps a wave: 6 tiles, the pipelined loop form
+    ("tq2_0", 128, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_pipe_kernel<4, 4, false, false>"),
+    ("tq2_0", 64, 1, 4, 6912, 1, "gemv_tq2::tq2_lean_pipe_kernel<4, 1, false, false>"),  # the spec defaults: 27 tiles
+    ("q4_0", 64, 4, 4, 4096, 1, "gemv_q4::q4_lean_pipe_kernel<0, 4, 4, false>"),  # 8 K steps of 16 blocks
+    ("q4_0", 64, 4, 4, 4096, 2, "gemv_q4::q4_lean_kernel<0, 4, 4, 2, false, false>"),  # two columns: one buffer
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
     ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, false>"),  # one pass: one column only
     ("iq4_nl", 8, 2, 8, 8192, 1, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
@@ -123,3 +127,16 @@ def test_loops_classes_and_approx_on_synthetic_code():
     assert isa.approx_ops([(0, "v_exp_f32", "", None)]) == ["v_exp_f32"]
     assert isa.classify("buffer_load_ushort") == "ld16" and isa.classify("ds_read_b128") == "lds"
     assert isa.classify("v_mfma_i32_16x16x32_i8") == "mfma"
+
+
+def test_lean_and_gemm_instantiations_do_not_spill():
+    """Every lean GEMV and matrix-core GEMM instantiation of this build keeps its registers: no VGPR or SGPR spills
+    to scratch memory (the general kernel's rare explicit-knob forms, nb 16 with 3 columns in bytes or emulated mode,
+    are outside this check)."""
+    spills = []
+    for co in isa.library_code_objects():
+        for name, k in co.kernels.items():
+            lean_or_gemm = "lean" in name or "gemm_kernel" in name
+            if lean_or_gemm and (k["vgpr_spill"] or k["sgpr_spill"] or k["scratch"]):
+                spills.append((name[:90], k["vgpr_spill"], k["scratch"]))
+    assert not spills, spills
