@@ -51,7 +51,8 @@ def cmd_check(args):
     except (SpecError, OSError) as e:
         print(f"komp check: {e}", file=sys.stderr)
         return 2
-    print(f"ok {c['kernel']}: {c['weights']} {c['op']} target {c['target']} {c['arch']} {spec.label(c)}; tune space: "
+    arch = f"{c['arch_requested']} (run as {c['arch']})" if "arch_requested" in c else c["arch"]
+    print(f"ok {c['kernel']}: {c['weights']} {c['op']} target {c['target']} {arch} {spec.label(c)}; tune space: "
           f"{n} legal configs")  # fmt: skip
     return 0
 
@@ -172,8 +173,9 @@ def cmd_gen(args):
     except (SpecError, OSError) as e:
         print(f"komp gen: {e}", file=sys.stderr)
         return 2
-    if c["arch"] != "gfx950":
-        print(f"komp gen: arch {c['arch']}: this build holds gfx950 code only", file=sys.stderr)
+    if c["arch"] != "gfx950" or "arch_requested" in c:
+        print(f"komp gen: arch {c.get('arch_requested', c['arch'])}: this build holds gfx950 code only (set arch "
+              f"gfx950, or arch=gfx950 on the command line)", file=sys.stderr)  # fmt: skip
         return 2
     out = args[args.index("-o") + 1] if "-o" in args else None
     emit = (args[args.index("--emit") + 1] if "--emit" in args else "hsaco,s").split(",")

@@ -14,7 +14,10 @@
 Problem keys (n, k, m) give the shape `verify` runs on.  KURN's own parser (kurn.spec.parse / parse_overrides /
 SpecError) is not available, so this module carries a parser for the same grammar: one `key value` per line, `#`
 comments, integer values as ints, and a `tune` line of `key=v1,v2` lists.  Keys, defaults, legality and the tune-space
-expansion follow src/komp/spec.py:22-79; `arch` takes gfx950 (the reference's sm_* values are NVIDIA targets).
+expansion follow src/komp/spec.py:22-79; `arch` takes gfx950.  The reference's own specs name NVIDIA targets (`arch
+sm_80`, examples/q4_0_gemv_triton.kurn:6): `check` and `verify` accept an sm_* value as the spec's foreign target and
+run the gfx950 kernels (resolve keeps it as `arch_requested`); `gen`, which writes code objects for the spec's arch,
+refuses it.
 """
 
 from __future__ import annotations
@@ -107,6 +110,10 @@ def resolve(spec, overrides=None):
         if k not in KEYS and k not in COMMON and k not in ("n", "k", "m"):
             raise SpecError(f"unknown key {k!r} for target {c['target']}: expected one of "
                             f"{sorted((*KEYS, *COMMON, 'n', 'k', 'm'))}")  # fmt: skip
+    arch = c.get("arch")
+    if isinstance(arch, str) and arch.startswith("sm_") and arch[3:].isdigit():  # the reference's NVIDIA targets
+        c["arch_requested"] = arch
+        c["arch"] = "gfx950"
     for k, allowed in KEYS.items():
         c.setdefault(k, FORMAT_DEFAULTS[c["weights"]].get(k, DEFAULTS.get(k)))
         if c[k] not in allowed:

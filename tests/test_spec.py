@@ -41,7 +41,7 @@ def test_defaults_and_format_defaults():
 
 
 @pytest.mark.parametrize("bad,needle", [({"block_n": 33}, "block_n"), ({"nb": 3}, "nb"), ({"num_warps": 16}, "num_warps"),
-                                        ({"mode": "wmma"}, "mode"), ({"arch": "sm_80"}, "arch"), ({"k": 100}, "multiple"),
+                                        ({"mode": "wmma"}, "mode"), ({"arch": "gfx942"}, "arch"), ({"k": 100}, "multiple"),
                                         ({"target": "cuda"}, "target"), ({"weights": "q8_0"}, "weights"),
                                         ({"colour": 1}, "unknown key"), ({"m": 0}, "m=")])  # fmt: skip
 def test_illegal_specs(bad, needle):
@@ -98,3 +98,12 @@ def test_spec_command_and_kurn_registration(capsys):
     assert "q4_0_gemv_triton" in capsys.readouterr().out
     assert cli.spec_command("gen", [SPEC_Q4]) == 0
     assert cli.spec_command("mix", [SPEC_Q4]) == 2
+
+
+def test_reference_sm_arch_runs_as_gfx950():
+    """An sm_* arch (the reference's NVIDIA targets) resolves to gfx950 and is kept as arch_requested."""
+    base, _ = spec.load(SPEC_Q4)
+    c = spec.resolve(base, {"arch": "sm_80"})
+    assert c["arch"] == "gfx950" and c["arch_requested"] == "sm_80"
+    with pytest.raises(spec.SpecError, match="arch"):
+        spec.resolve(base, {"arch": "sm_x"})
