@@ -11,6 +11,9 @@ p 0.3/0.4/0.3, f16 d ~ U(0.01, 0.05)), the input N(0, 1), all resident in HBM be
 served from the 256 MB Infinity Cache ("cold").  The K timed steps run as HIP-graph replays, so the host launch rate
 does not bound them.
 
+Every timing is a stretch of calls captured into one HIP graph, between two device clock marks (komp_clock) after an
+untimed lead call, replayed once after the warm-up.
+
 Printed: one JSON line of a few KB.  value = algorithmic bytes of the K steps (per GEMV: weights + f32 activations in +
 f32 outputs) / their wall time (GB/s); roofline = the fused tq2_0_gemv launches' algorithmic bytes / their average
 in-graph span (first wave's entry to last wave's stored outputs, from the library's wave stamps over a graph of the same
@@ -166,28 +169,14 @@ def run_graph(torch, fn, count, replays):
     return g
 
 
-def timed_steps(torch, step, ncopies, steps, warmup, min_graph=64):
-    """Run `warmup` then exactly `steps` steps as graph replays; returns elapsed ms of the timed steps.  Each graph holds
-    a whole number of passes over the weight copies and at least `min_graph` steps, so the gap between two replays is
-    shared by many steps, as in a decode loop captured once."""
-    per_graph = ncopies * max(1, math.ceil(min_graph / ncopies))
-    g_full = run_graph(torch, step, per_graph, 1)
-    rem = steps % per_graph
-    g_rem = run_graph(torch, step, rem, 1) if rem else None
-    for _ in range(max(1, math.ceil(warmup / per_graph))):
-        g_full.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps // per_graph):
-        g_full.replay()
-    if g_rem is not None:
-        g_rem.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3
-    return e0.elapsed_time(e1), wall
+def timed_steps(torch, step, ncopies, steps, warmup):
+    """Run `warmup` untimed calls (graph replays), then exactly `steps` calls back to back inside one graph, between
+    two device clock marks after an untimed lead call (timed_one_graph); returns (ms of the calls, host wall ms of the
+    replay).  The per-call time of a decode loop captured once: no graph start falls inside the interval."""
+    from comp_amd import _abi
+
+    ms, wall, _ = timed_one_graph(torch, _abi, step, ncopies, steps, warmup)
+    return ms, wall
 
 
 def timed_one_graph(torch, abi, step, ncopies, steps, warmup):
@@ -786,6 +775,8 @@ def batched_calls(torch, host, args):
 COUNTER_CASES = (  # (fmt, N, K, columns, launch, mode): the kernels the hardware-counter tables cover
     ("tq2_0", 6912, 2560, 1, "fused", 2), ("tq2_0", 2560, 6912, 1, "fused", 2),
     ("tq2_0", 6912, 2560, 3, "fused", 2), ("tq2_0", 2560, 6912, 3, "fused", 2),
+    ("tq2_0", 6912, 2560, 2, "gemv", 2), ("tq2_0", 6912, 2560, 3, "gemv", 2),
+    ("tq2_0", 2560, 6912, 2, "gemv", 2), ("tq2_0", 2560, 6912, 3, "gemv", 2),
     ("tq2_0", 32768, 8192, 1, "gemv", 2), ("q4_0", 4096, 14336, 1, "gemv", 2), ("q4_0", 4096, 14336, 3, "gemv", 2),
     ("q4_0", 128256, 4096, 1, "gemv", 2), ("q4_0", 14336, 4096, 64, "gemm", 2),
     # bytes mode (every value unpacked to an integer, no dot instruction) beside dp4a
