@@ -175,11 +175,13 @@ def timed_steps(torch, step, ncopies, steps, warmup):
     replay).  The per-call time of a decode loop captured once: no graph start falls inside the interval."""
     from comp_amd import _abi
 
-    ms, wall, _ = timed_one_graph(torch, _abi, step, ncopies, steps, warmup)
+    # three warm replays: a shape's first stretch measured after a single one ran 3-5% slow (the first plan of a knob
+    # sweep read 12.29 us against 11.95 for the same plan measured later)
+    ms, wall, _ = timed_one_graph(torch, _abi, step, ncopies, steps, warmup, warm_replays=3)
     return ms, wall
 
 
-def timed_one_graph(torch, abi, step, ncopies, steps, warmup):
+def timed_one_graph(torch, abi, step, ncopies, steps, warmup, warm_replays=1):
     """The headline's timing: `warmup` untimed steps (graph replays), then ONE graph holding a lead step, a clock mark,
     exactly `steps` steps and a second clock mark, replayed once.  The marks are the library's one-lane komp_clock
     kernel writing the device's real-time counter, since the runtime records no events inside a graph; the graph's
@@ -205,7 +207,7 @@ def timed_one_graph(torch, abi, step, ncopies, steps, warmup):
     if warmup > 0:
         per_graph = ncopies * max(1, math.ceil(64 / ncopies))
         g_warm = run_graph(torch, step, min(per_graph, warmup), 1)
-        for _ in range(math.ceil(warmup / per_graph)):
+        for _ in range(max(warm_replays, math.ceil(warmup / per_graph))):
             g_warm.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
