@@ -280,9 +280,24 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
     }
   }
   const int64_t c16 = (m + 15) / 16;
-  const int64_t groups = (c16 + 3) / 4;
-  const int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
-  const double r = static_cast<double>((n + 15) / 16) * groups / device_cus();
+  int64_t groups = (c16 + 3) / 4;
+  int cn = static_cast<int>(groups > 0 ? (c16 + groups - 1) / groups : 1);
+  const int64_t tiles = (n + 15) / 16;
+  double r = static_cast<double>(tiles) * groups / device_cus();
+  // Few row tiles a CU: fewer column tiles a workgroup, in more column groups (each reads its rows' weights again,
+  // mostly from L2).  4 column tiles and at most 2 row tiles a CU: halve until each CU has more than 2; at 64 columns
+  // Q4_0 4096 x 4096 16.3 -> 15.0 us, 4096 x 14336 46.0 -> 40.2, TQ2_0 2560 x 6912 18.6 -> 14.7 (one column tile a
+  // workgroup), TQ2_0 6912 x 2560 14.7 -> 12.0 (two).  3 column tiles with idle CUs: one column tile a workgroup
+  // (TQ2_0 2560 x 6912 at 48 columns 14.5 -> 11.9 us; at 4096 rows, one tile a CU, splitting measured slower).
+  const auto regroup = [&](int to) {
+    cn = to;
+    groups = (c16 + cn - 1) / cn;
+    r = static_cast<double>(tiles) * groups / device_cus();
+  };
+  if (cn == 4)
+    while (r <= 2.0 && cn > 1) regroup(cn / 2);
+  else if (cn == 3 && r < 1.0)
+    regroup(1);
   GemmPlan q = {8, 1, 1, cn, 2};
   if (r > 8.0)
     q = cn == 1 ? GemmPlan{1, 8, m > 8 && fmt != FMT_Q8_0 ? 2 : 1, 1, 2} : GemmPlan{1, 8, 1, cn, cn == 2 ? 2 : 1};
@@ -294,8 +309,9 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
     // two row tiles a wave: each activation load feeds twice the MFMAs (the activations are re-read for every row
     // tile, 8x the weight bytes a step at 64 columns); 4 waves from 4 row tiles a CU.  Q4_0 14336 x 4096 at 32 / 48 /
     // 64 columns: 32.0 / 44.2 / 56.1 -> 23.7 / 30.3 / 37.7 us; 28672 x 4096 at 64: 108 -> 67 us; TQ2_0 14336 x 4096
-    // at 64: 44.6 -> 27.2 us
-    q = r > 4.0 ? GemmPlan{2, 2, 2, cn, 2} : GemmPlan{4, 2, 2, cn, 2};
+    // at 64: 44.6 -> 27.2 us.  Past 3 tiles a CU, K split 2 ways (4 waves a workgroup, fewer partial sums to add):
+    // Q4_0 14336 x 4096 at 64 columns 35.4 -> 34.3 us
+    q = r > 3.0 ? GemmPlan{2, 2, 2, cn, 2} : GemmPlan{4, 2, 2, cn, 2};
   else if (r > 1.25 && cn > 1)
     q = GemmPlan{4, 2, 1, cn, 2};
   while (gemm_lds_bytes(fmt, q, static_cast<int>(k)) > kLdsMax && q.wn * q.wr > 1) {  // long rows: fewer rows a group

@@ -131,6 +131,7 @@ gemm_kernel(int N, int M, int K, int nblk, int64_t SW, const uint8_t* __restrict
   const int r16 = lane & 15;
   const int g = lane >> 4;
   const int n0 = blockIdx.x * WGR;
+  if (n0 >= N) return;  // a padding workgroup (see launch_s): the whole workgroup leaves before any barrier
   const int nw = n0 + 16 * WN * wr;  // first row of this wave's tiles
   const int m0 = blockIdx.y * (16 * CN);
   const int rows = max(0, min(16 * WN, N - nw));  // valid rows of this wave's tiles, valid columns of the workgroup
@@ -566,7 +567,11 @@ namespace {
 template <int FMT, int WK, int WR, int WN, int CN, int D, bool STORE_S>
 hipError_t launch_s(const GemmCall& c, const GemmPlan& p, hipStream_t stream) {
   const int nblk = c.k / fmt_info(FMT).block;
-  const dim3 grid((c.n + 16 * WN * WR - 1) / (16 * WN * WR), (c.m + 16 * CN - 1) / (16 * CN));
+  // Workgroups go to the 8 XCDs round-robin by linear id (x fastest).  With several column groups the row groups are
+  // padded to a multiple of 8, so every column group of a row group runs on one XCD and reads the rows' weights from
+  // that XCD's L2 after the first; the padding workgroups exit at once.
+  const unsigned gx = (c.n + 16 * WN * WR - 1) / (16 * WN * WR), gy = (c.m + 16 * CN - 1) / (16 * CN);
+  const dim3 grid(gy > 1 ? (gx + 7) / 8 * 8 : gx, gy);
   const dim3 block(64 * WK * WR);
   const size_t lds = gemm_lds_bytes(FMT, p, c.k);
   auto kern = gemm_impl::gemm_kernel<FMT, WK, WR, WN, CN, D, STORE_S>;

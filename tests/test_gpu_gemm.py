@@ -81,6 +81,8 @@ FAMILIES = [
     (33600, 256, 4, 128, 16),   # > 8 per CU: 8 waves, each its own rows
     (33600 - 5, 256, 12, 256, 16),  # ... 2 row tiles each
     (16400, 256, 70, 128, 48),  # ... 3 column tiles, 2 column groups
+    (4096, 512, 64, 64, 16),    # 4 column tiles over 1 row tile per CU: 4 column groups of 1 tile (4 x 2 waves)
+    (6912, 256, 64, 64, 32),    # ... over 1.7 per CU: 2 column groups of 2 tiles (2 x 2 waves; Q8_0: 2 x 4)
 ]
 
 
