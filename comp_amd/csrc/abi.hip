@@ -182,9 +182,9 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     // 3 columns: 15.8 against 24.7 us fused, 9.3 against 10.2 with q8 in).
     if (waves <= 16 && (m == 1 || waves >= 7)) {
       const int64_t blocks_per_slot = lpr / bpb;
-      // the 16-wave instantiations: nb up to 8 for one column, 4 for two and three (Q4_K: 4, 4 VGPRs of scales per
-      // slot)
-      const int nb_max = fmt == FMT_Q4_K || m > 1 ? 4 : 8;
+      // the 16-wave instantiations: nb up to 8 for one column, 4 for two and three; Q4_K 2 (its lean kernel's rows
+      // of 56 blocks in two steps of 32 ran 9.0 us at 4096 x 14336 fused, in one of 64 10.0)
+      const int nb_max = fmt == FMT_Q4_K ? 2 : (m > 1 ? 4 : 8);
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
       nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
       // past 8 waves, two or three columns (and bytes mode) run this plan on the lean kernels only: the general kernel
@@ -200,10 +200,24 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
         return plan_of(static_cast<int>(wg_rows), nb, static_cast<int>(waves), lpr, 1);
     }
   }
+  if (fmt == FMT_Q4_K && mode == KOMP_MODE_DP4A && m <= 3) {
+    // the Q4_K lean kernel (32-byte slots, 4 lanes a block): nb 2, 32 lanes a row for rows of up to 16 blocks (one
+    // K step), 64 for longer ones; the long rows in one workgroup of one row a wave per CU when that is at most 16
+    // waves; otherwise one column over 4 waves, two and three over 8.  Measured on MI355X against the other lean
+    // plans (1 column: 4096 x 4096 3.8 us, 14336 x 4096 7.6, 4096 x 14336 8.1; 3 columns at 14336 x 4096 10.2, at
+    // 4096 x 14336 11.7 against 12.5 over 8 waves), from 4.6 / 8.9 / 10.3 / 13.9 on the general kernel's plans
+    const int lq = chunks <= 64 ? 32 : 64;
+    int nbq = pow2_ceil((chunks + lq - 1) / lq);
+    nbq = nbq > 2 ? 2 : nbq;
+    const int64_t per_cu = (n + device_cus() - 1) / device_cus();
+    if (lq == 64 && per_cu <= 16) return plan_of(static_cast<int>(per_cu), nbq, static_cast<int>(per_cu), 64, 1);
+    const int wq = m > 1 ? 8 : 4;
+    return plan_of(wq * (64 / lq), nbq, wq, lq, 1);
+  }
   if (fmt == FMT_Q4_K) {
-    // Q4_K (32-byte slots): about two slots per lane (four from 12288 rows on), nb <= 2, and 8-16 rows per workgroup
-    // of at least 4 waves.  Measured on MI355X at 4096-14336 rows x 2560-14336 columns, 1 column: 10-25% faster
-    // than the 16-byte-chunk rules below.
+    // Q4_K (32-byte slots) on the general kernel (bytes and emulated modes): about two slots per lane (four from
+    // 12288 rows on), nb <= 2, and 8-16 rows per workgroup of at least 4 waves.  Measured on MI355X at 4096-14336
+    // rows x 2560-14336 columns, 1 column: 10-25% faster than the 16-byte-chunk rules below.
     int lq = pow2_ceil(n >= 12288 ? (chunks + 3) / 4 : (chunks + 1) / 2);
     lq = lq < bpb ? bpb : (lq > 64 ? 64 : lq);
     int nbq = pow2_ceil((chunks + lq - 1) / lq);

@@ -8,7 +8,9 @@ hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStrea
   if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, true>(c, p, stream);
   if (c.fmt == FMT_IQ4_NL)
     return q4_lean_eligible(c, p) ? launch_gemv_q4_lean(c, p, stream) : gemv_impl::by_mode<FMT_IQ4_NL, true>(c, p, stream);
-  return c.fmt == FMT_Q4_K ? launch_gemv_q4_k_fused(c, p, stream) : hipErrorInvalidValue;
+  if (c.fmt == FMT_Q4_K)
+    return q4k_lean_eligible(c, p) ? launch_gemv_q4k_lean(c, p, stream) : launch_gemv_q4_k_fused(c, p, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace komp

@@ -22,7 +22,7 @@ def run(*args):
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
     for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_tq2::tq2_lean_bytes_kernel<",
-                   "gemv_q4::q4_lean_kernel<",
+                   "gemv_q4::q4_lean_kernel<", "gemv_q4k::q4k_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
         assert any(family in n for n in names), family
@@ -30,7 +30,8 @@ def test_library_holds_gfx950_code_objects_with_every_kernel_family():
 
 @pytest.mark.parametrize("fmt,bn,nb,nw,name", [("q4_0", 64, 4, 4, "gemv_q4::q4_lean_kernel<0, 4, 4, 1, false, false>"),
                                                ("tq2_0", 32, 2, 4, "gemv_tq2::tq2_lean_kernel<8, 2, 1, false, false, false>"),
-                                               ("iq4_nl", 8, 2, 8, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>")])
+                                               ("iq4_nl", 8, 2, 8, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
+                                               ("q4_k", 64, 4, 4, "gemv_q4k::q4k_lean_kernel<4, 4, 1, false, false>")])
 def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     # one column in dp4a mode runs the single-column kernel with 64 / min(block_n / num_warps, 16) lanes per row
     assert cli._gemv_kernel(fmt, 2, nb, 1, bn, nw) == name
@@ -65,10 +66,14 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
     ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, false>"),  # one pass: one column only
     ("iq4_nl", 8, 2, 8, 8192, 1, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
+    ("q4_k", 8, 2, 4, 4096, 1, "gemv_q4k::q4k_lean_kernel<32, 2, 1, false, true>"),    # 16 blocks <= 8 x 2
+    ("q4_k", 16, 2, 8, 4096, 3, "gemv_q4k::q4k_lean_kernel<32, 2, 3, false, true>"),   # any column count
+    ("q4_k", 16, 2, 16, 14336, 1, "gemv_q4k::q4k_lean_kernel<64, 2, 1, false, false>"),  # 56 blocks: two K steps
 ])  # fmt: skip
 def test_single_pass_form_follows_the_launch(fmt, bn, nb, nw, k, m, name):
     """With K known, the name carries the single-pass flag the launch computes (one pass of rows, one K step; the
-    Q4 kernels only for one column), and the single-pass form's report is its straight-line weight stream."""
+    Q4_0 / IQ4_NL kernels only for one column), and the single-pass form's report is its straight-line weight
+    stream."""
     assert cli._gemv_kernel(fmt, 2, nb, m, bn, nw, k) == name
     r = isa.summary(name, cli.VALUES_PER_LOAD[fmt])
     assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"]
