@@ -106,7 +106,7 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     one pass>; tq2_0 when LDS holds the 16-bit activations); everything else the general gemv_kernel <format, mode,
     columns, nb, fused>.  "One pass" is
     the lean kernel's single-pass, single-K-step form, which the launch picks when the rows per wave fit one pass and a
-    row's K blocks one step (the single-column form only for q4_0 / iq4_nl); without k the loop form is named.  The
+    row's K blocks one step; without k the loop form is named.  The
     LDS-copy form stages two or three tq2_0 columns that need more than one pass of the workgroup's threads, when LDS
     holds them.  One column with nb < 8 whose waves walk 3 tiles or more (passes x K steps; k given) runs the
     pipelined loop form instead (q4_lean_pipe_kernel <format, lanes, nb, fused>, q4_lean_bytes_pipe_kernel <lanes, nb,
@@ -143,7 +143,7 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
             one = one_pass and k // 256 <= (lanes // 4) * nb
             return f"gemv_q4k::q4k_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
         elif fmt in ("q4_0", "iq4_nl"):
-            one = one_pass and cols == 1 and k // 32 <= lanes * nb
+            one = one_pass and k // 32 <= lanes * nb
             if pipe and not one:
                 if mode == 0:
                     return f"gemv_q4::q4_lean_bytes_pipe_kernel<{lanes}, {nb}, false>"

@@ -364,13 +364,13 @@ __global__ void __launch_bounds__(1024) q4_lean_bytes_pipe_kernel(KOMP_Q4_LEAN_A
 
 template <int FMT, int G, int NB, int MC, bool FUSED, bool BYTES>
 hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  // the single-pass, single-step form for one column (the decode case; two and three columns keep the general one);
-  // the pipelined loop form for one column whose waves walk kPipeMinTiles tiles or more
-  const bool one = MC == 1 && p.passes == 1 && c.k / 32 <= G * NB;
+  // the single-pass, single-step form (a straight-line weight stream) for every plan of one pass and one K step; the
+  // pipelined loop form for one column whose waves walk kPipeMinTiles tiles or more
+  const bool one = p.passes == 1 && c.k / 32 <= G * NB;
   const bool pipe = MC == 1 && !one && NB < 8 && p.passes * ((c.k / 32 + G * NB - 1) / (G * NB)) >= kPipeMinTiles;
-  auto kern = one ? q4_lean_kernel<FMT, G, NB, MC, FUSED, MC == 1> : q4_lean_kernel<FMT, G, NB, MC, FUSED, false>;
+  auto kern = one ? q4_lean_kernel<FMT, G, NB, MC, FUSED, true> : q4_lean_kernel<FMT, G, NB, MC, FUSED, false>;
   if constexpr (BYTES)
-    kern = one ? q4_lean_bytes_kernel<G, NB, MC, FUSED, MC == 1> : q4_lean_bytes_kernel<G, NB, MC, FUSED, false>;
+    kern = one ? q4_lean_bytes_kernel<G, NB, MC, FUSED, true> : q4_lean_bytes_kernel<G, NB, MC, FUSED, false>;
   if constexpr (MC == 1 && NB < 8) {
     if (pipe) kern = BYTES ? q4_lean_bytes_pipe_kernel<G, NB, FUSED> : q4_lean_pipe_kernel<FMT, G, NB, FUSED>;
   }

@@ -64,16 +64,15 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     ("q4_0", 64, 4, 4, 4096, 1, "gemv_q4::q4_lean_pipe_kernel<0, 4, 4, false>"),  # 8 K steps of 16 blocks
     ("q4_0", 64, 4, 4, 4096, 2, "gemv_q4::q4_lean_kernel<0, 4, 4, 2, false, false>"),  # two columns: one buffer
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
-    ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, false>"),  # one pass: one column only
+    ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, true>"),   # any column count
     ("iq4_nl", 8, 2, 8, 8192, 1, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
     ("q4_k", 8, 2, 4, 4096, 1, "gemv_q4k::q4k_lean_kernel<32, 2, 1, false, true>"),    # 16 blocks <= 8 x 2
     ("q4_k", 16, 2, 8, 4096, 3, "gemv_q4k::q4k_lean_kernel<32, 2, 3, false, true>"),   # any column count
     ("q4_k", 16, 2, 16, 14336, 1, "gemv_q4k::q4k_lean_kernel<64, 2, 1, false, false>"),  # 56 blocks: two K steps
 ])  # fmt: skip
 def test_single_pass_form_follows_the_launch(fmt, bn, nb, nw, k, m, name):
-    """With K known, the name carries the single-pass flag the launch computes (one pass of rows, one K step; the
-    Q4_0 / IQ4_NL kernels only for one column), and the single-pass form's report is its straight-line weight
-    stream."""
+    """With K known, the name carries the single-pass flag the launch computes (one pass of rows, one K step), and the
+    single-pass form's report is its straight-line weight stream."""
     assert cli._gemv_kernel(fmt, 2, nb, m, bn, nw, k) == name
     r = isa.summary(name, cli.VALUES_PER_LOAD[fmt])
     assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and not r["approx"]
