@@ -100,8 +100,8 @@ FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kern
 def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     """The kernel instantiation a launch of this config runs, the knobs giving lanes per row = 64 / min(block_n /
     num_warps, 16): in dp4a mode, q4_0 / iq4_nl / tq2_0 with 1-3 columns (nb <= 4, or 8 for one column) run the lean
-    kernel <(format,) lanes per row, nb, columns, fused, one pass(, tq2_0: staged through an LDS copy)> (q4_k: nb <= 4,
-    q4k_lean_kernel <lanes per row, nb, columns, fused, one pass>), and tq2_0 /
+    kernel <(format,) lanes per row, nb, columns, fused, one pass(, tq2_0: staged through an LDS copy)> (q8_0:
+    q8_lean_kernel, q4_k with nb <= 4: q4k_lean_kernel, both <lanes per row, nb, columns, fused, one pass>), and tq2_0 /
     q4_0 in bytes mode its bytes form (tq2_lean_bytes_kernel / q4_lean_bytes_kernel <lanes per row, nb, columns, fused,
     one pass>; tq2_0 when LDS holds the 16-bit activations); everything else the general gemv_kernel <format, mode,
     columns, nb, fused>.  "One pass" is
@@ -139,6 +139,9 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
                 dma = (staged + 15) // 16 * 16 + cols * k + cols * (k // 256) * 4 <= 160 * 1024
             return (f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}, "
                     f"{str(dma).lower()}>")
+        elif fmt == "q8_0" and mode == 2:
+            one = one_pass and k // 32 <= (lanes // 2) * nb
+            return f"gemv_q8::q8_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
         elif fmt == "q4_k" and mode == 2 and nb <= 4:
             one = one_pass and k // 256 <= (lanes // 4) * nb
             return f"gemv_q4k::q4k_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"

@@ -5,7 +5,8 @@
 namespace komp {
 
 hipError_t launch_gemv_more_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
-  if (c.fmt == FMT_Q8_0) return gemv_impl::by_mode<FMT_Q8_0, true>(c, p, stream);
+  if (c.fmt == FMT_Q8_0)
+    return q8_lean_eligible(c, p) ? launch_gemv_q8_lean(c, p, stream) : gemv_impl::by_mode<FMT_Q8_0, true>(c, p, stream);
   if (c.fmt == FMT_IQ4_NL)
     return q4_lean_eligible(c, p) ? launch_gemv_q4_lean(c, p, stream) : gemv_impl::by_mode<FMT_IQ4_NL, true>(c, p, stream);
   if (c.fmt == FMT_Q4_K)

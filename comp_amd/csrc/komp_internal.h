@@ -192,6 +192,11 @@ hipError_t launch_gemv_tq2_lean_bytes(const GemvCall& c, const GemvPlan& p, hipS
 bool tq2_lean_stampable(const GemvCall& c, const GemvPlan& p);
 hipError_t launch_gemv_tq2_lean_stamped(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 // Q4_0 and IQ4_NL, 1-3 columns in dp4a mode (gemv_q4.hip), and Q4_0 in bytes mode (gemv_q4_bytes.hip)
+bool q8_lean_eligible(const GemvCall& c, const GemvPlan& p);
+size_t q8_lean_lds_bytes(int lpr, int nb, int mc, int k);
+hipError_t launch_gemv_q8_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv_q8_lean_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
+
 bool q4k_lean_eligible(const GemvCall& c, const GemvPlan& p);
 size_t q4k_lean_lds_bytes(int lpr, int nb, int mc, int k);
 hipError_t launch_gemv_q4k_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);

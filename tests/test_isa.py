@@ -22,7 +22,7 @@ def run(*args):
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
     for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_tq2::tq2_lean_bytes_kernel<",
-                   "gemv_q4::q4_lean_kernel<", "gemv_q4k::q4k_lean_kernel<",
+                   "gemv_q4::q4_lean_kernel<", "gemv_q4k::q4k_lean_kernel<", "gemv_q8::q8_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
         assert any(family in n for n in names), family
@@ -66,6 +66,8 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
     ("q4_0", 8, 2, 8, 4096, 3, "gemv_q4::q4_lean_kernel<0, 64, 2, 3, false, true>"),   # any column count
     ("iq4_nl", 8, 2, 8, 8192, 1, "gemv_q4::q4_lean_kernel<3, 64, 2, 1, false, false>"),
+    ("q8_0", 8, 4, 8, 4096, 1, "gemv_q8::q8_lean_kernel<64, 4, 1, false, true>"),     # 128 blocks <= 32 x 4
+    ("q8_0", 16, 4, 4, 4096, 3, "gemv_q8::q8_lean_kernel<16, 4, 3, false, false>"),    # 32 blocks a step: 4 steps
     ("q4_k", 8, 2, 4, 4096, 1, "gemv_q4k::q4k_lean_kernel<32, 2, 1, false, true>"),    # 16 blocks <= 8 x 2
     ("q4_k", 16, 2, 8, 4096, 3, "gemv_q4k::q4k_lean_kernel<32, 2, 3, false, true>"),   # any column count
     ("q4_k", 16, 2, 16, 14336, 1, "gemv_q4k::q4k_lean_kernel<64, 2, 1, false, false>"),  # 56 blocks: two K steps
