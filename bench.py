@@ -781,6 +781,7 @@ COUNTER_CASES = (  # (fmt, N, K, columns, launch, mode): the kernels the hardwar
     ("tq2_0", 2560, 6912, 2, "gemv", 2), ("tq2_0", 2560, 6912, 3, "gemv", 2),
     ("tq2_0", 32768, 8192, 1, "gemv", 2), ("q4_0", 4096, 14336, 1, "gemv", 2), ("q4_0", 4096, 14336, 3, "gemv", 2),
     ("q4_0", 128256, 4096, 1, "gemv", 2), ("q4_0", 14336, 4096, 64, "gemm", 2),
+    ("q4_k", 14336, 4096, 1, "gemv", 2), ("q8_0", 14336, 4096, 1, "gemv", 2),
     # bytes mode (every value unpacked to an integer, no dot instruction) beside dp4a
     ("tq2_0", 6912, 2560, 1, "fused", 0), ("tq2_0", 32768, 8192, 1, "gemv", 0), ("q4_0", 4096, 14336, 1, "gemv", 0),
 )  # fmt: skip

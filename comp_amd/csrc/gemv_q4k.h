@@ -19,7 +19,10 @@ namespace komp {
 namespace gemv_q4k {
 
 constexpr unsigned kOob = 0x7FFFFFF0u;   // a buffer offset past every descriptor's range: the load returns zeros
-constexpr int kBlockStride = 288;        // LDS bytes per staged 256-value block (consecutive blocks start 8 banks on)
+// LDS bytes per staged 256-value block: 80 dwords, so that with the pieces rotated (below) the 16-byte reads of
+// consecutive lanes (lane q of a quad reads 64 bytes at 64q of its block, neighbouring quads the next blocks) fall on
+// distinct banks, for 32 or 64 banks
+constexpr int kBlockStride = 320;
 constexpr size_t kLdsLimit = 160 * 1024;
 
 // A raw buffer descriptor over `bytes` (at most 0x7FFFFFF0: one pass's rows, which the plans keep below 2^31 bytes).
@@ -129,7 +132,9 @@ __device__ __forceinline__ void q4k_lean_body(int N1, int nblk, int SW1, int nse
   };
   advance(lp, lst);
 
-  // ---- stage the columns: block b of column m (LDS slot m * nblk_pad + b) = its 256 q8 values in order at slot * XB;
+  // ---- stage the columns: block b of column m (LDS slot m * nblk_pad + b) = its 256 q8 values at slot * XB, as 16
+  // pieces of 16 bytes with piece 4j + i (j = the 64-value group, i its quarter) at position 4j + (i + j) % 4 (lane q
+  // reads its group's quarter i at instruction i, so the four lanes of a quad read four different bank ranges);
   // bs[slot][i] = the int32 sum of sub-block i's 32 values (two q8_K bsums); dx[slot] = d_x.  Slots past nblk hold
   // zero sums and d_x, so a block past the row's end (zero weights and scales) adds exact zeros ----
   unsigned char* xs = lds;
@@ -159,7 +164,7 @@ __device__ __forceinline__ void q4k_lean_body(int N1, int nblk, int SW1, int nse
       for (int t = 0; t < 4; ++t) s16 = __builtin_amdgcn_sdot4(static_cast<int>(qv[t]), 0x01010101, s16, false);
     }
     const int s32 = group_sum(s16, 2);  // lanes r, r ^ 1 hold the two halves of sub-block r / 2
-    *reinterpret_cast<u32x4*>(xs + b * XB + r * 16) = qv;
+    *reinterpret_cast<u32x4*>(xs + b * XB + ((r & ~3) | (((r & 3) + (r >> 2)) & 3)) * 16) = qv;
     if ((r & 1) == 0) bs[b * 8 + (r >> 1)] = s32;
     if (r == 0) dxs[b] = d;
   };
@@ -197,7 +202,10 @@ __device__ __forceinline__ void q4k_lean_body(int N1, int nblk, int SW1, int nse
   asm volatile("" ::: "memory");
 
   // ---- stream the weights ----
-  const unsigned char* xl = xs + gblk * XB + q * 64;  // lane q's 64 activations: sub-blocks 2q, 2q + 1
+  const unsigned char* xl = xs + gblk * XB;  // lane q's 64 activations (sub-blocks 2q, 2q + 1): quarter i at xo[i]
+  unsigned xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xo[i] = static_cast<unsigned>((4 * q + ((i + q) & 3)) * 16);
   const int* bl = bs + gblk * 8 + 2 * q;
   const float* dl = dxs + gblk;
   // the lane's scale selection (gemv_impl::q4_k_scale_pair): sub-blocks 2q, 2q + 1 are bytes 2 (q & 1), +1 of the
@@ -227,8 +235,10 @@ __device__ __forceinline__ void q4k_lean_body(int N1, int nblk, int SW1, int nse
 #pragma unroll
       for (int m = 0; m < MC; ++m) {
         const int bo = m * nblk_pad + tb + u * BPG;  // the slot's first block (the lane's is bo + gblk)
-        const u32x4* xp = reinterpret_cast<const u32x4*>(xl + bo * XB);
-        const int2 dd = gemv_impl::q4_k_group_dots<MODE_DP4A>(w[u], w2[u], xp[0], xp[1], xp[2], xp[3]);
+        const unsigned char* xp = xl + bo * XB;
+        const int2 dd = gemv_impl::q4_k_group_dots<MODE_DP4A>(
+            w[u], w2[u], *reinterpret_cast<const u32x4*>(xp + xo[0]), *reinterpret_cast<const u32x4*>(xp + xo[1]),
+            *reinterpret_cast<const u32x4*>(xp + xo[2]), *reinterpret_cast<const u32x4*>(xp + xo[3]));
         const int2 xsum = *reinterpret_cast<const int2*>(bl + bo * 8);
         // 24-bit multiplies (full rate): |dots| < 2^16, |sums| < 2^13, scales and mins < 64
         const int sd = __mul24(static_cast<int>(scm & 0xFFu), dd.x) + __mul24(static_cast<int>((scm >> 8) & 0xFFu), dd.y);

@@ -119,11 +119,12 @@ __device__ __forceinline__ void q8_lean_body(int N1, int nblk, int SW1, int nseg
   };
   advance(lp, lst);
 
-  // ---- stage the columns: xh[0][m][b] = activations 0..15 of block b of column m, xh[1][m][b] = 16..31, dxs[m][b] =
-  // d_x, for b < nblk_pad (zeros past nblk, so a block past the row's end adds 0); column m at m * nblk_pad ----
-  u32x4* xl = reinterpret_cast<u32x4*>(lds);
-  u32x4* xh = xl + MC * nblk_pad;
-  float* dxs = reinterpret_cast<float*>(xh + MC * nblk_pad);
+  // ---- stage the columns: x2[2 slot] = activations 0..15 of the block in LDS slot m * nblk_pad + b (block b of
+  // column m), x2[2 slot + 1] = 16..31 (the halves interleaved, so the lanes of a pair, and neighbouring pairs, read
+  // consecutive 16-byte pieces: no bank conflicts), dxs[slot] = d_x, for b < nblk_pad (zeros past nblk, so a block
+  // past the row's end adds 0) ----
+  u32x4* x2 = reinterpret_cast<u32x4*>(lds);
+  float* dxs = reinterpret_cast<float*>(x2 + 2 * MC * nblk_pad);
   auto slot = [&](int i) {  // flattened block i of the columns -> its LDS slot
     if constexpr (MC == 1) return i;
     const int m = i / nblk;
@@ -136,7 +137,7 @@ __device__ __forceinline__ void q8_lean_body(int N1, int nblk, int SW1, int nseg
     float d;
     int qsum;
     const unsigned packed = q8_0_group8(v, d, qsum);  // the quant_q8_0 arithmetic (byte-identical planes)
-    reinterpret_cast<unsigned*>(e < 4 ? xl + b : xh + b)[e & 3] = packed;
+    reinterpret_cast<unsigned*>(x2 + 2 * b + (e >> 2))[e & 3] = packed;
     if (e == 0) dxs[b] = d;
     if (__builtin_expect(blockIdx.x == 0 && XQo != nullptr, 0)) {  // one workgroup writes the q8_0 planes out
       reinterpret_cast<unsigned*>(XQo)[i] = packed;
@@ -145,8 +146,8 @@ __device__ __forceinline__ void q8_lean_body(int N1, int nblk, int SW1, int nseg
   };
   auto stage_q8 = [&](int bi, const u32x4& a, const u32x4& c, float dxv) {
     const int b = slot(bi);
-    xl[b] = a;
-    xh[b] = c;
+    x2[2 * b] = a;
+    x2[2 * b + 1] = c;
     dxs[b] = dxv;
   };
   if (stg) {
@@ -175,7 +176,7 @@ __device__ __forceinline__ void q8_lean_body(int N1, int nblk, int SW1, int nseg
   asm volatile("" ::: "memory");
 
   // ---- stream the weights ----
-  const u32x4* xq = (q == 0 ? xl : xh) + gblk;  // the lane's staged half of its block
+  const u32x4* xq = x2 + 2 * gblk + q;  // the lane's staged half of its block
   const float* dl = dxs + gblk;
   float acc[MC];
   int p = 0, st = 0;  // the tile being dotted: pass p, K step st
@@ -197,7 +198,7 @@ __device__ __forceinline__ void q8_lean_body(int N1, int nblk, int SW1, int nseg
 #pragma unroll
       for (int m = 0; m < MC; ++m) {
         const int bo = m * nblk_pad + tb + u * BPG;  // the slot's first block (the lane's is bo + gblk)
-        const int s = group_sum(gemv_impl::q8_0_chunk_dot<MODE_DP4A>(w[u], xq[bo]), 2);
+        const int s = group_sum(gemv_impl::q8_0_chunk_dot<MODE_DP4A>(w[u], xq[2 * bo]), 2);
         if (__builtin_expect(S != nullptr, 0)) {
           if (q == 0 && rv && b < nblk) S[(static_cast<int64_t>(m) * N + row) * nblk + b] = s;
         }
