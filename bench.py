@@ -24,11 +24,11 @@ the workload list in the modes (dp4a, bytes) and knob sets it names, one compact
 streaming-read floor / GEMV).
 
 Written to --detail-out (default gpurun_out/bench_detail.json): the same line plus detail = per-shape GEMV us/call and
-GB/s for the Q4_0 / TQ2_0 shape list and Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs);
-configs in full; multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one gemv_multi launch
+GB/s for the Q4_0 / TQ2_0 shape list and Llama-3-8B shapes of Q8_0, IQ4_NL and Q4_K (cold, library-chosen knobs; and
+hot: one weight copy, resident in the 256 MB MALL where it fits); configs in full; multi_matrix = projections stored apart (BitNet-2B gate/up, Llama-3-8B Q/K/V) in one gemv_multi launch
 against one launch per matrix; batched_gemm = 4, 16 and 64 decode tokens at once on Llama-3-8B (Q4_0, and 14336 x
 4096 in Q8_0, IQ4_NL and Q4_K) and BitNet-2B (TQ2_0) projections, the matrix-core GEMM against GEMV launches of 3
-columns; ingest = ggml block bytes split into the planes on the device.
+columns; ingest = ggml block bytes split into the planes on the device; quantizers = quant_q8_0 / quant_q8_K alone.
 """
 
 from __future__ import annotations
@@ -505,7 +505,13 @@ def detail(torch, host, abi, args):
         d_us = disp[kind][0] * 1e3 / disp[kind][1]
         b = gemv_bytes(fmt, n, k, m)
         us = ms * 1e3 / reps
-        del copies, call
+
+        def call_hot(i, w=copies[0], xq=xq, xd=xd, y=y, fmt=fmt, n=n, k=k):  # one copy: resident in the 256 MB MALL
+            host.gemv_into(fmt, w[0], w[1], xq, xd, y, n, k, None, 0, 2, 0)
+
+        ms_hot, _ = timed_steps(torch, call_hot, 1, reps, per_graph)
+        us_hot = ms_hot * 1e3 / reps
+        del copies, call, call_hot
         torch.cuda.empty_cache()
         floor = read_floor_us(torch, host, b)
         if host.uses_gemm(fmt, m, n, k):  # block_n=None routes this many columns to the matrix-core GEMM
@@ -518,7 +524,37 @@ def detail(torch, host, abi, args):
                      "bytes": b, "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                      "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "dispatch_us": round(d_us, 3),
                      "gbs_dispatch": round(b / d_us / 1e3, 1), "read_floor_us": round(floor, 3),
-                     "of_read_floor": round(floor / us, 3), "copies": nc})  # fmt: skip
+                     "of_read_floor": round(floor / us, 3), "copies": nc, "us_per_call_hot": round(us_hot, 3),
+                     "gbs_hot": round(b / us_hot / 1e3, 1)})  # fmt: skip
+    return rows
+
+
+QUANT_SHAPES = (("q4_0", 4096), ("q4_0", 14336), ("tq2_0", 2560), ("tq2_0", 6912))  # (weight format, K)
+
+
+def quant_detail(torch, host, args):
+    """The activation quantizers alone (quant_q8_0 for Q4_0's activations, quant_q8_K for TQ2_0's, without bsums),
+    graph replays over 8 rotated inputs, 1 and 3 columns: us per call and GB/s of the f32 read plus the q8 planes
+    written (quant_bytes)."""
+    rows = []
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 5)
+    for fmt, k in QUANT_SHAPES:
+        ablk = BLOCKS[fmt][2]
+        for m in (1, 3):
+            xs = [torch.randn((m, k), generator=gen, device="cuda") for _ in range(8)]
+            xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+            xd = torch.empty((m, k // ablk), dtype=torch.float32, device="cuda")
+
+            def call(i, xs=xs, xq=xq, xd=xd, fmt=fmt):
+                host.quantize_into(fmt, xs[i % 8], xq, xd)
+
+            reps = 256
+            ms, _ = timed_steps(torch, call, 8, reps, 64)
+            us = ms * 1e3 / reps
+            b = quant_bytes(fmt, k, m)
+            rows.append({"quantizer": "quant_q8_0" if ablk == 32 else "quant_q8_K", "k": k, "m": m, "bytes": b,
+                         "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1)})  # fmt: skip
     return rows
 
 
@@ -829,7 +865,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-detail", action="store_true")
     ap.add_argument("--detail-out", default=os.path.join("gpurun_out", "bench_detail.json"), metavar="PATH",
-                    help="where the full per-shape tables (detail, configs, multi_matrix, batched_gemm, ingest) go "
+                    help="where the full per-shape tables (detail, configs, multi_matrix, batched_gemm, ingest, "
+                         "quantizers) go "
                          "(empty: not written); the result line carries a compact row per workload configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -891,7 +928,7 @@ def main():
     if not args.no_detail:
         full = {"detail": detail(torch, host, _abi, args), "configs": config_detail(torch, host, args),
                 "multi_matrix": multi_detail(torch, host, args), "batched_gemm": batched_detail(torch, host, args),
-                "ingest": ingest_detail(torch, host, args)}  # fmt: skip
+                "ingest": ingest_detail(torch, host, args), "quantizers": quant_detail(torch, host, args)}  # fmt: skip
         out["configs"] = config_summary(full["configs"])
         if args.detail_out:
             os.makedirs(os.path.dirname(os.path.abspath(args.detail_out)), exist_ok=True)
