@@ -62,6 +62,7 @@ SIGNATURES = {
     "komp_q4_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_tq2_0_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "komp_gemm_plan": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "komp_gemv_mfma_plan": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _I64, _P, _P]),
     "komp_q4_0_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "komp_tq2_0_split": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "komp_dp4a_probe": (_INT, [_P, _P, _P, _P, _I64, _INT, _P]),
@@ -136,6 +137,15 @@ def gemm_plan(fmt_id, m, n, k, sw):
     v = [ctypes.c_int(0) for _ in range(3)]
     st = lib().komp_gemm_plan(fmt_id, m, n, k, sw, *(ctypes.byref(x) for x in v))
     return tuple(x.value for x in v) if st == 0 else None
+
+
+def gemv_mfma_plan(fmt_id, fused, mode, m, n, k, sw):
+    """(rows per workgroup, waves) of the matrix-core GEMV when the library plan runs it for this call, else None."""
+    v = [ctypes.c_int(0) for _ in range(2)]
+    st = lib().komp_gemv_mfma_plan(fmt_id, int(fused), mode, m, n, k, sw, *(ctypes.byref(x) for x in v))
+    if st < 0:
+        raise KompArgumentError(last_error())
+    return tuple(x.value for x in v) if st == 1 else None
 
 
 def timing_begin(max_dispatches=1 << 16):

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkomp_hip.so")
 SOURCES = ("abi.hip", "quant.hip", "gemv.hip", "gemv_fused.hip", "gemv_more.hip", "gemv_more_fused.hip",
-           "gemv_q4_k.hip", "gemv_q4_k_fused.hip", "gemv_tq2.hip", "gemv_tq2_bytes.hip", "gemv_tq2_stamp.hip", "gemv_q4.hip",
+           "gemv_q4_k.hip", "gemv_q4_k_fused.hip", "gemv_tq2.hip", "gemv_tq2_bytes.hip", "gemv_tq2_stamp.hip", "gemv_tq2_mfma.hip", "gemv_q4.hip",
            "gemv_q4_bytes.hip", "gemv_q4k.hip", "gemv_q4k_fused.hip", "gemv_q8.hip", "gemv_q8_fused.hip", "gemm.hip", "split.hip")
 ARCH = "gfx950"
 

@@ -353,6 +353,27 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
   return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;
 }
 
+// The matrix-core GEMV (gemv_tq2_mfma.hip) for kMfmaM TQ2_0 columns with q8_K in, block_n == 0 in dp4a mode.
+// Measured on MI355X against the lean kernel's plans (graph replays, cold weights), three columns: BitNet-2B 6912 x
+// 2560 3.95 -> 3.84 us, 2560 x 6912 4.6 -> 4.4, 6913 x 2816 4.5 -> 3.9, 32768 x 8192 23.3 -> 18.4.  Two columns
+// stay on the lean kernel (as fast or faster at every shape measured).  Plans: one block a wave (up to 16 waves a
+// workgroup) for rows of up to 16 blocks, else about two; from 4 row tiles a CU, two tiles a workgroup (each
+// activation load serves both) and four blocks a wave.  False when the shape is past it (rows of more than 64 blocks,
+// or past its 32-bit descriptor ranges).
+constexpr int64_t kMfmaM = 3;
+bool tq2_mfma_plan(int64_t m, int64_t n, int64_t k, int64_t sw, MfmaPlan* p) {
+  if (m != kMfmaM || k <= 0 || k % 256 || n < 1) return false;
+  const int64_t nblk = k / 256;
+  const int64_t tiles = (n + 15) / 16;
+  const bool big = tiles >= 4 * device_cus();
+  int64_t waves = big ? (nblk + 3) / 4 : (nblk <= 16 ? nblk : (nblk + 1) / 2);
+  waves = waves > 16 ? 16 : waves;
+  const int64_t nbw = (nblk + waves - 1) / waves;
+  if (nbw > 4 || 16 * sw > 0x7FFFFFF0 || 4 * k > 0x7FFFFFF0) return false;
+  *p = MfmaPlan{big ? 2 : 1, static_cast<int>(waves), static_cast<int>(nbw)};
+  return true;
+}
+
 enum Route { kRouteAuto = 0, kRouteGemm = 1 };
 
 struct GemvMat {
@@ -462,6 +483,25 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     if (route == kRouteGemm)
       return fail(KOMP_EINVAL, "%s: K=%lld / SW past the GEMM's limits (64*K and 32*SW below 2^31, scale slab in LDS)",
                   name, (long long)K);
+  }
+  MfmaPlan mp;
+  if (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && count == 1 &&
+      tq2_mfma_plan(M, mats[0].n, K, mats[0].sw, &mp)) {
+    GemvCall c = {};
+    c.fmt = fmt;
+    c.wq = mats[0].wq;
+    c.ws = mats[0].ws;
+    c.xq = a.xq;
+    c.xd = a.xd;
+    c.y = mats[0].y;
+    c.s = mats[0].s;
+    c.m = static_cast<int>(M);
+    c.n = static_cast<int>(mats[0].n);
+    c.k = static_cast<int>(K);
+    c.sw = mats[0].sw;
+    c.mode = mode;
+    c.nseg = 1;
+    if (tq2_mfma_eligible(c, mp)) return hip_status(launch_gemv_tq2_mfma(c, mp, static_cast<hipStream_t>(stream)), name);
   }
   int mc = static_cast<int>(M < 3 ? M : 3);
   while (mc > 1 && gemv_lds_bytes(fmt, mc, static_cast<int>(K)) > kLdsMax) --mc;
@@ -674,6 +714,17 @@ int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* ro
   if (cols_per_wg != nullptr) *cols_per_wg = 16 * p.cn;
   if (waves != nullptr) *waves = p.wk * p.wr;
   return KOMP_OK;
+}
+
+int komp_gemv_mfma_plan(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg,
+                        int* waves) {
+  if (fmt < FMT_Q4_0 || fmt > FMT_Q4_K) return fail(KOMP_EINVAL, "komp_gemv_mfma_plan: fmt=%d", fmt);
+  if (M < 0 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemv_mfma_plan: bad argument");
+  MfmaPlan p;
+  const bool on = !fused && mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && tq2_mfma_plan(M, N, K, SW, &p);
+  if (rows_per_wg != nullptr) *rows_per_wg = on ? 16 * p.tiles : 0;
+  if (waves != nullptr) *waves = on ? p.waves : 0;
+  return on ? 1 : 0;
 }
 
 int komp_q4_0_gemv_multi(int count, const uint8_t* const* WQ, const int16_t* const* WS, float* const* Y,

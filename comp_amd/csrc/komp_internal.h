@@ -197,6 +197,16 @@ size_t q8_lean_lds_bytes(int lpr, int nb, int mc, int k);
 hipError_t launch_gemv_q8_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q8_lean_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 
+// TQ2_0, 2-4 columns in dp4a mode, q8_K in, on the matrix cores (gemv_tq2_mfma.hip): workgroups of `tiles` 16-row
+// tiles whose `waves` waves split K into ranges of at most `nbw` blocks
+struct MfmaPlan {
+  int tiles;
+  int waves;
+  int nbw;
+};
+bool tq2_mfma_eligible(const GemvCall& c, const MfmaPlan& p);
+hipError_t launch_gemv_tq2_mfma(const GemvCall& c, const MfmaPlan& p, hipStream_t stream);
+
 bool q4k_lean_eligible(const GemvCall& c, const GemvPlan& p);
 size_t q4k_lean_lds_bytes(int lpr, int nb, int mc, int k);
 hipError_t launch_gemv_q4k_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);

@@ -303,6 +303,14 @@ def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
     return not fused and mode == 2 and m >= GEMM_MIN_M[fmt] and gemm_plan(fmt, m, n, k, sw) is not None
 
 
+def uses_mfma(fmt, m, n, k, fused=False, mode=2, sw=None):
+    """True when gemv(..., block_n=None) runs the matrix-core GEMV for this call (TQ2_0, q8_K in, dp4a, three
+    columns): S as the GEMV kernels', Y to f32 rounding (another order of the f32 sums)."""
+    if sw is None:
+        sw = k // FORMATS[fmt]["block"] * FORMATS[fmt]["qbytes"]
+    return _abi.gemv_mfma_plan(FMT_ID[fmt], fused, mode, m, n, k, sw) is not None
+
+
 def quantize_into(fmt, x, xq, xd, xb=None, bb=4):
     """Allocation-free quantize: writes the q8 planes into preallocated xq / xd (and the q8_K bsums into xb).
 

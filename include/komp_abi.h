@@ -64,7 +64,9 @@ int komp_q4_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const
                    int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
                    void* stream);
 
-/* The same for TQ2_0 weights x q8_K activations.  K % 256 == 0; SW % 16 == 0 and SW >= K/4.
+/* The same for TQ2_0 weights x q8_K activations.  K % 256 == 0; SW % 16 == 0 and SW >= K/4.  With block_n == 0 in
+ * KOMP_MODE_DP4A, three columns run on the matrix cores when komp_gemv_mfma_plan says so (S the same, Y to f32
+ * rounding).
  * Replaces: host.gemv (src/komp/host.py:76-85) launching kernels.tq2_0_gemv (src/komp/kernels.py:97-142). */
 int komp_tq2_0_gemv(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, const float* XD, float* Y, int32_t* S,
                     int64_t M, int64_t N, int64_t K, int64_t SW, int block_n, int nb, int mode, int num_warps,
@@ -189,6 +191,16 @@ int komp_tq2_0_gemm(const uint8_t* WQ, const int16_t* WS, const int8_t* XQ, cons
  * No reference counterpart. */
 int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg, int* cols_per_wg,
                    int* waves);
+
+/* Whether komp_tq2_0_gemv with block_n == 0 runs the matrix-core GEMV for this call (fused 0 / 1, mode as the GEMVs):
+ * TQ2_0 with q8_K activations in, KOMP_MODE_DP4A, 3 columns, rows of at most 64 blocks.  Returns 1 and its
+ * workgroup's rows and waves when it does, 0 (and zeros) when the call runs on the GEMV kernels, KOMP_EINVAL on a bad
+ * argument.  That kernel computes S bit-identical to the GEMVs' and Y to f32 rounding (its f32 sums run in another
+ * order): the activations are the A operand of v_mfma_i32_16x16x64_i8 and 16 weight rows its B operand, so the VALU
+ * work per weight does not grow with the columns.
+ * No reference counterpart: the reference runs one program per column (src/komp/kernels.py:50). */
+int komp_gemv_mfma_plan(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int64_t SW, int* rows_per_wg,
+                        int* waves);
 
 /* ggml block bytes -> KURN's split planes on the device.  W: N rows of K/32 Q4_0 blocks (18 bytes: f16 d, 16 quant
  * bytes) or K/256 TQ2_0 blocks (66 bytes: 64 quant bytes, f16 d), contiguous, 4-byte aligned.  Writes WQ u8 [N][SW]

@@ -39,9 +39,10 @@ def test_fused_equals_two_launches(fmt, n, k, m, mode, extreme, knobs):
     assert torch.equal(s1, s2)
     # with block_n=None each launch plans for itself: Y is bit-identical when both planned alike (the f32 sums then
     # run in the same order), and within the oracle tolerance below otherwise
-    # (from host.GEMM_MIN_M columns on, the unfused dp4a launch with block_n=None runs the matrix-core GEMM instead)
+    # (from host.GEMM_MIN_M columns on, the unfused dp4a launch with block_n=None runs the matrix-core GEMM instead,
+    # and three TQ2_0 columns the matrix-core GEMV)
     if knobs or (host.auto_plan(fmt, m, n, k, True, mode) == host.auto_plan(fmt, m, n, k, False, mode)
-                 and not host.uses_gemm(fmt, m, n, k, False, mode)):
+                 and not host.uses_gemm(fmt, m, n, k, False, mode) and not host.uses_mfma(fmt, m, n, k, False, mode)):
         assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
     for a, b in zip(q, qq):
         assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int16 else a, b.view(torch.uint8) if b.dtype != torch.int16 else b)

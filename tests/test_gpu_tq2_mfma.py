@@ -1,0 +1,90 @@
+"""The TQ2_0 matrix-core GEMV (gemv_tq2_mfma.hip: three columns, q8_K in, dp4a mode, block_n=None) through the C ABI: S exact and Y within the output gate against the oracle, S bit for bit the lean dp4a
+kernel's (explicit knobs), at the BitNet-2B shapes, ragged row counts, rows of 1-56 blocks (one wave a workgroup up to
+16 waves of 1-4 blocks), one and two row tiles a workgroup, and the extreme data (crumb 3 against +-127
+activations)."""
+
+import numpy as np
+import pytest
+import torch
+
+from comp_amd import _abi, host
+from oracle import oracle as O
+from tests.checks import outputs_ok
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    (6912, 2560, 3),   # BitNet-2B W1: 432 workgroups of 10 waves, one block a wave
+    (2560, 6912, 3),   # BitNet-2B W2: 14 waves of 2 blocks, the last one 1
+    (300, 2560, 3),    # a partial last tile (12 of 16 rows)
+    (77, 14336, 3),    # 56 blocks: 16 waves of 3-4 blocks
+    (16, 256, 3),      # one block: one wave, no partial sums to add
+    (33, 512, 3),      # two blocks, two waves; 3 tiles, the last of 1 row
+    (1000, 4096, 3),   # 16 blocks, 16 waves
+    (16389, 512, 3),   # 1025 row tiles: two tiles a workgroup (the last one past the matrix), one wave of 2 blocks
+    (16400, 2304, 3),  # two tiles a workgroup, 5 waves of 1-2 blocks
+    (16390, 4096, 3),  # two tiles a workgroup, 8 waves of 2 blocks
+]
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("extreme", [False, True])
+def test_mfma_gemv_matches_oracle_and_lean_kernel(case, extreme):
+    n, k, m = CASES[case]
+    print(f"tq2 mfma n={n} k={k} m={m} extreme={extreme}", flush=True)
+    assert host.uses_mfma("tq2_0", m, n, k)
+    W, x = O.problem("tq2_0", n, k, m, 90 + case, extreme)
+    wq, ws = host.split("tq2_0", W, n, k)
+    wq_d, ws_d = dev(wq), dev(ws)
+    xq, xd = host.quantize("tq2_0", dev(x))
+    y, s = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    y_plain, _ = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0)
+    y_lean, s_lean = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, 64, 1, 2, 4, store_s=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_lean)
+    assert torch.equal(y.view(torch.int32), y_plain.view(torch.int32))  # S stores do not change Y
+    rq, rd, _ = O.quantize("tq2_0", x)
+    r, rs = O.gemv("tq2_0", wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
+    assert outputs_ok("tq2_0", y.cpu().numpy(), ws, rd, rs, r)
+    assert outputs_ok("tq2_0", y_lean.cpu().numpy(), ws, rd, rs, r)
+
+
+def test_mfma_gemv_routing():
+    # three unfused dp4a columns with block_n=None; one and two columns, fused launches, the other modes and explicit
+    # knobs keep the GEMV kernels, 4+ columns the GEMM
+    assert host.uses_mfma("tq2_0", 3, 6912, 2560) and host.uses_mfma("tq2_0", 3, 32768, 8192)
+    assert not host.uses_mfma("tq2_0", 2, 32768, 8192) and not host.uses_mfma("tq2_0", 2, 6912, 2560)
+    assert not host.uses_mfma("tq2_0", 1, 32768, 8192) and not host.uses_mfma("tq2_0", 4, 6912, 2560)
+    assert not host.uses_mfma("tq2_0", 3, 6912, 2560, fused=True)
+    assert not host.uses_mfma("tq2_0", 3, 6912, 2560, mode=0) and not host.uses_mfma("q4_0", 3, 4096, 4096)
+    assert not host.uses_mfma("tq2_0", 3, 4096, 65536)  # rows of 256 blocks: past its 4 blocks a wave
+
+
+def test_mfma_gemv_stamped_instantiation():
+    # with the tuning harness's stamps on, the launch runs the stamped instantiation: the same Y and S, and one record
+    # per wave whose phases are in order
+    n, k, m = 6912, 2560, 3
+    W, x = O.problem("tq2_0", n, k, m, 99)
+    wq, ws = host.split("tq2_0", W, n, k)
+    wq_d, ws_d = dev(wq), dev(ws)
+    xq, xd = host.quantize("tq2_0", dev(x))
+    y0, s0 = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    buf = torch.zeros(1 << 20, dtype=torch.int32, device="cuda")
+    _abi.stamps_begin(buf)
+    try:
+        y1, s1 = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    finally:
+        used, khz = _abi.stamps_end()
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(s0, s1)
+    rows, waves = _abi.gemv_mfma_plan(1, False, 2, m, n, k, k // 4)
+    recs = _abi.parse_stamps(buf[:used].cpu().numpy().view(np.uint32), khz)
+    assert len(recs) == 1 and recs[0]["n"] == n and recs[0]["k"] == k
+    assert recs[0]["waves"] == (n + rows - 1) // rows * waves
+    r = recs[0]
+    assert (r["entry"] <= r["staged"]).all() and (r["staged"] <= r["dots"]).all() and (r["dots"] <= r["stored"]).all()
