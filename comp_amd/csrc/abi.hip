@@ -353,19 +353,23 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
   return gemm_lds_bytes(fmt, q, static_cast<int>(k)) <= kLdsMax;
 }
 
-// The matrix-core GEMV (gemv_tq2_mfma.hip) for kMfmaM TQ2_0 columns with q8_K in, block_n == 0 in dp4a mode.
-// Measured on MI355X against the lean kernel's plans (graph replays, cold weights), three columns: BitNet-2B 6912 x
-// 2560 3.95 -> 3.84 us, 2560 x 6912 4.6 -> 4.4, 6913 x 2816 4.5 -> 3.9, 32768 x 8192 23.3 -> 18.4.  Two columns
-// stay on the lean kernel (as fast or faster at every shape measured).  Plans: one block a wave (up to 16 waves a
+// The matrix-core GEMV (gemv_tq2_mfma.hip) for kMfmaM TQ2_0 columns, block_n == 0 in dp4a mode.  Measured on MI355X
+// against the lean kernel's plans (graph replays, cold weights), three columns with q8_K in: BitNet-2B 6912 x 2560
+// 3.95 -> 3.84 us, 2560 x 6912 4.6 -> 4.4, 6913 x 2816 4.5 -> 3.9, 32768 x 8192 23.3 -> 18.4; f32 in (each wave
+// quantizing its own blocks): 32768 x 8192 32.4 -> 24.0, but 1.1-1.3 us slower at the BitNet-2B shapes, where every
+// workgroup reading all 3 x K f32 inputs costs more than the dots save (there the lean kernel's fewer, fuller
+// workgroups stay), so fused launches take it from 4 row tiles a CU on.  Two columns stay on the lean kernel (as fast
+// or faster at every shape measured).  Plans: one block a wave (up to 16 waves a
 // workgroup) for rows of up to 16 blocks, else about two; from 4 row tiles a CU, two tiles a workgroup (each
 // activation load serves both) and four blocks a wave.  False when the shape is past it (rows of more than 64 blocks,
 // or past its 32-bit descriptor ranges).
 constexpr int64_t kMfmaM = 3;
-bool tq2_mfma_plan(int64_t m, int64_t n, int64_t k, int64_t sw, MfmaPlan* p) {
+bool tq2_mfma_plan(int64_t m, int64_t n, int64_t k, int64_t sw, bool fused, MfmaPlan* p) {
   if (m != kMfmaM || k <= 0 || k % 256 || n < 1) return false;
   const int64_t nblk = k / 256;
   const int64_t tiles = (n + 15) / 16;
   const bool big = tiles >= 4 * device_cus();
+  if (fused && !big) return false;
   int64_t waves = big ? (nblk + 3) / 4 : (nblk <= 16 ? nblk : (nblk + 1) / 2);
   waves = waves > 16 ? 16 : waves;
   const int64_t nbw = (nblk + waves - 1) / waves;
@@ -485,14 +489,18 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
                   name, (long long)K);
   }
   MfmaPlan mp;
-  if (!fused && block_n == 0 && mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && count == 1 &&
-      tq2_mfma_plan(M, mats[0].n, K, mats[0].sw, &mp)) {
+  if (block_n == 0 && mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && count == 1 &&
+      tq2_mfma_plan(M, mats[0].n, K, mats[0].sw, fused, &mp)) {
     GemvCall c = {};
     c.fmt = fmt;
     c.wq = mats[0].wq;
     c.ws = mats[0].ws;
-    c.xq = a.xq;
-    c.xd = a.xd;
+    c.xq = fused ? nullptr : a.xq;
+    c.xd = fused ? nullptr : a.xd;
+    c.x = fused ? a.x : nullptr;
+    c.xq_out = a.xq_out;
+    c.xd_out = a.xd_out;
+    c.xb_out = a.xb_out;
     c.y = mats[0].y;
     c.s = mats[0].s;
     c.m = static_cast<int>(M);
@@ -721,7 +729,7 @@ int komp_gemv_mfma_plan(int fmt, int fused, int mode, int64_t M, int64_t N, int6
   if (fmt < FMT_Q4_0 || fmt > FMT_Q4_K) return fail(KOMP_EINVAL, "komp_gemv_mfma_plan: fmt=%d", fmt);
   if (M < 0 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemv_mfma_plan: bad argument");
   MfmaPlan p;
-  const bool on = !fused && mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && tq2_mfma_plan(M, N, K, SW, &p);
+  const bool on = mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && tq2_mfma_plan(M, N, K, SW, fused != 0, &p);
   if (rows_per_wg != nullptr) *rows_per_wg = on ? 16 * p.tiles : 0;
   if (waves != nullptr) *waves = on ? p.waves : 0;
   return on ? 1 : 0;

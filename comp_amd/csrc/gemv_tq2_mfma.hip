@@ -49,11 +49,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
 // counter on entry, once its loads have landed, after its blocks are scaled and once the workgroup's outputs are
 // stored, and lane 0 writes the four low words to stamps[4 + 4 * (blockIdx.x * waves + wave)] (header {kStampMagic,
 // waves of the grid, N, K} from thread 0 of workgroup 0), the lean kernels' record layout.
-template <int T, int NBW, int MC, bool STAMP>
+// FUSED: X f32 [MC][K] in instead of the q8_K planes; each wave quantizes the blocks of its own range (all columns)
+// with the quantizer's arithmetic (q8_K_row16: 16 lanes a block and column, four of them a pass) into a region of LDS
+// of its own and reads its A pieces back from there, so no wave waits for another before its dots; the blocks' q8
+// sums give the -1 offsets (no offset MFMAs).  Workgroup 0 also writes the q8_K planes when XQo is not NULL.
+template <int T, int NBW, int MC, bool FUSED, bool STAMP>
 __global__ void __launch_bounds__(64 * kMaxWaves)
-tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, int N,
+tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, int N,
                 int nblk, int SW, int K, const float* __restrict__ XD, float* __restrict__ Y,
-                int32_t* __restrict__ S, uint32_t* __restrict__ stamps) {
+                int32_t* __restrict__ S, uint32_t* __restrict__ stamps, int8_t* __restrict__ XQo,
+                float* __restrict__ XDo, int16_t* __restrict__ XBo) {
   extern __shared__ __align__(16) unsigned char lds[];
   uint64_t t_entry = 0, t_in = 0, t_dots = 0;
   if constexpr (STAMP) {
@@ -73,22 +78,40 @@ tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, c
   // (g/2)*128 + 32j + 16(g%2); one load a slot reads all of them, lane (4j + c, g) taking piece (c, j).  The A operand
   // of crumb j wants it in lane (c, g): a DPP row shift left by 4j (lanes of other A rows, columns past MC, and slots
   // past the wave's range read zeros or are never used) ----
-  const auto xr = rsrc(XQ, static_cast<unsigned>(MC * K));
-  const int xc = r16 & 3, xj = r16 >> 2;
-  const unsigned vx = xc < MC ? static_cast<unsigned>(xc * K + (g >> 1) * 128 + (g & 1) * 16 + 32 * xj) : kOob;
+  // Fused: pass pp's 16-lane row q (pair P = 4 pp + q = slot i * MC + column c) loads the 16 f32 values 16 r16.. of
+  // that block and column
+  constexpr int NP = NBW * MC;         // (slot, column) pairs of the wave
+  constexpr int NPASS = (NP + 3) / 4;  // quantizer passes, four pairs each
   u32x4 xl[NBW];
-#pragma unroll
-  for (int i = 0; i < NBW; ++i)
-    xl[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, i < nbw ? vx : kOob, static_cast<unsigned>((b0 + i) * 256), 0);
-  // d_x of each column and slot: wave-uniform, through the scalar cache
+  f32x4 xv[FUSED ? NPASS : 1][4];
   float dx[NBW][MC];
+  if constexpr (FUSED) {
+    const auto fr = rsrc(XA, static_cast<unsigned>(MC * K * 4));
 #pragma unroll
-  for (int i = 0; i < NBW; ++i)
+    for (int pp = 0; pp < NPASS; ++pp) {
+      const int pr = 4 * pp + g;  // this lane's pair
+      const int i = pr / MC, c = pr - i * MC;
+      const unsigned vf = pr < NP && i < nbw ? static_cast<unsigned>((c * K + (b0 + i) * 256 + 16 * r16) * 4) : kOob;
 #pragma unroll
-    for (int k = 0; k < MC; ++k) {  // a slot past the range reads the row's last d_x and scales by zero (no branch)
-      const float v = XD[k * nblk + min(b0 + i, nblk - 1)];
-      dx[i][k] = i < nbw ? v : 0.0f;
+      for (int q = 0; q < 4; ++q)
+        xv[pp][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(fr, vf + 16 * q, 0, 0));
     }
+  } else {
+    const auto xr = rsrc(XA, static_cast<unsigned>(MC * K));
+    const int xc = r16 & 3, xj = r16 >> 2;
+    const unsigned vx = xc < MC ? static_cast<unsigned>(xc * K + (g >> 1) * 128 + (g & 1) * 16 + 32 * xj) : kOob;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+      xl[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, i < nbw ? vx : kOob, static_cast<unsigned>((b0 + i) * 256), 0);
+    // d_x of each column and slot: wave-uniform, through the scalar cache
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+#pragma unroll
+      for (int k = 0; k < MC; ++k) {  // a slot past the range reads the row's last d_x and scales by zero (no branch)
+        const float v = XD[k * nblk + min(b0 + i, nblk - 1)];
+        dx[i][k] = i < nbw ? v : 0.0f;
+      }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the weights and scales of the T tiles: lane (r16, g) reads bytes 16g.. of each block of row r16, and the
@@ -148,22 +171,65 @@ tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, c
   // independent chains of four (the offset of each slot, and the crumbs of each slot and tile from zero), interleaved
   // across slots and tiles, so consecutive MFMAs rarely wait for each other's results.
   i32x4 xa[NBW][4];
+  int msum[FUSED ? NBW : 1][MC];  // fused: -(the block's q8 sum) of each slot and column
+  if constexpr (FUSED) {
+    // quantize the wave's pairs into its LDS region (256 bytes a pair, in value order), then read the A pieces back
+    unsigned char* const xs = lds + wave * (NP * 256);
 #pragma unroll
-  for (int i = 0; i < NBW; ++i)
+    for (int pp = 0; pp < NPASS; ++pp) {
+      const int pr = 4 * pp + g;
+      const int i = pr / MC, c = pr - i * MC;
+      u32x4 qv;
+      float d;
+      int qsum;
+      const int bsum = q8_K_row16(xv[pp], r16, qv, d, qsum);
+      if (pr < NP) *reinterpret_cast<u32x4*>(xs + pr * 256 + 16 * r16) = qv;
+      if (__builtin_expect(blockIdx.x == 0 && XQo != nullptr, 0)) {  // workgroup 0 writes the q8_K planes out
+        if (pr < NP && i < nbw) {
+          const int b = b0 + i;
+          *reinterpret_cast<u32x4*>(XQo + c * K + b * 256 + 16 * r16) = qv;
+          if (r16 == 0) XDo[c * nblk + b] = d;
+          if (XBo != nullptr) XBo[c * (K / 16) + b * 16 + r16] = static_cast<int16_t>(bsum);
+        }
+      }
+      // pair 4 pp + q's d and sum sit in every lane of row q
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xa[i][0][e] = static_cast<int>(xl[i][e]);
-      xa[i][1][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x104, 0xF, 0xF, false);  // row_shl:4
-      xa[i][2][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x108, 0xF, 0xF, false);  // row_shl:8
-      xa[i][3][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x10C, 0xF, 0xF, false);  // row_shl:12
+      for (int q = 0; q < 4; ++q) {
+        const int pq = 4 * pp + q;
+        if (pq < NP) {
+          dx[pq / MC][pq % MC] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d), 16 * q));
+          msum[pq / MC][pq % MC] = -__builtin_amdgcn_readlane(qsum, 16 * q);
+        }
+      }
     }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+    asm volatile("" ::: "memory");
+    const int xc = r16 < MC ? r16 : MC - 1;  // the lanes of A rows past MC read a real column (their C is unused)
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xa[i][j] = *reinterpret_cast<const i32x4*>(xs + (i * MC + xc) * 256 + (g >> 1) * 128 + 32 * j + (g & 1) * 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xa[i][0][e] = static_cast<int>(xl[i][e]);
+        xa[i][1][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x104, 0xF, 0xF, false);  // row_shl:4
+        xa[i][2][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x108, 0xF, 0xF, false);  // row_shl:8
+        xa[i][3][e] = __builtin_amdgcn_update_dpp(0, static_cast<int>(xl[i][e]), 0x10C, 0xF, 0xF, false);  // row_shl:12
+      }
+  }
   i32x4 corr[NBW], cc[T][NBW];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
     for (int i = 0; i < NBW; ++i)
-      corr[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i][j], i32x4{-1, -1, -1, -1}, j ? corr[i] : i32x4{0, 0, 0, 0},
-                                                      0, 0, 0);
+      if constexpr (!FUSED)
+        corr[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i][j], i32x4{-1, -1, -1, -1},
+                                                        j ? corr[i] : i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -178,7 +244,13 @@ tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, c
     const int row = row0 + 16 * t + r16;
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-      const i32x4 sb = cc[t][i] + corr[i];  // the exact block dots (|s| < 2^17)
+      i32x4 sb;  // the exact block dots (|s| < 2^17)
+      if constexpr (FUSED) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sb[k] = cc[t][i][k] + (k < MC ? msum[i][k] : 0);
+      } else {
+        sb = cc[t][i] + corr[i];
+      }
       if (__builtin_expect(S != nullptr, 0)) {
         if (g == 0 && row < N && i < nbw) {
 #pragma unroll
@@ -226,7 +298,7 @@ tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, c
     stamp_out();
     return;
   }
-  float* red = reinterpret_cast<float*>(lds);  // [wave][t][k][16]
+  float* red = reinterpret_cast<float*>(lds + (FUSED ? ks * NP * 256 : 0));  // [wave][t][k][16], past the staging
   if (g == 0) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
@@ -246,28 +318,32 @@ tq2_mfma_kernel(const int8_t* __restrict__ XQ, const uint8_t* __restrict__ WQ, c
   stamp_out();
 }
 
-template <int T, int NBW, int MC>
+template <int T, int NBW, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const MfmaPlan& p, hipStream_t stream) {
   const int nblk = c.k / 256;
   const unsigned groups = static_cast<unsigned>((c.n + 16 * T - 1) / (16 * T));
   // the tuning harness's wave stamps, while there is room for them
   uint32_t* const slot = stamps_on() ? stamp_slot(4 + 4 * int64_t{groups} * p.waves) : nullptr;
-  const auto kern = slot != nullptr ? tq2_mfma_kernel<T, NBW, MC, true> : tq2_mfma_kernel<T, NBW, MC, false>;
-  const size_t lds = p.waves > 1 ? static_cast<size_t>(p.waves) * T * MC * 16 * sizeof(float) : 0;
+  const auto kern =
+      slot != nullptr ? tq2_mfma_kernel<T, NBW, MC, FUSED, true> : tq2_mfma_kernel<T, NBW, MC, FUSED, false>;
+  const size_t lds = tq2_mfma_lds_bytes(T, NBW, MC, FUSED, p.waves);
   const dim3 grid(groups), block(static_cast<unsigned>(64 * p.waves));
   const int sw = static_cast<int>(c.sw);
+  const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
   const Timing tm = timing_slot(KIND_TQ2_0_GEMV);
   if (tm.on)
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, c.xq, c.wq, c.ws, c.n, nblk, sw, c.k,
-                          c.xd, c.y, c.s, slot);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, xa, c.wq, c.ws, c.n, nblk, sw, c.k,
+                          c.xd, c.y, c.s, slot, c.xq_out, c.xd_out, c.xb_out);
   else
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, c.xq, c.wq, c.ws, c.n, nblk, sw, c.k, c.xd, c.y, c.s, slot);
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, xa, c.wq, c.ws, c.n, nblk, sw, c.k, c.xd, c.y, c.s, slot,
+                       c.xq_out, c.xd_out, c.xb_out);
   return hipGetLastError();
 }
 
 template <int T, int NBW>
 hipError_t by_mc(const GemvCall& c, const MfmaPlan& p, hipStream_t s) {
-  return c.m == 3 ? launch_k<T, NBW, 3>(c, p, s) : hipErrorInvalidValue;  // the column count the library routes here
+  if (c.m != 3) return hipErrorInvalidValue;  // the column count the library routes here
+  return c.x != nullptr ? launch_k<T, NBW, 3, true>(c, p, s) : launch_k<T, NBW, 3, false>(c, p, s);
 }
 
 template <int T>
@@ -283,8 +359,14 @@ hipError_t by_nbw(const GemvCall& c, const MfmaPlan& p, hipStream_t s) {
 
 }  // namespace gemv_tq2_mfma
 
+size_t tq2_mfma_lds_bytes(int tiles, int nbw, int mc, bool fused, int waves) {
+  const size_t stage = fused ? static_cast<size_t>(waves) * nbw * mc * 256 : 0;  // each wave's quantized blocks
+  return stage + (waves > 1 ? static_cast<size_t>(waves) * tiles * mc * 16 * sizeof(float) : 0);
+}
+
 bool tq2_mfma_eligible(const GemvCall& c, const MfmaPlan& p) {
-  if (c.fmt != FMT_TQ2_0 || c.mode != MODE_DP4A || c.x != nullptr || c.nseg > 1 || c.m != 3) return false;
+  if (c.fmt != FMT_TQ2_0 || c.mode != MODE_DP4A || c.nseg > 1 || c.m != 3) return false;
+  if (c.x == nullptr && (c.xq == nullptr || c.xd == nullptr)) return false;
   if (c.k % 256 != 0 || c.k <= 0 || c.n <= 0) return false;
   if (p.tiles < 1 || p.tiles > 2 || p.waves < 1 || p.waves > gemv_tq2_mfma::kMaxWaves || p.nbw < 1 || p.nbw > 4)
     return false;

@@ -204,6 +204,7 @@ struct MfmaPlan {
   int waves;
   int nbw;
 };
+size_t tq2_mfma_lds_bytes(int tiles, int nbw, int mc, bool fused, int waves);
 bool tq2_mfma_eligible(const GemvCall& c, const MfmaPlan& p);
 hipError_t launch_gemv_tq2_mfma(const GemvCall& c, const MfmaPlan& p, hipStream_t stream);
 

@@ -1,4 +1,4 @@
-"""The TQ2_0 matrix-core GEMV (gemv_tq2_mfma.hip: three columns, q8_K in, dp4a mode, block_n=None) through the C ABI: S exact and Y within the output gate against the oracle, S bit for bit the lean dp4a
+"""The TQ2_0 matrix-core GEMV (gemv_tq2_mfma.hip: three columns, q8_K or f32 in, dp4a mode, block_n=None) through the C ABI: S exact and Y within the output gate against the oracle, S bit for bit the lean dp4a
 kernel's (explicit knobs), at the BitNet-2B shapes, ragged row counts, rows of 1-56 blocks (one wave a workgroup up to
 16 waves of 1-4 blocks), one and two row tiles a workgroup, and the extreme data (crumb 3 against +-127
 activations)."""
@@ -44,9 +44,16 @@ def test_mfma_gemv_matches_oracle_and_lean_kernel(case, extreme):
     y, s = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
     y_plain, _ = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0)
     y_lean, s_lean = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, 64, 1, 2, 4, store_s=True)
+    # fused (f32 in; from 4 row tiles a CU on): the same plan, each wave quantizing its own blocks; S and Y bit for bit
+    # the unfused launch's
+    fused = host.uses_mfma("tq2_0", m, n, k, fused=True)
+    assert fused == (n >= 16384)
+    y_f, s_f = host.gemv_f32("tq2_0", wq_d, ws_d, dev(x), n, k, None, 0, 2, 0, store_s=True)
     torch.cuda.synchronize()
-    assert torch.equal(s, s_lean)
+    assert torch.equal(s, s_lean) and torch.equal(s_f, s)
     assert torch.equal(y.view(torch.int32), y_plain.view(torch.int32))  # S stores do not change Y
+    if fused:
+        assert torch.equal(y_f.view(torch.int32), y.view(torch.int32))
     rq, rd, _ = O.quantize("tq2_0", x)
     r, rs = O.gemv("tq2_0", wq, ws, rq, rd, n, k)
     assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
@@ -55,12 +62,12 @@ def test_mfma_gemv_matches_oracle_and_lean_kernel(case, extreme):
 
 
 def test_mfma_gemv_routing():
-    # three unfused dp4a columns with block_n=None; one and two columns, fused launches, the other modes and explicit
-    # knobs keep the GEMV kernels, 4+ columns the GEMM
+    # three dp4a columns with block_n=None, q8 in (f32 in from 4 row tiles a CU on); one and two columns, the other
+    # modes and explicit knobs keep the GEMV kernels, 4+ columns the GEMM
     assert host.uses_mfma("tq2_0", 3, 6912, 2560) and host.uses_mfma("tq2_0", 3, 32768, 8192)
     assert not host.uses_mfma("tq2_0", 2, 32768, 8192) and not host.uses_mfma("tq2_0", 2, 6912, 2560)
     assert not host.uses_mfma("tq2_0", 1, 32768, 8192) and not host.uses_mfma("tq2_0", 4, 6912, 2560)
-    assert not host.uses_mfma("tq2_0", 3, 6912, 2560, fused=True)
+    assert host.uses_mfma("tq2_0", 3, 32768, 8192, fused=True) and not host.uses_mfma("tq2_0", 3, 6912, 2560, fused=True)
     assert not host.uses_mfma("tq2_0", 3, 6912, 2560, mode=0) and not host.uses_mfma("q4_0", 3, 4096, 4096)
     assert not host.uses_mfma("tq2_0", 3, 4096, 65536)  # rows of 256 blocks: past its 4 blocks a wave
 
@@ -88,3 +95,21 @@ def test_mfma_gemv_stamped_instantiation():
     assert recs[0]["waves"] == (n + rows - 1) // rows * waves
     r = recs[0]
     assert (r["entry"] <= r["staged"]).all() and (r["staged"] <= r["dots"]).all() and (r["dots"] <= r["stored"]).all()
+
+
+@pytest.mark.parametrize("extreme", [False, True])
+def test_mfma_gemv_fused_writes_the_quantizer_planes(extreme):
+    # return_q: workgroup 0's waves write the q8_K planes and bsums of their blocks, byte for byte the quantizer's
+    n, k, m = 16400, 2304, 3
+    W, x = O.problem("tq2_0", n, k, m, 98, extreme)
+    wq, ws = host.split("tq2_0", W, n, k)
+    assert host.uses_mfma("tq2_0", m, n, k, fused=True)
+    y, s, (xq, xd, xb) = host.gemv_f32("tq2_0", dev(wq), dev(ws), dev(x), n, k, store_s=True, return_q=True)
+    torch.cuda.synchronize()
+    rq, rd, rb = O.quantize("tq2_0", x)
+    assert np.array_equal(xq.cpu().numpy(), rq)
+    assert np.array_equal(xd.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(xb.cpu().numpy(), rb)
+    r, rs = O.gemv("tq2_0", wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
+    assert outputs_ok("tq2_0", y.cpu().numpy(), ws, rd, rs, r)
