@@ -517,6 +517,8 @@ def detail(torch, host, abi, args):
         if host.uses_gemm(fmt, m, n, k):  # block_n=None routes this many columns to the matrix-core GEMM
             path, gp = "gemm", host.gemm_plan(fmt, m, n, k)
             plan = [gp[key] for key in ("rows", "cols", "waves")]
+        elif host.uses_mfma(fmt, m, n, k):  # ... or (three TQ2_0 columns) the matrix-core GEMV: [rows, waves]
+            path, plan = "mfma_gemv", list(host.mfma_plan(fmt, m, n, k))
         else:
             path, ap = "gemv", host.auto_plan(fmt, m, n, k)
             plan = [ap[key] for key in ("block_n", "nb", "waves", "lanes_per_row", "passes")]
@@ -612,10 +614,12 @@ def config_detail(torch, host, args):
                     b = gemv_bytes(fmt, n, k, m)
                     us = ms_t * 1e3 / reps
                     gemm = knobs is None and host.uses_gemm(fmt, m, n, k, mode=mode)
+                    mfma = knobs is None and host.uses_mfma(fmt, m, n, k, mode=mode)
                     rows.append({"config": cfg, "fmt": fmt, "n": n, "k": k, "m": m,
                                  "mode": MODE_NAMES[mode],
                                  "knobs": list(knobs) if knobs else "library plan",
-                                 "path": "gemm" if gemm else "gemv", "outliers": outliers, "bytes": b,
+                                 "path": "gemm" if gemm else ("mfma_gemv" if mfma else "gemv"), "outliers": outliers,
+                                 "bytes": b,
                                  "us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                                  "pct_peak": round(b / us / 1e3 / PEAK_GBS * 100, 1), "read_floor_us": round(floor, 3),
                                  "of_read_floor": round(floor / us, 3), "copies": nc})  # fmt: skip
@@ -815,7 +819,8 @@ COUNTER_CASES = (  # (fmt, N, K, columns, launch, mode): the kernels the hardwar
     ("tq2_0", 6912, 2560, 3, "fused", 2), ("tq2_0", 2560, 6912, 3, "fused", 2),
     ("tq2_0", 6912, 2560, 2, "gemv", 2), ("tq2_0", 6912, 2560, 3, "gemv", 2),
     ("tq2_0", 2560, 6912, 2, "gemv", 2), ("tq2_0", 2560, 6912, 3, "gemv", 2),
-    ("tq2_0", 32768, 8192, 1, "gemv", 2), ("q4_0", 4096, 14336, 1, "gemv", 2), ("q4_0", 4096, 14336, 3, "gemv", 2),
+    ("tq2_0", 32768, 8192, 1, "gemv", 2), ("tq2_0", 32768, 8192, 3, "gemv", 2),
+    ("q4_0", 4096, 14336, 1, "gemv", 2), ("q4_0", 4096, 14336, 3, "gemv", 2),
     ("q4_0", 128256, 4096, 1, "gemv", 2), ("q4_0", 14336, 4096, 64, "gemm", 2),
     ("q4_k", 14336, 4096, 1, "gemv", 2), ("q8_0", 14336, 4096, 1, "gemv", 2),
     # bytes mode (every value unpacked to an integer, no dot instruction) beside dp4a

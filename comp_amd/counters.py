@@ -11,7 +11,8 @@ order) or a file holding it.  The GEMV and GEMM dispatches of every pass are tak
 averaged over a case's dispatches.  Per weight = instructions x 64 lanes / (N x K): the whole kernel's instructions,
 staging, reductions and stores included.  `dot4` is the exact integer work the format defines: 0.25 v_dot4 per weight
 and column (4 products an instruction), the floor of the dp4a path; the VALU figure includes it.  A case may name its
-mode ("dp4a", the default, or "bytes": no dot instruction, so 0 there).
+mode ("dp4a", the default, or "bytes": no dot instruction, so 0 there); the matrix-core kernels (GEMM, the
+three-column TQ2_0 GEMV) issue none either.
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ import os
 
 # kernel families that make one GEMV / GEMM call (the quantizer and the copies of the weight rotation are not counted)
 FAMILIES = ("tq2_lean_kernel", "tq2_lean_bytes_kernel", "q4_lean_kernel", "q4_lean_bytes_kernel", "q8_lean_kernel",
-            "q4k_lean_kernel", "gemv_kernel", "gemm_kernel")
+            "q4k_lean_kernel", "tq2_mfma_kernel", "gemv_kernel", "gemm_kernel")
 
 
 def _family(name):
@@ -73,7 +74,8 @@ def table(dispatches, cases):
         avg = {k: sum(d["counters"].get(k, 0.0) for d in ds) / len(ds) for k in keys}
         weights = case["n"] * case["k"]
         mode = case.get("mode", "dp4a")
-        dots = case["launch"] != "gemm" and mode != "bytes"
+        # the matrix-core kernels (GEMM, three-column TQ2_0 GEMV) do their integer dots on MFMA, not v_dot4
+        dots = case["launch"] != "gemm" and mode != "bytes" and "mfma_kernel" not in ds[0]["kernel"]
         row = {"fmt": case["fmt"], "n": case["n"], "k": case["k"], "m": case["m"], "launch": case["launch"],
                "mode": mode, "kernel": ds[0]["kernel"], "grid": ds[0]["grid"], "wg": ds[0]["wg"],
                "dispatches": len(ds), "dot4_per_weight": 0.25 * case["m"] if dots else 0.0}  # fmt: skip

@@ -304,11 +304,18 @@ def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
 
 
 def uses_mfma(fmt, m, n, k, fused=False, mode=2, sw=None):
-    """True when gemv(..., block_n=None) runs the matrix-core GEMV for this call (TQ2_0, q8_K in, dp4a, three
-    columns): S as the GEMV kernels', Y to f32 rounding (another order of the f32 sums)."""
+    """True when gemv(..., block_n=None) (gemv_f32 with fused=True) runs the matrix-core GEMV for this call (TQ2_0,
+    dp4a, three columns; f32 in from 4 row tiles a CU on): S as the GEMV kernels', Y to f32 rounding (another order of
+    the f32 sums)."""
+    return mfma_plan(fmt, m, n, k, fused, mode, sw) is not None
+
+
+def mfma_plan(fmt, m, n, k, fused=False, mode=2, sw=None):
+    """(rows, waves) per workgroup of the matrix-core GEMV when gemv(..., block_n=None) runs it for this call, else
+    None."""
     if sw is None:
         sw = k // FORMATS[fmt]["block"] * FORMATS[fmt]["qbytes"]
-    return _abi.gemv_mfma_plan(FMT_ID[fmt], fused, mode, m, n, k, sw) is not None
+    return _abi.gemv_mfma_plan(FMT_ID[fmt], fused, mode, m, n, k, sw)
 
 
 def quantize_into(fmt, x, xq, xd, xb=None, bb=4):
