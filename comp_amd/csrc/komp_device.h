@@ -108,8 +108,20 @@ __device__ __forceinline__ T group_sum(T v, int g) {
     if (g >= 8) v += dpp_i<KOMP_DPP_HALF_MIRROR>(v);
     if (g >= 16) v += dpp_i<KOMP_DPP_MIRROR>(v);
   }
-  if (g >= 32) v += __shfl_xor(v, 16, 64);
-  if (g >= 64) v += __shfl_xor(v, 32, 64);
+  // across rows: v_permlane16_swap(v, v) leaves rows (0 0 2 2) in its first result and (1 1 3 3) in its second,
+  // v_permlane32_swap(v, v) rows (0 1 0 1) and (2 3 2 3), so one swap and one add give each lane its own value plus
+  // its partner row's (lane ^ 16, lane ^ 32: the same sums, added in the same order up to commutation, as an exchange
+  // through LDS, without the LDS round trip)
+  if (g >= 32) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    v = __builtin_bit_cast(T, static_cast<unsigned>(p[0])) + __builtin_bit_cast(T, static_cast<unsigned>(p[1]));
+  }
+  if (g >= 64) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    v = __builtin_bit_cast(T, static_cast<unsigned>(p[0])) + __builtin_bit_cast(T, static_cast<unsigned>(p[1]));
+  }
   return v;
 }
 
