@@ -97,7 +97,7 @@ VALUES_PER_LOAD = {"q4_0": 32, "tq2_0": 64, "q8_0": 16, "iq4_nl": 32, "q4_k": 64
 FMT_NUM = {"q4_0": 0, "tq2_0": 1, "q8_0": 2, "iq4_nl": 3, "q4_k": 4}  # the kernels' format template argument
 
 
-def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
+def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=None):
     """The kernel instantiation a launch of this config runs, the knobs giving lanes per row = 64 / min(block_n /
     num_warps, 16): in dp4a mode, q4_0 / iq4_nl / tq2_0 with 1-3 columns (nb <= 4, or 8 for one column) run the lean
     kernel <(format,) lanes per row, nb, columns, fused, one pass(, tq2_0: staged through an LDS copy)> (q8_0:
@@ -110,7 +110,9 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
     LDS-copy form stages two or three tq2_0 columns that need more than one pass of the workgroup's threads, when LDS
     holds them.  One column with nb < 8 whose waves walk 3 tiles or more (passes x K steps; k given) runs the
     pipelined loop form instead (q4_lean_pipe_kernel <format, lanes, nb, fused>, q4_lean_bytes_pipe_kernel <lanes, nb,
-    fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>)."""
+    fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>).  One tq2_0 dp4a column in the single-pass form with nb <= 4,
+    launched as at most one workgroup a CU (n given: ceil(n / block_n) <= 256, MI355X's CUs), runs the form that reads
+    its LDS pieces ahead of the dots (tq2_lean_pre_kernel <lanes, nb, fused>)."""
     cols = min(max(m, 1), 3)
     lean_mode = mode == 2 or (mode == 0 and fmt in ("tq2_0", "q4_0"))
     if lean_mode and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
@@ -137,6 +139,8 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None):
                 bstep = (lanes // 4) * nb
                 staged = cols * -(-(k // 256) // bstep) * bstep * 296
                 dma = (staged + 15) // 16 * 16 + cols * k + cols * (k // 256) * 4 <= 160 * 1024
+            if one and cols == 1 and nb <= 4 and n is not None and -(-n // block_n) <= 256:
+                return f"gemv_tq2::tq2_lean_pre_kernel<{lanes}, {nb}, false>"
             return (f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}, "
                     f"{str(dma).lower()}>")
         elif fmt == "q8_0" and mode == 2:
@@ -191,7 +195,7 @@ def cmd_gen(args):
     quant = "quant_q8_0" if fmt == "q4_0" else "quant_q8_K"
     try:
         r = isa.summary(_gemv_kernel(fmt, mode, c["nb"], c.get("m", 1), c.get("block_n"), c.get("num_warps"),
-                                     c.get("k")), VALUES_PER_LOAD[fmt], keep=out is not None)  # fmt: skip
+                                     c.get("k"), c.get("n")), VALUES_PER_LOAD[fmt], keep=out is not None)  # fmt: skip
         q = isa.summary(f"{quant}_kernel", 1, keep=out is not None)
     except (OSError, RuntimeError, KeyError) as e:
         print(f"komp gen: {e}", file=sys.stderr)

@@ -592,6 +592,8 @@ Timing timing_slot(int kind) {
   return t;
 }
 
+int device_cu_count() { return device_cus(); }
+
 bool stamps_on() { return g_stamps.on.load(std::memory_order_relaxed); }
 
 uint32_t* stamp_slot(int64_t words) {

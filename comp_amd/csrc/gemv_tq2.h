@@ -135,7 +135,8 @@ __device__ __forceinline__ int quad_scatter2(int p0, int p1, uint64_t odd) {
 // writes the four low words to segs.stamps[4 + 4 * (blockIdx.x * waves + wave)]; thread 0 of workgroup 0 writes the
 // header {kStampMagic, waves of the grid, N, K}.  Scheduling barriers keep each reading in its place.
 // PIPE: the loop form with the weight loads software-pipelined, for waves of many tiles (the reference's knob plans).
-template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES, bool STAMP = false, bool PIPE = false>
+template <int LPR, int NB, int MC, bool FUSED, bool ONE, bool DMA, bool BYTES, bool STAMP = false, bool PIPE = false,
+          bool PRE = false>
 __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nseg, int rows_per_wg, int passes,
                                               const uint8_t* __restrict__ WQ1, const int16_t* __restrict__ WS1,
                                               const void* __restrict__ XA, const float* __restrict__ XD,
@@ -434,6 +435,29 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
     for (int m = 0; m < MC; ++m)
 #pragma unroll
       for (int u = 0; u < NB; ++u) pd[m][u] = 0;
+    // PRE: every slot's activation pieces and every owned block's meta are read from LDS before the first dot (slots
+    // past the row's end read the zero padding), so their latency overlaps the wait for the weights instead of
+    // following it; at the price of 16 VGPRs a slot, so only for launches of at most a workgroup a CU, whose
+    // occupancy they do not cost
+    static_assert(!PRE || (!BYTES && NB * MC <= 4), "PRE: dp4a tiles of at most 4 slots x columns");
+    u32x4 xpre[PRE ? NB : 1][PRE ? MC : 1][4];
+    int2 mpre[PRE ? NOWN : 1][PRE ? MC : 1];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u)
+#pragma unroll
+        for (int m = 0; m < MC; ++m)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            xpre[u][m][j] = *reinterpret_cast<const u32x4*>(xl + (m * nblk_pad + tb + u * BPG) * XB + 32 * j);
+#pragma unroll
+      for (int i = 0; i < NOWN; ++i) {
+        const int u = NB >= 4 ? 4 * i + q : (owner ? q : 0);
+#pragma unroll
+        for (int m = 0; m < MC; ++m) mpre[i][m] = ml[m * nblk_pad + tb + u * BPG];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       if (D == 1 && u * BPG >= lim) break;
@@ -442,7 +466,7 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
         const unsigned char* xp = xl + (m * nblk_pad + tb + u * BPG) * XB;
         u32x4 xv[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xp + 32 * j);
+        for (int j = 0; j < 4; ++j) xv[j] = PRE ? xpre[u][m][j] : *reinterpret_cast<const u32x4*>(xp + 32 * j);
         if constexpr (BYTES) {
           u32x4 xo[4];
 #pragma unroll
@@ -477,7 +501,7 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
           v = quad_scatter2(pd[m][0], pd[m][1], odd);
         else
           v = quad_scatter4(pd[m][4 * i], pd[m][4 * i + 1], pd[m][4 * i + 2], pd[m][4 * i + 3], odd, hi);
-        const int2 mt = ml[m * nblk_pad + tb + u * BPG];
+        const int2 mt = PRE ? mpre[i][m] : ml[m * nblk_pad + tb + u * BPG];
         const int s = (BYTES ? v : v >> 4) + mt.y;  // the block's exact dot
         if (__builtin_expect(S != nullptr, 0)) {
           const int b = tb + u * BPG + gblk;
@@ -545,10 +569,18 @@ __global__ void __launch_bounds__(1024) tq2_lean_kernel(KOMP_TQ2_LEAN_ARGS) {
   tq2_lean_body<LPR, NB, MC, FUSED, ONE, DMA, false>(KOMP_TQ2_LEAN_PASS);
 }
 
-// The stamped single-pass, single-step dp4a form (STAMP above): the measurement instantiation of the tuning harness.
-template <int LPR, int NB, int MC, bool FUSED>
+// The single-pass, single-step dp4a form of one column with every slot's LDS reads ahead of the dots (PRE above), for
+// launches of at most one workgroup a CU.
+template <int LPR, int NB, bool FUSED>
+__global__ void __launch_bounds__(1024) tq2_lean_pre_kernel(KOMP_TQ2_LEAN_ARGS) {
+  tq2_lean_body<LPR, NB, 1, FUSED, true, false, false, false, false, true>(KOMP_TQ2_LEAN_PASS);
+}
+
+// The stamped single-pass, single-step dp4a form (STAMP above): the measurement instantiation of the tuning harness,
+// with or without the early LDS reads as the plain launch would run them.
+template <int LPR, int NB, int MC, bool FUSED, bool PRE>
 __global__ void __launch_bounds__(1024) tq2_lean_stamped_kernel(KOMP_TQ2_LEAN_ARGS) {
-  tq2_lean_body<LPR, NB, MC, FUSED, true, false, false, true>(KOMP_TQ2_LEAN_PASS);
+  tq2_lean_body<LPR, NB, MC, FUSED, true, false, false, true, false, PRE>(KOMP_TQ2_LEAN_PASS);
 }
 
 template <int LPR, int NB, int MC, bool FUSED, bool ONE>
@@ -575,10 +607,25 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
                     p.passes * ((c.k / 256 + (LPR / 4) * NB - 1) / ((LPR / 4) * NB)) >= kPipeMinTiles;
   decltype(&tq2_lean_kernel<LPR, NB, MC, FUSED, true, false>) kern;
   bool dma = false;
+  int64_t groups = (c.n + p.block_n - 1) / p.block_n;
+  if (c.nseg > 1) {
+    groups = 0;
+    for (int i = 0; i < c.nseg; ++i) groups += (c.segs.n[i] + p.block_n - 1) / p.block_n;
+  }
+  // the early LDS reads for one column's single-pass form when the launch holds at most one workgroup a CU (the
+  // decode shapes of a few MB): their registers cost no occupancy there (BitNet-2B 6912 x 2560 fused: span 2.64 ->
+  // 2.49 us), while the many-workgroup launches of large matrices lose waves a SIMD to them (TQ2_0 32768 x 8192:
+  // 13.3 -> 15.3 us)
+  constexpr bool kPreForm = !BYTES && MC == 1 && NB <= 4;
+  const bool pre = kPreForm && one && !tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) &&
+                   groups <= device_cu_count();
   if constexpr (STAMP) {
     if (BYTES || !one || tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) || c.segs.stamps == nullptr)
       return hipErrorInvalidConfiguration;
-    kern = tq2_lean_stamped_kernel<LPR, NB, MC, FUSED>;
+    kern = tq2_lean_stamped_kernel<LPR, NB, MC, FUSED, false>;
+    if constexpr (kPreForm) {
+      if (pre) kern = tq2_lean_stamped_kernel<LPR, NB, MC, FUSED, true>;
+    }
   } else if constexpr (BYTES) {
     kern = one ? tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, false>;
     if constexpr (MC == 1 && NB < 8) {
@@ -589,25 +636,27 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     if constexpr (MC == 1 && NB < 8) {
       if (pipe) kern = tq2_lean_pipe_kernel<LPR, NB, FUSED, false>;
     }
+    if constexpr (kPreForm) {
+      if (pre) kern = tq2_lean_pre_kernel<LPR, NB, FUSED>;
+    }
     if constexpr (MC > 1 && !FUSED) {
       dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false);
       if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
     }
   }
   GemvSegs segs = c.segs;
-  int64_t groups = (c.n + p.block_n - 1) / p.block_n;
   if (c.nseg > 1) {
-    groups = 0;
+    int64_t first = 0;
     for (int i = 0; i < c.nseg; ++i) {
-      segs.first_wg[i] = static_cast<int>(groups);
-      groups += (segs.n[i] + p.block_n - 1) / p.block_n;
+      segs.first_wg[i] = static_cast<int>(first);
+      first += (segs.n[i] + p.block_n - 1) / p.block_n;
     }
   }
   const int nblk = c.k / 256;
   const size_t lds = tq2_lean_lds_bytes(LPR, NB, MC, c.k, FUSED, 64 * p.waves, BYTES);
-  static std::atomic<unsigned> lds_limit[5][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
-  const hipError_t le =
-      allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_limit[pipe ? 4 : (one ? 1 : 0) + (dma ? 2 : 0)]);
+  static std::atomic<unsigned> lds_limit[6][kMaxDevices];  // each kernel's allowed dynamic LDS, per device
+  const hipError_t le = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds,
+                                          lds_limit[pre ? 5 : (pipe ? 4 : (one ? 1 : 0) + (dma ? 2 : 0))]);
   if (le != hipSuccess) return le;
   const dim3 grid(static_cast<unsigned>(groups));
   const dim3 block(static_cast<unsigned>(64 * p.waves));

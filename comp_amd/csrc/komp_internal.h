@@ -173,6 +173,7 @@ constexpr uint32_t kStampMagic = 0x4B535450u;
 bool stamps_on();
 uint32_t* stamp_slot(int64_t words);
 
+int device_cu_count();  // CUs of the current device (256 on MI355X, and when no device can be queried)
 size_t gemv_lds_bytes(int fmt, int m, int k);
 hipError_t launch_gemv(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);

@@ -22,6 +22,7 @@ def run(*args):
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
     for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_tq2::tq2_lean_bytes_kernel<",
+                   "gemv_tq2::tq2_lean_pre_kernel<", "gemv_tq2_mfma::tq2_mfma_kernel<",
                    "gemv_q4::q4_lean_kernel<", "gemv_q4k::q4k_lean_kernel<", "gemv_q8::q8_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
@@ -81,6 +82,17 @@ def test_single_pass_form_follows_the_launch(fmt, bn, nb, nw, k, m, name):
     assert r["loop"].get("dot4", 0) > 0 and r["loop"].get("ld128", 0) > 0
 
 
+def test_early_read_form_follows_the_grid():
+    """One tq2_0 dp4a column in the single-pass form runs the early-LDS-read form when the launch has at most one
+    workgroup a CU (N known), the plain form otherwise; both keep their registers."""
+    pre = "gemv_tq2::tq2_lean_pre_kernel<16, 4, false>"
+    assert cli._gemv_kernel("tq2_0", 2, 4, 1, 16, 4, 2560, 4096) == pre  # 256 workgroups
+    assert cli._gemv_kernel("tq2_0", 2, 4, 1, 16, 4, 2560, 6912) == "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, true, false>"
+    assert cli._gemv_kernel("tq2_0", 2, 4, 3, 16, 4, 2560, 300).startswith("gemv_tq2::tq2_lean_kernel<16, 4, 3,")
+    r = isa.summary(pre, cli.VALUES_PER_LOAD["tq2_0"])
+    assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["loop"].get("dot4", 0) > 0
+
+
 @pytest.mark.parametrize("spec,fmt", [(SPEC_Q4, "q4_0"), (SPEC_TQ2, "tq2_0")])
 def test_gen_reports_and_writes(spec, fmt, tmp_path):
     r = run("gen", spec, "-o", str(tmp_path))
@@ -136,13 +148,13 @@ def test_loops_classes_and_approx_on_synthetic_code():
 
 
 def test_lean_and_gemm_instantiations_do_not_spill():
-    """Every lean GEMV and matrix-core GEMM instantiation of this build keeps its registers: no VGPR or SGPR spills
+    """Every lean GEMV, matrix-core GEMV and GEMM instantiation of this build keeps its registers: no VGPR or SGPR spills
     to scratch memory (the general kernel's rare explicit-knob forms, nb 16 with 3 columns in bytes or emulated mode,
     are outside this check)."""
     spills = []
     for co in isa.library_code_objects():
         for name, k in co.kernels.items():
-            lean_or_gemm = "lean" in name or "gemm_kernel" in name
+            lean_or_gemm = "lean" in name or "gemm_kernel" in name or "mfma_kernel" in name
             if lean_or_gemm and (k["vgpr_spill"] or k["sgpr_spill"] or k["scratch"]):
                 spills.append((name[:90], k["vgpr_spill"], k["scratch"]))
     assert not spills, spills
