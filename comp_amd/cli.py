@@ -112,8 +112,12 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=Non
     pipelined loop form instead (q4_lean_pipe_kernel <format, lanes, nb, fused>, q4_lean_bytes_pipe_kernel <lanes, nb,
     fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>).  One tq2_0 dp4a column in the single-pass form with nb <= 4,
     launched as at most one workgroup a CU (n given: ceil(n / block_n) <= 256, MI355X's CUs), runs the form that reads
-    its LDS pieces ahead of the dots (tq2_lean_pre_kernel <lanes, nb, fused>)."""
+    its LDS pieces ahead of the dots (tq2_lean_pre_kernel <lanes, nb, fused>).  A tq2_0 K step below 256 bytes a row
+    (lanes x nb x 16) is widened to it (nb doubled up to 4), as the launch does."""
     cols = min(max(m, 1), 3)
+    if fmt == "tq2_0" and block_n and num_warps:  # the launch widens a tq2_0 K step to 256 bytes a row
+        while 64 // min(block_n // num_warps, 16) * nb < 16 and nb < 4:
+            nb *= 2
     lean_mode = mode == 2 or (mode == 0 and fmt in ("tq2_0", "q4_0"))
     if lean_mode and block_n and num_warps and (nb in (1, 2, 4) or (nb == 8 and cols == 1)):
         rpw = block_n // num_warps

@@ -259,7 +259,7 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   return plan_of(w * rpw, nb, w, lpr, 1);
 }
 
-GemvPlan knob_plan(int block_n, int nb, int num_warps) {
+GemvPlan knob_plan(int fmt, int block_n, int nb, int num_warps) {
   GemvPlan plan;
   plan.block_n = block_n;
   plan.nb = nb;
@@ -270,6 +270,13 @@ GemvPlan knob_plan(int block_n, int nb, int num_warps) {
   while ((64 >> plan.lpr_log2) > rpp) ++plan.lpr_log2;
   plan.passes = rpw / rpp;
   plan.rows_per_wave = rpw;
+  // TQ2_0 (64-byte blocks): a K step of fewer than 256 bytes a row (lanes a row x nb x 16) leaves every load
+  // instruction half a cache line of each row, and the few workgroups of such knob sets (one per block_n rows) are
+  // bound by the misses each CU keeps in flight.  The step is widened to 256 bytes a row (nb 1 or 2 -> 4 at 4 lanes a
+  // row, 1 -> 2 at 8): the same rows a workgroup and waves, S the same, Y within the same bound.  The reference's spec
+  // defaults (block_n 64, nb 1, num_warps 4) at BitNet-2B 2560 x 6912: 9.95 -> 7.46 us; 6912 x 2560 4.93 -> 4.22.
+  if (fmt == FMT_TQ2_0)
+    while ((1 << plan.lpr_log2) * plan.nb < 16 && plan.nb < 4) plan.nb *= 2;
   return plan;
 }
 
@@ -519,7 +526,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
   int64_t sw_max = 0;
   for (int i = 0; i < count; ++i) sw_max = mats[i].sw > sw_max ? mats[i].sw : sw_max;
   const GemvPlan plan =
-      block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K, sw_max) : knob_plan(block_n, nb, num_warps);
+      block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K, sw_max) : knob_plan(fmt, block_n, nb, num_warps);
 
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
     GemvCall c = {};

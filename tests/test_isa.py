@@ -61,7 +61,7 @@ def test_single_column_configs_name_their_kernel(fmt, bn, nb, nw, name):
     ("tq2_0", 16, 2, 4, 2560, 3, "gemv_tq2::tq2_lean_kernel<16, 2, 3, false, false, true>"),  # 10 blocks > 4 x 2
     # two passes of 3 K steps a wave: 6 tiles, the pipelined loop form
     ("tq2_0", 128, 4, 4, 2560, 1, "gemv_tq2::tq2_lean_pipe_kernel<4, 4, false, false>"),
-    ("tq2_0", 64, 1, 4, 6912, 1, "gemv_tq2::tq2_lean_pipe_kernel<4, 1, false, false>"),  # the spec defaults: 27 tiles
+    ("tq2_0", 64, 1, 4, 6912, 1, "gemv_tq2::tq2_lean_pipe_kernel<4, 4, false, false>"),  # the spec defaults: nb 1 -> 4, 7 tiles
     ("q4_0", 64, 4, 4, 4096, 1, "gemv_q4::q4_lean_pipe_kernel<0, 4, 4, false>"),  # 8 K steps of 16 blocks
     ("q4_0", 64, 4, 4, 4096, 2, "gemv_q4::q4_lean_kernel<0, 4, 4, 2, false, false>"),  # two columns: one buffer
     ("q4_0", 8, 2, 8, 4096, 1, "gemv_q4::q4_lean_kernel<0, 64, 2, 1, false, true>"),    # 128 blocks <= 64 x 2
