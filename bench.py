@@ -51,7 +51,7 @@ COLD_BYTES = 1 << 30  # weight copies rotated per workload (4x the 256 MB Infini
 # HBM bytes per launch of the headline's fused tq2_0 kernel (mean of the two shapes, m=1, dp4a, library-chosen knobs),
 # from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a 256 MiB copy:
 # profiles/tq2_0_gemv_bitnet2b_decode_chain.md.  Reported only for that configuration.
-TRAFFIC_FUSED_BITNET_M1 = 4833134
+TRAFFIC_FUSED_BITNET_M1 = 4829049
 
 
 # (values per weight block, weight bytes per block, values per activation block) of each weight format
