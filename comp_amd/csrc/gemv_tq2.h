@@ -571,9 +571,9 @@ __global__ void __launch_bounds__(1024) tq2_lean_kernel(KOMP_TQ2_LEAN_ARGS) {
 
 // The single-pass, single-step dp4a form of one column with every slot's LDS reads ahead of the dots (PRE above), for
 // launches of at most one workgroup a CU.
-template <int LPR, int NB, bool FUSED>
+template <int LPR, int NB, int MC, bool FUSED, bool DMA>
 __global__ void __launch_bounds__(1024) tq2_lean_pre_kernel(KOMP_TQ2_LEAN_ARGS) {
-  tq2_lean_body<LPR, NB, 1, FUSED, true, false, false, false, false, true>(KOMP_TQ2_LEAN_PASS);
+  tq2_lean_body<LPR, NB, MC, FUSED, true, DMA, false, false, false, true>(KOMP_TQ2_LEAN_PASS);
 }
 
 // The stamped single-pass, single-step dp4a form (STAMP above): the measurement instantiation of the tuning harness,
@@ -616,9 +616,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   // decode shapes of a few MB): their registers cost no occupancy there (BitNet-2B 6912 x 2560 fused: span 2.64 ->
   // 2.49 us), while the many-workgroup launches of large matrices lose waves a SIMD to them (TQ2_0 32768 x 8192:
   // 13.3 -> 15.3 us)
-  constexpr bool kPreForm = !BYTES && MC == 1 && NB <= 4;
-  const bool pre = kPreForm && one && !tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) &&
-                   groups <= device_cu_count();
+  constexpr bool kPreForm = !BYTES && MC <= 2 && NB * MC <= 4;
+  const bool pre = kPreForm && one && groups <= device_cu_count();
   if constexpr (STAMP) {
     if (BYTES || !one || tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) || c.segs.stamps == nullptr)
       return hipErrorInvalidConfiguration;
@@ -637,11 +636,14 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
       if (pipe) kern = tq2_lean_pipe_kernel<LPR, NB, FUSED, false>;
     }
     if constexpr (kPreForm) {
-      if (pre) kern = tq2_lean_pre_kernel<LPR, NB, FUSED>;
+      if (pre) kern = tq2_lean_pre_kernel<LPR, NB, MC, FUSED, false>;
     }
     if constexpr (MC > 1 && !FUSED) {
       dma = tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false);
       if (dma) kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, true> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, true>;
+      if constexpr (kPreForm) {
+        if (dma && pre) kern = tq2_lean_pre_kernel<LPR, NB, MC, FUSED, true>;
+      }
     }
   }
   GemvSegs segs = c.segs;

@@ -83,12 +83,14 @@ def test_single_pass_form_follows_the_launch(fmt, bn, nb, nw, k, m, name):
 
 
 def test_early_read_form_follows_the_grid():
-    """One tq2_0 dp4a column in the single-pass form runs the early-LDS-read form when the launch has at most one
-    workgroup a CU (N known), the plain form otherwise; both keep their registers."""
-    pre = "gemv_tq2::tq2_lean_pre_kernel<16, 4, false>"
+    """One or two tq2_0 dp4a columns in the single-pass form (nb x columns <= 4) run the early-LDS-read form when the
+    launch has at most one workgroup a CU (N known), the plain form otherwise; both keep their registers."""
+    pre = "gemv_tq2::tq2_lean_pre_kernel<16, 4, 1, false, false>"
     assert cli._gemv_kernel("tq2_0", 2, 4, 1, 16, 4, 2560, 4096) == pre  # 256 workgroups
     assert cli._gemv_kernel("tq2_0", 2, 4, 1, 16, 4, 2560, 6912) == "gemv_tq2::tq2_lean_kernel<16, 4, 1, false, true, false>"
     assert cli._gemv_kernel("tq2_0", 2, 4, 3, 16, 4, 2560, 300).startswith("gemv_tq2::tq2_lean_kernel<16, 4, 3,")
+    # two columns at nb 2 (4 slots x columns): the early reads too, here with the columns copied global -> LDS
+    assert cli._gemv_kernel("tq2_0", 2, 2, 2, 8, 8, 6912, 2048) == "gemv_tq2::tq2_lean_pre_kernel<64, 2, 2, false, true>"
     r = isa.summary(pre, cli.VALUES_PER_LOAD["tq2_0"])
     assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["loop"].get("dot4", 0) > 0
 
