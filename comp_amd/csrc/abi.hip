@@ -245,6 +245,15 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
     // many rows per CU with short rows (Llama-3-8B's gate and up projections, 14336 x 4096): 4-wave workgroups of 8
     // rows, two rows per wave with 32 lanes each, nb 2 (2-4 K steps); 10-15% faster than one K step of 64 lanes
     return plan_of(8, 2, 4, 32, 1);
+  if (fmt == FMT_TQ2_0 && m == 3 && mode == KOMP_MODE_DP4A && nblk <= 16) {
+    // three TQ2_0 columns over few rows (these plans): the lean kernel stages 16 threads per block and column, and a
+    // second staging pass of 8 waves costs more than a wider workgroup; one row a wave, as many waves as one pass
+    // takes (127 x 2816: 3.21 -> 2.75 us, f32 in 3.71 -> 3.33; 2048 x 2816: 3.47 -> 3.01; 1000 x 4096, 12 waves: 3.08
+    // -> 2.92; at 2560 columns 8 waves already stage in one pass).  Longer rows (6912 columns) keep 8 waves: 16 of
+    // them in two passes ran slower.
+    const int64_t stage_waves = (m * nblk * 16 + 63) / 64;
+    if (stage_waves > 8) return plan_of(static_cast<int>(stage_waves), 1, static_cast<int>(stage_waves), 64, 1);
+  }
   int lpr = pow2_ceil(fused ? (chunks + 1) / 2 : chunks);
   lpr = lpr < 4 ? 4 : (lpr > 64 ? 64 : lpr);
   if (lpr < bpb) lpr = bpb;  // a row group holds whole blocks
@@ -362,26 +371,31 @@ bool gemm_plan(int fmt, int64_t m, int64_t n, int64_t k, int64_t sw, GemmPlan* p
 
 // The matrix-core GEMV (gemv_tq2_mfma.hip) for kMfmaM TQ2_0 columns, block_n == 0 in dp4a mode.  Measured on MI355X
 // against the lean kernel's plans (graph replays, cold weights), three columns with q8_K in: BitNet-2B 6912 x 2560
-// 3.95 -> 3.84 us, 2560 x 6912 4.6 -> 4.4, 6913 x 2816 4.5 -> 3.9, 32768 x 8192 23.3 -> 18.4; f32 in (each wave
-// quantizing its own blocks): 32768 x 8192 32.4 -> 24.0, but 1.1-1.3 us slower at the BitNet-2B shapes, where every
-// workgroup reading all 3 x K f32 inputs costs more than the dots save (there the lean kernel's fewer, fuller
-// workgroups stay), so fused launches take it from 4 row tiles a CU on.  Two columns stay on the lean kernel (as fast
-// or faster at every shape measured).  Plans: one block a wave (up to 16 waves a
-// workgroup) for rows of up to 16 blocks, else about two; from 4 row tiles a CU, two tiles a workgroup (each
-// activation load serves both) and four blocks a wave.  False when the shape is past it (rows of more than 64 blocks,
-// or past its 32-bit descriptor ranges).
+// 3.95 -> 3.84 us, 2560 x 6912 4.44 -> 4.22, 6913 x 2816 4.5 -> 3.9, 4097 x 2816 4.2 -> 3.3, 32768 x 8192 23.3 ->
+// 18.4; f32 in (each wave quantizing its own blocks): 32768 x 8192 32.4 -> 24.0, but 1.1-1.3 us slower at the
+// BitNet-2B shapes, where every workgroup reading all 3 x K f32 inputs costs more than the dots save (there the lean
+// kernel's fewer, fuller workgroups stay), so fused launches take it from 4 row tiles a CU on.  Up to 8 rows a CU the
+// lean kernel is faster (0.3-0.9 us at 64-2048 rows x 2560-8192 columns): every workgroup reads all 3 x K
+// activations for few rows.  Two columns stay on the lean kernel (as fast or faster at every shape measured).
+// Plans: rows spread evenly over the CUs, at most 16 a workgroup (2560 rows: 256 workgroups of 10, 4.22 us against
+// 4.39 for 160 of 16); one block a wave (up to 16 waves a workgroup) for rows of up to 16 blocks, else about two; from
+// 4 row tiles a CU, two tiles a workgroup (each activation load serves both) and four blocks a wave.  False when the
+// shape is past it (rows of more than 64 blocks, or past its 32-bit descriptor ranges).
 constexpr int64_t kMfmaM = 3;
 bool tq2_mfma_plan(int64_t m, int64_t n, int64_t k, int64_t sw, bool fused, MfmaPlan* p) {
   if (m != kMfmaM || k <= 0 || k % 256 || n < 1) return false;
   const int64_t nblk = k / 256;
+  const int64_t cus = device_cus();
   const int64_t tiles = (n + 15) / 16;
-  const bool big = tiles >= 4 * device_cus();
-  if (fused && !big) return false;
+  const bool big = tiles >= 4 * cus;
+  if (n <= 8 * cus || (fused && !big)) return false;
   int64_t waves = big ? (nblk + 3) / 4 : (nblk <= 16 ? nblk : (nblk + 1) / 2);
   waves = waves > 16 ? 16 : waves;
   const int64_t nbw = (nblk + waves - 1) / waves;
   if (nbw > 4 || 16 * sw > 0x7FFFFFF0 || 4 * k > 0x7FFFFFF0) return false;
-  *p = MfmaPlan{big ? 2 : 1, static_cast<int>(waves), static_cast<int>(nbw)};
+  const int64_t even = (n + cus - 1) / cus;  // rows a CU: more than 8
+  const int64_t rows = big ? 32 : (even < 16 ? even : 16);
+  *p = MfmaPlan{big ? 2 : 1, static_cast<int>(waves), static_cast<int>(nbw), static_cast<int>(rows)};
   return true;
 }
 
@@ -739,7 +753,7 @@ int komp_gemv_mfma_plan(int fmt, int fused, int mode, int64_t M, int64_t N, int6
   if (M < 0 || N < 0 || K < 0 || SW < 0) return fail(KOMP_EINVAL, "komp_gemv_mfma_plan: bad argument");
   MfmaPlan p;
   const bool on = mode == KOMP_MODE_DP4A && fmt == FMT_TQ2_0 && tq2_mfma_plan(M, N, K, SW, fused != 0, &p);
-  if (rows_per_wg != nullptr) *rows_per_wg = on ? 16 * p.tiles : 0;
+  if (rows_per_wg != nullptr) *rows_per_wg = on ? p.rows : 0;
   if (waves != nullptr) *waves = on ? p.waves : 0;
   return on ? 1 : 0;
 }

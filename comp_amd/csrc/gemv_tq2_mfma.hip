@@ -44,8 +44,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-// T row tiles of 16 a workgroup, at most NBW blocks a wave, MC columns (at most 4: the C lanes of row group 0).  The first 14 argument dwords (preloaded
-// into SGPRs) are the ones the first loads need.  STAMP: the measurement instantiation; each wave reads the real-time
+// R rows a workgroup (the host's plan, at most 16 T) in T row tiles of 16, at most NBW blocks a wave, MC columns (at
+// most 4: the C lanes of row group 0).  The lanes of a tile's rows past R (or past N) load zeros and store nothing, so
+// R balances the rows over the CUs (2560 rows: 256 workgroups of 10 rows, not 160 of 16).  The first 15 argument
+// dwords (preloaded into SGPRs) are the ones the first loads need.  STAMP: the measurement instantiation; each wave reads the real-time
 // counter on entry, once its loads have landed, after its blocks are scaled and once the workgroup's outputs are
 // stored, and lane 0 writes the four low words to stamps[4 + 4 * (blockIdx.x * waves + wave)] (header {kStampMagic,
 // waves of the grid, N, K} from thread 0 of workgroup 0), the lean kernels' record layout.
@@ -56,7 +58,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
 template <int T, int NBW, int MC, bool FUSED, bool STAMP>
 __global__ void __launch_bounds__(64 * kMaxWaves)
 tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, const int16_t* __restrict__ WS, int N,
-                int nblk, int SW, int K, const float* __restrict__ XD, float* __restrict__ Y,
+                int R, int nblk, int SW, int K, const float* __restrict__ XD, float* __restrict__ Y,
                 int32_t* __restrict__ S, uint32_t* __restrict__ stamps, int8_t* __restrict__ XQo,
                 float* __restrict__ XDo, int16_t* __restrict__ XBo) {
   extern __shared__ __align__(16) unsigned char lds[];
@@ -70,7 +72,8 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
   const int ks = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);  // waves, each a range of blocks
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int row0 = blockIdx.x * (16 * T);
+  const int row0 = blockIdx.x * R;
+  const int row_end = min(N, row0 + R);  // past the workgroup's last row
   const int b0 = wave * nblk / ks;  // this wave's blocks: [b0, b0 + nbw), nbw <= NBW (the host's plan)
   const int nbw = (wave + 1) * nblk / ks - b0;
 
@@ -121,7 +124,7 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int rt = row0 + 16 * t;
-    const unsigned rows = __builtin_amdgcn_readfirstlane(min(16, max(0, N - rt)));  // wave-uniform
+    const unsigned rows = __builtin_amdgcn_readfirstlane(min(16, max(0, row_end - rt)));  // wave-uniform
     const auto wr = rsrc(WQ + static_cast<int64_t>(rt) * SW, rows * static_cast<unsigned>(SW));
     const unsigned vw = static_cast<unsigned>(r16 * SW + 16 * g);
 #pragma unroll
@@ -252,7 +255,7 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
         sb = cc[t][i] + corr[i];
       }
       if (__builtin_expect(S != nullptr, 0)) {
-        if (g == 0 && row < N && i < nbw) {
+        if (g == 0 && row < row_end && i < nbw) {
 #pragma unroll
           for (int k = 0; k < MC; ++k) S[(static_cast<int64_t>(k) * N + row) * nblk + b0 + i] = sb[k];
         }
@@ -289,7 +292,7 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int row = row0 + 16 * t + r16;
-        if (row < N) {
+        if (row < row_end) {
 #pragma unroll
           for (int k = 0; k < MC; ++k) Y[static_cast<int64_t>(k) * N + row] = acc[t][k];
         }
@@ -313,7 +316,7 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
     float sum = red[(t * MC + k) * 16 + r];
     for (int p = 1; p < ks; ++p) sum += red[((p * T + t) * MC + k) * 16 + r];
     const int row = row0 + 16 * t + r;
-    if (row < N) Y[static_cast<int64_t>(k) * N + row] = sum;
+    if (row < row_end) Y[static_cast<int64_t>(k) * N + row] = sum;
   }
   stamp_out();
 }
@@ -321,7 +324,7 @@ tq2_mfma_kernel(const void* __restrict__ XA, const uint8_t* __restrict__ WQ, con
 template <int T, int NBW, int MC, bool FUSED>
 hipError_t launch_k(const GemvCall& c, const MfmaPlan& p, hipStream_t stream) {
   const int nblk = c.k / 256;
-  const unsigned groups = static_cast<unsigned>((c.n + 16 * T - 1) / (16 * T));
+  const unsigned groups = static_cast<unsigned>((c.n + p.rows - 1) / p.rows);
   // the tuning harness's wave stamps, while there is room for them
   uint32_t* const slot = stamps_on() ? stamp_slot(4 + 4 * int64_t{groups} * p.waves) : nullptr;
   const auto kern =
@@ -332,10 +335,10 @@ hipError_t launch_k(const GemvCall& c, const MfmaPlan& p, hipStream_t stream) {
   const void* xa = FUSED ? static_cast<const void*>(c.x) : static_cast<const void*>(c.xq);
   const Timing tm = timing_slot(KIND_TQ2_0_GEMV);
   if (tm.on)
-    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, xa, c.wq, c.ws, c.n, nblk, sw, c.k,
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, tm.start, tm.stop, 0, xa, c.wq, c.ws, c.n, p.rows, nblk, sw, c.k,
                           c.xd, c.y, c.s, slot, c.xq_out, c.xd_out, c.xb_out);
   else
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, xa, c.wq, c.ws, c.n, nblk, sw, c.k, c.xd, c.y, c.s, slot,
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, xa, c.wq, c.ws, c.n, p.rows, nblk, sw, c.k, c.xd, c.y, c.s, slot,
                        c.xq_out, c.xd_out, c.xb_out);
   return hipGetLastError();
 }
@@ -368,7 +371,7 @@ bool tq2_mfma_eligible(const GemvCall& c, const MfmaPlan& p) {
   if (c.fmt != FMT_TQ2_0 || c.mode != MODE_DP4A || c.nseg > 1 || c.m != 3) return false;
   if (c.x == nullptr && (c.xq == nullptr || c.xd == nullptr)) return false;
   if (c.k % 256 != 0 || c.k <= 0 || c.n <= 0) return false;
-  if (p.tiles < 1 || p.tiles > 2 || p.waves < 1 || p.waves > gemv_tq2_mfma::kMaxWaves || p.nbw < 1 || p.nbw > 4)
+  if (p.tiles < 1 || p.tiles > 2 || p.rows < 1 || p.rows > 16 * p.tiles || p.waves < 1 || p.waves > gemv_tq2_mfma::kMaxWaves || p.nbw < 1 || p.nbw > 4)
     return false;
   const int64_t nblk = c.k / 256;
   if ((nblk + p.waves - 1) / p.waves > p.nbw) return false;                   // each wave's range fits its slots

@@ -198,12 +198,13 @@ size_t q8_lean_lds_bytes(int lpr, int nb, int mc, int k);
 hipError_t launch_gemv_q8_lean(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_gemv_q8_lean_fused(const GemvCall& c, const GemvPlan& p, hipStream_t stream);
 
-// TQ2_0, 2-4 columns in dp4a mode, q8_K in, on the matrix cores (gemv_tq2_mfma.hip): workgroups of `tiles` 16-row
-// tiles whose `waves` waves split K into ranges of at most `nbw` blocks
+// TQ2_0, three columns in dp4a mode, q8_K or f32 in, on the matrix cores (gemv_tq2_mfma.hip): workgroups of `rows`
+// rows in `tiles` 16-row tiles (rows <= 16 tiles) whose `waves` waves split K into ranges of at most `nbw` blocks
 struct MfmaPlan {
   int tiles;
   int waves;
   int nbw;
+  int rows;
 };
 size_t tq2_mfma_lds_bytes(int tiles, int nbw, int mc, bool fused, int waves);
 bool tq2_mfma_eligible(const GemvCall& c, const MfmaPlan& p);

@@ -305,8 +305,8 @@ def uses_gemm(fmt, m, n, k, fused=False, mode=2, sw=None):
 
 def uses_mfma(fmt, m, n, k, fused=False, mode=2, sw=None):
     """True when gemv(..., block_n=None) (gemv_f32 with fused=True) runs the matrix-core GEMV for this call (TQ2_0,
-    dp4a, three columns; f32 in from 4 row tiles a CU on): S as the GEMV kernels', Y to f32 rounding (another order of
-    the f32 sums)."""
+    dp4a, three columns, more than 8 rows a CU; f32 in from 4 row tiles a CU on): S as the GEMV kernels', Y to f32
+    rounding (another order of the f32 sums)."""
     return mfma_plan(fmt, m, n, k, fused, mode, sw) is not None
 
 

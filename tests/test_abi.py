@@ -192,11 +192,19 @@ def test_auto_plan_q4_0_columns_llama_shapes(n, k, plan):
 
 
 def test_auto_plan_tq2_columns_few_rows_use_knob_sets():
-    # 2-3 columns need at least 7 waves of the one-workgroup-per-CU plan; fewer rows take the 8-wave knob-set plans
+    # 2-3 columns need at least 7 waves of the one-workgroup-per-CU plan; fewer rows take the 8-wave knob-set plans,
+    # except three dp4a columns whose q8_K staging (16 threads per block and column) needs more than 8 waves: one
+    # row a wave, as many waves as one staging pass takes (3 x 11 blocks x 16 = 528 threads: 9 waves)
     for n, k in ((127, 2816), (4097, 2816)):
-        for m in (2, 3):
-            bn, nb, nw, lanes, passes = _abi.auto_plan(1, m, n, k, True)
+        for fused in (True, False):
+            bn, nb, nw, lanes, passes = _abi.auto_plan(1, 2, n, k, fused)
             assert bn in (8, 16, 32, 64, 128) and nw == 8 and lanes == 64 // min(bn // nw, 16)
+            assert _abi.auto_plan(1, 3, n, k, fused) == (9, 1, 9, 64, 1)
+            bn, nb, nw, lanes, passes = _abi.auto_plan(1, 3, n, k, fused, 0)  # bytes mode: the knob sets
+            assert nw == 8 and lanes == 64 // min(bn // nw, 16)
+    assert _abi.auto_plan(1, 3, 1000, 4096, False) == (12, 1, 12, 64, 1)
+    assert _abi.auto_plan(1, 3, 300, 2560, False)[2] == 8  # 480 staging threads: 8 waves take them in one pass
+    assert _abi.auto_plan(1, 3, 127, 6912, False)[2] == 8  # 1296: two passes either way, 8 waves
     assert _abi.auto_plan(1, 3, 6913, 2816, True)[2] == 7  # 28 rows per CU: 7 waves of 4 rows
 
 

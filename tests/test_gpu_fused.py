@@ -20,7 +20,8 @@ def dev(a):
 CASES = [("q4_0", 37, 416, 3), ("q4_0", 4097, 4192, 1), ("q4_0", 64, 512, 4), ("tq2_0", 37, 768, 3),
          ("tq2_0", 6913, 2816, 2), ("tq2_0", 5, 1280, 1), ("q8_0", 37, 416, 3), ("q8_0", 4097, 4192, 1),
          ("iq4_nl", 37, 416, 3), ("iq4_nl", 4097, 4192, 1), ("iq4_nl", 64, 512, 4), ("q4_k", 37, 768, 3),
-         ("q4_k", 4097, 4352, 1), ("q4_k", 64, 1024, 4)]  # fmt: skip
+         ("q4_k", 4097, 4352, 1), ("q4_k", 64, 1024, 4),
+         ("tq2_0", 2048, 2816, 3), ("tq2_0", 1000, 4096, 3)]  # 3 columns over few rows: 9 and 12 waves of one row  # fmt: skip
 
 
 @pytest.mark.parametrize("fmt,n,k,m", CASES)

@@ -1,5 +1,6 @@
 """The TQ2_0 matrix-core GEMV (gemv_tq2_mfma.hip: three columns, q8_K or f32 in, dp4a mode, block_n=None) through the C ABI: S exact and Y within the output gate against the oracle, S bit for bit the lean dp4a
-kernel's (explicit knobs), at the BitNet-2B shapes, ragged row counts, rows of 1-56 blocks (one wave a workgroup up to
+kernel's (explicit knobs), at the BitNet-2B shapes, ragged row counts (full and partial last workgroups of 9-16 rows),
+rows of 1-56 blocks (one wave a workgroup up to
 16 waves of 1-4 blocks), one and two row tiles a workgroup, and the extreme data (crumb 3 against +-127
 activations)."""
 
@@ -13,14 +14,14 @@ from tests.checks import outputs_ok
 
 pytestmark = pytest.mark.gpu
 
-CASES = [
-    (6912, 2560, 3),   # BitNet-2B W1: 432 workgroups of 10 waves, one block a wave
-    (2560, 6912, 3),   # BitNet-2B W2: 14 waves of 2 blocks, the last one 1
-    (300, 2560, 3),    # a partial last tile (12 of 16 rows)
-    (77, 14336, 3),    # 56 blocks: 16 waves of 3-4 blocks
-    (16, 256, 3),      # one block: one wave, no partial sums to add
-    (33, 512, 3),      # two blocks, two waves; 3 tiles, the last of 1 row
-    (1000, 4096, 3),   # 16 blocks, 16 waves
+CASES = [  # workgroups as planned on the 256 CUs of an MI355X
+    (6912, 2560, 3),   # BitNet-2B W1: 432 workgroups of 16 rows and 10 waves, one block a wave
+    (2560, 6912, 3),   # BitNet-2B W2: 256 workgroups of 10 rows; 14 waves of 2 blocks, the last one 1
+    (2600, 2560, 3),   # 237 workgroups of 11 rows, the last of 4
+    (2100, 14336, 3),  # 56 blocks: 16 waves of 3-4 blocks; 234 workgroups of 9 rows, the last of 3
+    (2053, 256, 3),    # one block: one wave, no partial sums to add; the last workgroup of 1 row
+    (2090, 512, 3),    # two blocks, two waves; the last workgroup of 2 rows
+    (3000, 4096, 3),   # 16 blocks, 16 waves; 250 workgroups of 12 rows
     (16389, 512, 3),   # 1025 row tiles: two tiles a workgroup (the last one past the matrix), one wave of 2 blocks
     (16400, 2304, 3),  # two tiles a workgroup, 5 waves of 1-2 blocks
     (16390, 4096, 3),  # two tiles a workgroup, 8 waves of 2 blocks
@@ -70,6 +71,11 @@ def test_mfma_gemv_routing():
     assert host.uses_mfma("tq2_0", 3, 32768, 8192, fused=True) and not host.uses_mfma("tq2_0", 3, 6912, 2560, fused=True)
     assert not host.uses_mfma("tq2_0", 3, 6912, 2560, mode=0) and not host.uses_mfma("q4_0", 3, 4096, 4096)
     assert not host.uses_mfma("tq2_0", 3, 4096, 65536)  # rows of 256 blocks: past its 4 blocks a wave
+    # up to 8 rows a CU (2048 on 256 CUs) the lean kernel is faster; past it the rows spread evenly, at most 16 a
+    # workgroup
+    assert not host.uses_mfma("tq2_0", 3, 2048, 2560) and not host.uses_mfma("tq2_0", 3, 127, 2816)
+    assert host.mfma_plan("tq2_0", 3, 2560, 6912) == (10, 14) and host.mfma_plan("tq2_0", 3, 6912, 2560) == (16, 10)
+    assert host.mfma_plan("tq2_0", 3, 32768, 8192) == (32, 8)
 
 
 def test_mfma_gemv_stamped_instantiation():
