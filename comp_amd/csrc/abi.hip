@@ -268,6 +268,14 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
   return plan_of(w * rpw, nb, w, lpr, 1);
 }
 
+// Unfused single Q4_0 / IQ4_NL columns in the lean kernel's modes (dp4a; Q4_0 bytes too): the launches whose knob
+// programs may run one workgroup a wave (gemv_entry).
+bool knob_waves_apart(int fmt, bool fused, int mode, int64_t m) {
+  return !fused && m == 1 &&
+         ((fmt == FMT_Q4_0 && (mode == KOMP_MODE_DP4A || mode == KOMP_MODE_BYTES)) ||
+          (fmt == FMT_IQ4_NL && mode == KOMP_MODE_DP4A));
+}
+
 GemvPlan knob_plan(int fmt, int block_n, int nb, int num_warps) {
   GemvPlan plan;
   plan.block_n = block_n;
@@ -539,8 +547,20 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
 
   int64_t sw_max = 0;
   for (int i = 0; i < count; ++i) sw_max = mats[i].sw > sw_max ? mats[i].sw : sw_max;
-  const GemvPlan plan =
+  GemvPlan plan =
       block_n == 0 ? auto_plan(fmt, fused, mode, M, total_rows, K, sw_max) : knob_plan(fmt, block_n, nb, num_warps);
+  if (block_n != 0 && num_warps > 1 && knob_waves_apart(fmt, fused, mode, M)) {
+    // The knobs fix each wave's rows (block_n / num_warps), lanes per row and nb, and with them every output bit: a
+    // program's waves share no rows.  How the waves group into workgroups is the launch's: when the programs hold no
+    // more waves than the device has CUs, each wave runs as a workgroup of its own, so the programs' rows spread over
+    // every CU instead of block_n / num_warps of them (Q4_0 4096 x 4096 at 64/4/4: 64 workgroups of 4 waves 7.45 us,
+    // 256 of one 6.25; 4096 x 14336 22.0 -> 17.0; 128/4/8 12.4 -> 6.3; IQ4_NL 8.55 -> 8.15).  Unfused Q4_0 / IQ4_NL
+    // columns on the lean kernel only: a fused launch's workgroups each quantize all of K, which one wave does slower
+    // (8.7 -> 10.5 us), and TQ2_0's each stage all of K (2560 x 6912 at 64/1/4: 7.45 -> 7.52, bytes 10.3 -> 10.8).
+    int64_t programs = 0;
+    for (int i = 0; i < count; ++i) programs += (mats[i].n + block_n - 1) / block_n;
+    if (programs * num_warps <= device_cus()) plan = knob_plan(fmt, block_n / num_warps, nb, 1);
+  }
 
   for (int64_t m0 = 0; m0 < M; m0 += mc) {
     GemvCall c = {};
