@@ -167,7 +167,9 @@ int komp_q4_k_split(const uint8_t* W, uint8_t* WQ, int16_t* WS, int64_t N, int64
  * in sequence.  The explicit knobs map (block_n, nb, num_warps) to lanes_per_row = 64 / min(block_n / num_warps, 16)
  * and passes = (block_n / num_warps) / min(block_n / num_warps, 16); an auto plan with other values, or with
  * block_n / num_warps outside the knob sets (one workgroup of ceil(N / CUs) rows per CU, up to 16 waves, for small
- * single-column GEMVs), has no explicit knob equivalent.
+ * single-column GEMVs), has no explicit knob equivalent.  (Explicit knobs of unfused single Q4_0 / IQ4_NL columns
+ * whose block_n-row programs hold no more waves than the device has CUs launch each wave as a workgroup of its own:
+ * the same rows, lanes and K steps a wave, the same results.)
  * No reference counterpart: the reference always takes the knobs from its caller. */
 int komp_gemv_auto_config(int fmt, int fused, int mode, int64_t M, int64_t N, int64_t K, int* block_n, int* nb,
                           int* num_warps, int* lanes_per_row, int* passes);
