@@ -197,6 +197,12 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       const int nb_max = fmt == FMT_Q4_K ? 2 : (m > 1 ? 4 : 8);
       int nb = pow2_ceil((nblk + blocks_per_slot - 1) / blocks_per_slot);
       nb = nb < 1 ? 1 : (nb > nb_max ? nb_max : nb);
+      if (fmt == FMT_Q4_0 && m > 1 && !fused && mode == KOMP_MODE_DP4A && nblk > blocks_per_slot * nb && nblk <= 256)
+        // two or three Q4_0 columns with q8 in whose rows this plan takes in two K steps but 64 lanes of nb 4 in
+        // one (a few blocks past 128: K = 4192): the one-column plan's shape, 8 waves of one row in one step
+        // (4097 x 4192, 3 columns 5.21 -> 4.58 us, 2 columns 4.68 -> 4.06; 6913 x 4192 6.58 -> 6.08).  Fused
+        // launches were slower so (8.8 -> 9.4 us), and IQ4_NL no faster.
+        return plan_of(8, pow2_ceil((nblk + 63) / 64), 8, 64, 1);
       // past 8 waves, two or three columns (and bytes mode) run this plan on the lean kernels only: the general kernel
       // takes at most 8 waves there
       const size_t lean_lds = fmt == FMT_TQ2_0 ? tq2_lean_lds_bytes(lpr, nb, static_cast<int>(m), static_cast<int>(k), fused,

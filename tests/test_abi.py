@@ -191,6 +191,15 @@ def test_auto_plan_q4_0_columns_llama_shapes(n, k, plan):
     assert _abi.auto_plan(0, 1, n, k, False)[2] == 8  # one unfused column keeps the 8-wave plan
 
 
+def test_auto_plan_q4_0_columns_one_k_step():
+    # 131 blocks a row (K 4192): the one-CU plan's 32 lanes x nb 4 would take two K steps, 64 lanes one; with q8 in,
+    # 2-3 columns take the one-column plan's shape, fused launches keep the wider plan
+    for n in (4097, 6913):
+        for m in (2, 3):
+            assert _abi.auto_plan(0, m, n, 4192, False) == (8, 4, 8, 64, 1)
+            assert _abi.auto_plan(0, m, n, 4192, True)[3] == 32
+
+
 def test_auto_plan_tq2_columns_few_rows_use_knob_sets():
     # 2-3 columns need at least 7 waves of the one-workgroup-per-CU plan; fewer rows take the 8-wave knob-set plans,
     # except three dp4a columns whose q8_K staging (16 threads per block and column) needs more than 8 waves: one
