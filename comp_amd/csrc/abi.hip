@@ -407,6 +407,7 @@ bool tq2_mfma_plan(int64_t m, int64_t n, int64_t k, int64_t sw, bool fused, Mfma
   waves = waves > 16 ? 16 : waves;
   const int64_t nbw = (nblk + waves - 1) / waves;
   if (nbw > 4 || 16 * sw > 0x7FFFFFF0 || 4 * k > 0x7FFFFFF0) return false;
+  if (sw < 64 * nblk || sw % 16 != 0) return false;  // its 16-byte weight loads need 16-byte aligned rows
   const int64_t even = (n + cus - 1) / cus;  // rows a CU: more than 8
   const int64_t rows = big ? 32 : (even < 16 ? even : 16);
   *p = MfmaPlan{big ? 2 : 1, static_cast<int>(waves), static_cast<int>(nbw), static_cast<int>(rows)};

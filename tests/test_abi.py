@@ -191,6 +191,16 @@ def test_auto_plan_q4_0_columns_llama_shapes(n, k, plan):
     assert _abi.auto_plan(0, 1, n, k, False)[2] == 8  # one unfused column keeps the 8-wave plan
 
 
+def test_mfma_plan_needs_aligned_rows():
+    # the three-column TQ2_0 matrix-core GEMV: 16-byte aligned row strides of at least the packed row, more than 8
+    # rows a CU (256 CUs when no device is visible)
+    assert _abi.gemv_mfma_plan(1, False, 2, 3, 6912, 2560, 640) is not None
+    assert _abi.gemv_mfma_plan(1, False, 2, 3, 6912, 2560, 704) is not None
+    assert _abi.gemv_mfma_plan(1, False, 2, 3, 6912, 2560, 648) is None
+    assert _abi.gemv_mfma_plan(1, False, 2, 3, 6912, 2560, 624) is None
+    assert _abi.gemv_mfma_plan(1, False, 2, 2, 6912, 2560, 640) is None
+
+
 def test_auto_plan_q4_0_columns_one_k_step():
     # 131 blocks a row (K 4192): the one-CU plan's 32 lanes x nb 4 would take two K steps, 64 lanes one; with q8 in,
     # 2-3 columns take the one-column plan's shape, fused launches keep the wider plan

@@ -78,6 +78,34 @@ def test_mfma_gemv_routing():
     assert host.mfma_plan("tq2_0", 3, 32768, 8192) == (32, 8)
 
 
+@pytest.mark.parametrize("pad", [16, 64])
+def test_mfma_gemv_padded_row_stride(pad):
+    # a weight plane with padded rows (the row stride is the tensor's): Y and S bit for bit the packed plane's, on the
+    # matrix cores; a stride that is not a multiple of 16 is refused by the entry point (and by the plan query)
+    n, k, m = 2560, 6912, 3
+    row = k // 4
+    sw = row + pad
+    print(f"tq2 mfma padded rows sw={sw}", flush=True)
+    W, x = O.problem("tq2_0", n, k, m, 77 + pad)
+    wq, ws = host.split("tq2_0", W, n, k)
+    wq_d, ws_d = dev(wq), dev(ws)
+    wide = torch.full((n, sw), 0xA5, dtype=torch.uint8, device="cuda")  # pad bytes never read
+    wide[:, :row] = wq_d
+    xq, xd = host.quantize("tq2_0", dev(x))
+    assert host.uses_mfma("tq2_0", m, n, k, sw=sw) and not host.uses_mfma("tq2_0", m, n, k, sw=row + 8)
+    y, s = host.gemv("tq2_0", wide, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    y0, s0 = host.gemv("tq2_0", wq_d, ws_d, xq, xd, n, k, None, 0, 2, 0, store_s=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s0) and torch.equal(y.view(torch.int32), y0.view(torch.int32))
+    rq, rd, _ = O.quantize("tq2_0", x)
+    r, rs = O.gemv("tq2_0", wq, ws, rq, rd, n, k)
+    assert np.array_equal(s.cpu().numpy().astype(np.int64), rs)
+    assert outputs_ok("tq2_0", y.cpu().numpy(), ws, rd, rs, r)
+    odd = torch.zeros((n, row + 8), dtype=torch.uint8, device="cuda")
+    with pytest.raises(_abi.KompArgumentError, match="multiple of 16"):
+        host.gemv("tq2_0", odd, ws_d, xq, xd, n, k, None, 0, 2, 0)
+
+
 def test_mfma_gemv_stamped_instantiation():
     # with the tuning harness's stamps on, the launch runs the stamped instantiation: the same Y and S, and one record
     # per wave whose phases are in order
