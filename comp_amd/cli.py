@@ -111,8 +111,9 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=Non
     holds them.  One column with nb < 8 whose waves walk 3 tiles or more (passes x K steps; k given) runs the
     pipelined loop form instead (q4_lean_pipe_kernel <format, lanes, nb, fused>, q4_lean_bytes_pipe_kernel <lanes, nb,
     fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>).  One or two tq2_0 dp4a columns in the single-pass form with
-    nb x columns <= 4, launched as at most one workgroup a CU (n given: ceil(n / block_n) <= 256, MI355X's CUs), run the
-    form that reads its LDS pieces ahead of the dots (tq2_lean_pre_kernel <lanes, nb, columns, fused, copy staging>).  A tq2_0 K step below 256 bytes a row
+    nb x columns <= 4 (or two columns at nb 4 in workgroups of at most 8 waves), launched as at most one workgroup a CU
+    (n given: ceil(n / block_n) <= 256, MI355X's CUs), run the form that reads its LDS pieces ahead of the dots
+    (tq2_lean_pre_kernel <lanes, nb, columns, fused, copy staging>).  A tq2_0 K step below 256 bytes a row
     (lanes x nb x 16) is widened to it (nb doubled up to 4), as the launch does."""
     cols = min(max(m, 1), 3)
     if fmt == "tq2_0" and block_n and num_warps:  # the launch widens a tq2_0 K step to 256 bytes a row
@@ -143,7 +144,8 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=Non
                 bstep = (lanes // 4) * nb
                 staged = cols * -(-(k // 256) // bstep) * bstep * 296
                 dma = (staged + 15) // 16 * 16 + cols * k + cols * (k // 256) * 4 <= 160 * 1024
-            if one and cols <= 2 and nb * cols <= 4 and n is not None and -(-n // block_n) <= 256:
+            pre_form = nb * cols <= 4 or (cols == 2 and nb == 4 and num_warps <= 8)
+            if one and cols <= 2 and pre_form and n is not None and -(-n // block_n) <= 256:
                 return f"gemv_tq2::tq2_lean_pre_kernel<{lanes}, {nb}, {cols}, false, {str(dma).lower()}>"
             return (f"gemv_tq2::tq2_lean_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}, "
                     f"{str(dma).lower()}>")

@@ -438,8 +438,8 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
     // PRE: every slot's activation pieces and every owned block's meta are read from LDS before the first dot (slots
     // past the row's end read the zero padding), so their latency overlaps the wait for the weights instead of
     // following it; at the price of 16 VGPRs a slot, so only for launches of at most a workgroup a CU, whose
-    // occupancy they do not cost
-    static_assert(!PRE || (!BYTES && NB * MC <= 4), "PRE: dp4a tiles of at most 4 slots x columns");
+    // occupancy they do not cost (5-8 slots x columns in workgroups of at most 8 waves: 512-thread bounds)
+    static_assert(!PRE || (!BYTES && NB * MC <= 8), "PRE: dp4a tiles of at most 8 slots x columns");
     u32x4 xpre[PRE ? NB : 1][PRE ? MC : 1][4];
     int2 mpre[PRE ? NOWN : 1][PRE ? MC : 1];
     if constexpr (PRE) {
@@ -572,14 +572,14 @@ __global__ void __launch_bounds__(1024) tq2_lean_kernel(KOMP_TQ2_LEAN_ARGS) {
 // The single-pass, single-step dp4a form of one column with every slot's LDS reads ahead of the dots (PRE above), for
 // launches of at most one workgroup a CU.
 template <int LPR, int NB, int MC, bool FUSED, bool DMA>
-__global__ void __launch_bounds__(1024) tq2_lean_pre_kernel(KOMP_TQ2_LEAN_ARGS) {
+__global__ void __launch_bounds__(NB * MC > 4 ? 512 : 1024) tq2_lean_pre_kernel(KOMP_TQ2_LEAN_ARGS) {
   tq2_lean_body<LPR, NB, MC, FUSED, true, DMA, false, false, false, true>(KOMP_TQ2_LEAN_PASS);
 }
 
 // The stamped single-pass, single-step dp4a form (STAMP above): the measurement instantiation of the tuning harness,
 // with or without the early LDS reads as the plain launch would run them.
 template <int LPR, int NB, int MC, bool FUSED, bool PRE>
-__global__ void __launch_bounds__(1024) tq2_lean_stamped_kernel(KOMP_TQ2_LEAN_ARGS) {
+__global__ void __launch_bounds__(PRE && NB * MC > 4 ? 512 : 1024) tq2_lean_stamped_kernel(KOMP_TQ2_LEAN_ARGS) {
   tq2_lean_body<LPR, NB, MC, FUSED, true, false, false, true, false, PRE>(KOMP_TQ2_LEAN_PASS);
 }
 
@@ -616,8 +616,8 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   // decode shapes of a few MB): their registers cost no occupancy there (BitNet-2B 6912 x 2560 fused: span 2.64 ->
   // 2.49 us), while the many-workgroup launches of large matrices lose waves a SIMD to them (TQ2_0 32768 x 8192:
   // 13.3 -> 15.3 us)
-  constexpr bool kPreForm = !BYTES && MC <= 2 && NB * MC <= 4;
-  const bool pre = kPreForm && one && groups <= device_cu_count();
+  constexpr bool kPreForm = !BYTES && (NB * MC <= 4 || (MC == 2 && NB == 4));
+  const bool pre = kPreForm && one && groups <= device_cu_count() && (NB * MC <= 4 || p.waves <= 8);
   if constexpr (STAMP) {
     if (BYTES || !one || tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) || c.segs.stamps == nullptr)
       return hipErrorInvalidConfiguration;

@@ -83,7 +83,8 @@ def test_single_pass_form_follows_the_launch(fmt, bn, nb, nw, k, m, name):
 
 
 def test_early_read_form_follows_the_grid():
-    """One or two tq2_0 dp4a columns in the single-pass form (nb x columns <= 4) run the early-LDS-read form when the
+    """One or two tq2_0 dp4a columns in the single-pass form (nb x columns <= 4, or 2 columns at nb 4 in at most 8
+    waves) run the early-LDS-read form when the
     launch has at most one workgroup a CU (N known), the plain form otherwise; both keep their registers."""
     pre = "gemv_tq2::tq2_lean_pre_kernel<16, 4, 1, false, false>"
     assert cli._gemv_kernel("tq2_0", 2, 4, 1, 16, 4, 2560, 4096) == pre  # 256 workgroups
@@ -91,8 +92,13 @@ def test_early_read_form_follows_the_grid():
     assert cli._gemv_kernel("tq2_0", 2, 4, 3, 16, 4, 2560, 300).startswith("gemv_tq2::tq2_lean_kernel<16, 4, 3,")
     # two columns at nb 2 (4 slots x columns): the early reads too, here with the columns copied global -> LDS
     assert cli._gemv_kernel("tq2_0", 2, 2, 2, 8, 8, 6912, 2048) == "gemv_tq2::tq2_lean_pre_kernel<64, 2, 2, false, true>"
-    r = isa.summary(pre, cli.VALUES_PER_LOAD["tq2_0"])
-    assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["loop"].get("dot4", 0) > 0
+    # two columns at nb 4 (8 slots x columns) in workgroups of at most 8 waves (512-thread bounds: 256 VGPRs a wave)
+    pre8 = "gemv_tq2::tq2_lean_pre_kernel<16, 4, 2, false, false>"
+    assert cli._gemv_kernel("tq2_0", 2, 4, 2, 32, 8, 2560, 6912) == pre8
+    assert cli._gemv_kernel("tq2_0", 2, 4, 2, 64, 16, 2560, 6912).startswith("gemv_tq2::tq2_lean_kernel<16, 4, 2,")
+    for name in (pre, pre8):
+        r = isa.summary(name, cli.VALUES_PER_LOAD["tq2_0"])
+        assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["loop"].get("dot4", 0) > 0
 
 
 @pytest.mark.parametrize("spec,fmt", [(SPEC_Q4, "q4_0"), (SPEC_TQ2, "tq2_0")])
