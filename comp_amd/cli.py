@@ -113,7 +113,8 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=Non
     fused>, tq2_lean_pipe_kernel <lanes, nb, fused, bytes>).  One or two tq2_0 dp4a columns in the single-pass form with
     nb x columns <= 4 (or two columns at nb 4 in workgroups of at most 8 waves), launched as at most one workgroup a CU
     (n given: ceil(n / block_n) <= 256, MI355X's CUs), run the form that reads its LDS pieces ahead of the dots
-    (tq2_lean_pre_kernel <lanes, nb, columns, fused, copy staging>).  A tq2_0 K step below 256 bytes a row
+    (tq2_lean_pre_kernel <lanes, nb, columns, fused, copy staging>; one bytes-mode column at nb <= 4 likewise:
+    tq2_lean_bytes_pre_kernel <lanes, nb, fused>).  A tq2_0 K step below 256 bytes a row
     (lanes x nb x 16) is widened to it (nb doubled up to 4), as the launch does."""
     cols = min(max(m, 1), 3)
     if fmt == "tq2_0" and block_n and num_warps:  # the launch widens a tq2_0 K step to 256 bytes a row
@@ -134,6 +135,9 @@ def _gemv_kernel(fmt, mode, nb, m=1, block_n=None, num_warps=None, k=None, n=Non
             if k is None or cols * -(-(k // 256) // bstep) * bstep * (2 * 288 + 8) <= 160 * 1024:
                 if pipe and not one:
                     return f"gemv_tq2::tq2_lean_pipe_kernel<{lanes}, {nb}, false, true>"
+                if (one and cols == 1 and nb <= 4 and (nb <= 2 or num_warps <= 8) and n is not None
+                        and -(-n // block_n) <= 256):
+                    return f"gemv_tq2::tq2_lean_bytes_pre_kernel<{lanes}, {nb}, false>"
                 return f"gemv_tq2::tq2_lean_bytes_kernel<{lanes}, {nb}, {cols}, false, {str(one).lower()}>"
         elif fmt == "tq2_0":
             one = one_pass and k // 256 <= (lanes // 4) * nb

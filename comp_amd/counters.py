@@ -22,7 +22,8 @@ import json
 import os
 
 # kernel families that make one GEMV / GEMM call (the quantizer and the copies of the weight rotation are not counted)
-FAMILIES = ("tq2_lean_kernel", "tq2_lean_pre_kernel", "tq2_lean_bytes_kernel", "q4_lean_kernel", "q4_lean_bytes_kernel",
+FAMILIES = ("tq2_lean_kernel", "tq2_lean_pre_kernel", "tq2_lean_bytes_kernel", "tq2_lean_bytes_pre_kernel",
+            "q4_lean_kernel", "q4_lean_bytes_kernel",
             "q8_lean_kernel", "q4k_lean_kernel", "tq2_mfma_kernel", "gemv_kernel", "gemm_kernel")
 
 

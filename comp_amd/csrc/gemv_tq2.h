@@ -439,8 +439,10 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
     // past the row's end read the zero padding), so their latency overlaps the wait for the weights instead of
     // following it; at the price of 16 VGPRs a slot, so only for launches of at most a workgroup a CU, whose
     // occupancy they do not cost (5-8 slots x columns in workgroups of at most 8 waves: 512-thread bounds)
-    static_assert(!PRE || (!BYTES && NB * MC <= 8), "PRE: dp4a tiles of at most 8 slots x columns");
+    // (bytes mode: both planes, 32 VGPRs a slot)
+    static_assert(!PRE || NB * MC * (BYTES ? 2 : 1) <= 8, "PRE: tiles of at most 8 slots x columns x planes");
     u32x4 xpre[PRE ? NB : 1][PRE ? MC : 1][4];
+    u32x4 xopre[PRE && BYTES ? NB : 1][PRE && BYTES ? MC : 1][4];
     int2 mpre[PRE ? NOWN : 1][PRE ? MC : 1];
     if constexpr (PRE) {
 #pragma unroll
@@ -448,8 +450,11 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
 #pragma unroll
         for (int m = 0; m < MC; ++m)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < 4; ++j) {
             xpre[u][m][j] = *reinterpret_cast<const u32x4*>(xl + (m * nblk_pad + tb + u * BPG) * XB + 32 * j);
+            if constexpr (BYTES)
+              xopre[u][m][j] = *reinterpret_cast<const u32x4*>(xl + (m * nblk_pad + tb + u * BPG) * XB + opl + 32 * j);
+          }
 #pragma unroll
       for (int i = 0; i < NOWN; ++i) {
         const int u = NB >= 4 ? 4 * i + q : (owner ? q : 0);
@@ -470,7 +475,7 @@ __device__ __forceinline__ void tq2_lean_body(int N1, int nblk, int SW1, int nse
         if constexpr (BYTES) {
           u32x4 xo[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) xo[j] = *reinterpret_cast<const u32x4*>(xp + opl + 32 * j);
+          for (int j = 0; j < 4; ++j) xo[j] = PRE ? xopre[u][m][j] : *reinterpret_cast<const u32x4*>(xp + opl + 32 * j);
           pd[m][u] = chunk_dot_bytes(wb[u], xv, xo);
         } else {
           pd[m][u] = chunk_dot16(wb[u], xv, km);
@@ -588,6 +593,13 @@ __global__ void __launch_bounds__(1024) tq2_lean_bytes_kernel(KOMP_TQ2_LEAN_ARGS
   tq2_lean_body<LPR, NB, MC, FUSED, ONE, false, true>(KOMP_TQ2_LEAN_PASS);
 }
 
+// The single-pass bytes-mode form of one column with both planes' LDS reads ahead of the dots (PRE above), for
+// launches of at most one workgroup a CU.
+template <int LPR, int NB, bool FUSED>
+__global__ void __launch_bounds__(NB * 2 > 4 ? 512 : 1024) tq2_lean_bytes_pre_kernel(KOMP_TQ2_LEAN_ARGS) {
+  tq2_lean_body<LPR, NB, 1, FUSED, true, false, true, false, false, true>(KOMP_TQ2_LEAN_PASS);
+}
+
 // The pipelined loop forms (PIPE above) of one column, dp4a and bytes mode.
 template <int LPR, int NB, bool FUSED, bool BYTES>
 __global__ void __launch_bounds__(1024) tq2_lean_pipe_kernel(KOMP_TQ2_LEAN_ARGS) {
@@ -616,8 +628,11 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
   // decode shapes of a few MB): their registers cost no occupancy there (BitNet-2B 6912 x 2560 fused: span 2.64 ->
   // 2.49 us), while the many-workgroup launches of large matrices lose waves a SIMD to them (TQ2_0 32768 x 8192:
   // 13.3 -> 15.3 us)
-  constexpr bool kPreForm = !BYTES && (NB * MC <= 4 || (MC == 2 && NB == 4));
-  const bool pre = kPreForm && one && groups <= device_cu_count() && (NB * MC <= 4 || p.waves <= 8);
+  // (bytes mode: one column, nb <= 4, both planes read early: 6912 x 2560 3.72 -> 3.49 us, f32 in 3.67 -> 3.48,
+  // 2560 x 6912 3.54 -> 3.48; but f32 in at nb 2, 2560 x 6912, 3.59 -> 3.67, so not there)
+  constexpr bool kPreForm = BYTES ? (MC == 1 && NB <= 4 && (!FUSED || NB == 4)) : (NB * MC <= 4 || (MC == 2 && NB == 4));
+  constexpr int kPreSlots = NB * MC * (BYTES ? 2 : 1);
+  const bool pre = kPreForm && one && groups <= device_cu_count() && (kPreSlots <= 4 || p.waves <= 8);
   if constexpr (STAMP) {
     if (BYTES || !one || tq2_lean_dma(LPR, NB, MC, c.k, FUSED, 64 * p.waves, false) || c.segs.stamps == nullptr)
       return hipErrorInvalidConfiguration;
@@ -629,6 +644,9 @@ hipError_t launch_k(const GemvCall& c, const GemvPlan& p, hipStream_t stream) {
     kern = one ? tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, true> : tq2_lean_bytes_kernel<LPR, NB, MC, FUSED, false>;
     if constexpr (MC == 1 && NB < 8) {
       if (pipe) kern = tq2_lean_pipe_kernel<LPR, NB, FUSED, true>;
+    }
+    if constexpr (kPreForm) {
+      if (pre) kern = tq2_lean_bytes_pre_kernel<LPR, NB, FUSED>;
     }
   } else {
     kern = one ? tq2_lean_kernel<LPR, NB, MC, FUSED, true, false> : tq2_lean_kernel<LPR, NB, MC, FUSED, false, false>;

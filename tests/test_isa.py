@@ -22,7 +22,7 @@ def run(*args):
 def test_library_holds_gfx950_code_objects_with_every_kernel_family():
     names = [n for co in isa.library_code_objects() for n in co.kernels]
     for family in ("gemv_impl::gemv_kernel<", "gemv_tq2::tq2_lean_kernel<", "gemv_tq2::tq2_lean_bytes_kernel<",
-                   "gemv_tq2::tq2_lean_pre_kernel<", "gemv_tq2_mfma::tq2_mfma_kernel<",
+                   "gemv_tq2::tq2_lean_pre_kernel<", "gemv_tq2::tq2_lean_bytes_pre_kernel<", "gemv_tq2_mfma::tq2_mfma_kernel<",
                    "gemv_q4::q4_lean_kernel<", "gemv_q4k::q4k_lean_kernel<", "gemv_q8::q8_lean_kernel<",
                    "gemm_impl::gemm_kernel<", "quant_q8_0_kernel", "quant_q8_K_kernel", "stream_read_kernel",
                    "split_impl::split_kernel"):
@@ -99,6 +99,12 @@ def test_early_read_form_follows_the_grid():
     for name in (pre, pre8):
         r = isa.summary(name, cli.VALUES_PER_LOAD["tq2_0"])
         assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["loop"].get("dot4", 0) > 0
+    # bytes mode, one column at nb <= 4: both staged planes read early (no dot instruction)
+    pre_b = "gemv_tq2::tq2_lean_bytes_pre_kernel<16, 4, false>"
+    assert cli._gemv_kernel("tq2_0", 0, 4, 1, 16, 4, 2560, 4096) == pre_b
+    assert cli._gemv_kernel("tq2_0", 0, 4, 1, 16, 4, 2560, 6912).startswith("gemv_tq2::tq2_lean_bytes_kernel<16, 4, 1,")
+    r = isa.summary(pre_b, cli.VALUES_PER_LOAD["tq2_0"])
+    assert r["vgpr_spill"] == 0 and r["sgpr_spill"] == 0 and r["dot4_total"] == 0
 
 
 @pytest.mark.parametrize("spec,fmt", [(SPEC_Q4, "q4_0"), (SPEC_TQ2, "tq2_0")])
