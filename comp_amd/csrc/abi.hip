@@ -186,6 +186,14 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       waves = stage_waves;
       wg_rows = waves * rpp;  // fewer, fuller workgroups
     }
+    // One TQ2_0 column over few rows a CU: as many waves as one staging pass takes, each with its full rows (fewer,
+    // fuller workgroups) instead of one wave staging in several passes: 127 x 2816 2.81 -> 2.16 us (f32 in 3.30 ->
+    // 2.17, bytes 3.23 -> 2.50), 127 x 6912 3.46 -> 2.28 (f32 in 4.96 -> 2.52), 300 x 2560 2.79 -> 2.21, 2048 x
+    // 2560 2.63 -> 2.34 (f32 in 2.88 -> 2.31)
+    if (fmt == FMT_TQ2_0 && m == 1 && stage_waves > waves && stage_waves <= 16) {
+      waves = stage_waves;
+      wg_rows = waves * rpp;
+    }
     // two or three columns only with two waves on most SIMDs: with fewer, the 8-wave plans below, two workgroups
     // a CU, stage and dot faster (TQ2_0 4097 x 2816, 3 columns: 4.16 against 4.32 us; 127 x 2816: 3.0 against 4.8).
     // Q4_0 at Llama-3-8B shapes, 2-3 columns: 8-36% faster than those plans, the fused launches most (4096 x 14336,

@@ -201,6 +201,16 @@ def test_mfma_plan_needs_aligned_rows():
     assert _abi.gemv_mfma_plan(1, False, 2, 2, 6912, 2560, 640) is None
 
 
+def test_auto_plan_tq2_one_column_stages_in_one_pass():
+    # one TQ2_0 column over few rows a CU: as many waves as one staging pass of 16 threads a block takes, each with
+    # its full rows; fused, q8 in and bytes mode alike; the BitNet-2B plans already have the waves
+    for fused in (False, True):
+        for mode in (2, 0):
+            assert _abi.auto_plan(1, 1, 127, 2816, fused, mode) == (12, 4, 3, 16, 1)  # 11 blocks: 176 threads
+            assert _abi.auto_plan(1, 1, 127, 6912, fused, mode) == (7, 2, 7, 64, 1)  # 27 blocks: 432 threads
+            assert _abi.auto_plan(1, 1, 6912, 2560, fused, mode) == (27, 4, 7, 16, 1)
+
+
 def test_auto_plan_q4_0_columns_one_k_step():
     # 131 blocks a row (K 4192): the one-CU plan's 32 lanes x nb 4 would take two K steps, 64 lanes one; with q8 in,
     # 2-3 columns take the one-column plan's shape, fused launches keep the wider plan
