@@ -195,9 +195,9 @@ int komp_gemm_plan(int fmt, int64_t M, int64_t N, int64_t K, int64_t SW, int* ro
                    int* waves);
 
 /* Whether komp_tq2_0_gemv with block_n == 0 runs the matrix-core GEMV for this call (fused 0 / 1, mode as the GEMVs):
- * TQ2_0, KOMP_MODE_DP4A, 3 columns, rows of at most 64 blocks, q8_K activations in (f32 in: from 4 row tiles a CU
- * on).  Returns 1 and its
- * workgroup's rows and waves when it does, 0 (and zeros) when the call runs on the GEMV kernels, KOMP_EINVAL on a bad
+ * TQ2_0, KOMP_MODE_DP4A, 3 columns, more than 8 rows a CU, rows of at most 64 blocks, SW a multiple of 16, q8_K
+ * activations in (f32 in: from 4 row tiles a CU on).  Returns 1 and its workgroup's rows (spread evenly over the
+ * CUs, at most 16, or 32 in two tiles) and waves when it does, 0 (and zeros) when the call runs on the GEMV kernels, KOMP_EINVAL on a bad
  * argument.  That kernel computes S bit-identical to the GEMVs' and Y to f32 rounding (its f32 sums run in another
  * order): the activations are the A operand of v_mfma_i32_16x16x64_i8 and 16 weight rows its B operand, so the VALU
  * work per weight does not grow with the columns.
