@@ -568,7 +568,7 @@ int gemv_entry(int fmt, bool fused, const char* name, const GemvArgs& a, int64_t
     // The knobs fix each wave's rows (block_n / num_warps), lanes per row and nb, and with them every output bit: a
     // program's waves share no rows.  How the waves group into workgroups is the launch's: when the programs hold no
     // more waves than the device has CUs, each wave runs as a workgroup of its own, so the programs' rows spread over
-    // every CU instead of block_n / num_warps of them (Q4_0 4096 x 4096 at 64/4/4: 64 workgroups of 4 waves 7.45 us,
+    // a CU a wave instead of a CU a program (Q4_0 4096 x 4096 at 64/4/4: 64 workgroups of 4 waves 7.45 us,
     // 256 of one 6.25; 4096 x 14336 22.0 -> 17.0; 128/4/8 12.4 -> 6.3; IQ4_NL 8.55 -> 8.15).  Unfused Q4_0 / IQ4_NL
     // columns on the lean kernel only: a fused launch's workgroups each quantize all of K, which one wave does slower
     // (8.7 -> 10.5 us), and TQ2_0's each stage all of K (2560 x 6912 at 64/1/4: 7.45 -> 7.52, bytes 10.3 -> 10.8).
