@@ -186,13 +186,21 @@ GemvPlan auto_plan(int fmt, bool fused, int mode, int64_t m, int64_t n, int64_t 
       waves = stage_waves;
       wg_rows = waves * rpp;  // fewer, fuller workgroups
     }
-    // One TQ2_0 column over few rows a CU: as many waves as one staging pass takes, each with its full rows (fewer,
-    // fuller workgroups) instead of one wave staging in several passes: 127 x 2816 2.81 -> 2.16 us (f32 in 3.30 ->
-    // 2.17, bytes 3.23 -> 2.50), 127 x 6912 3.46 -> 2.28 (f32 in 4.96 -> 2.52), 300 x 2560 2.79 -> 2.21, 2048 x
-    // 2560 2.63 -> 2.34 (f32 in 2.88 -> 2.31)
-    if (fmt == FMT_TQ2_0 && m == 1 && stage_waves > waves && stage_waves <= 16) {
-      waves = stage_waves;
-      wg_rows = waves * rpp;
+    // One column over few rows a CU (at most 8 waves of them), TQ2_0 or f32 in: as many waves as one staging pass
+    // takes (16 threads a block of q8_K activations, 8 a block of q8_0 ones; at most 16), each with its full rows
+    // (fewer, fuller workgroups), instead of one wave staging in several passes.  TQ2_0: 127 x 2816 2.81 -> 2.16 us
+    // (f32 in 3.30 -> 2.17, bytes 3.23 -> 2.50), 127 x 6912 3.46 -> 2.28 (f32 in 4.96 -> 2.52), 300 x 2560 2.79 ->
+    // 2.21, 2048 x 2560 2.63 -> 2.34 (f32 in 2.88 -> 2.31).  f32 in: Q4_0 127 x 4192 7.12 -> 3.36, 300 x 4096 4.31 ->
+    // 2.53, 1000 x 4096 3.33 -> 2.62, 2048 x 4096 3.29 -> 2.87; IQ4_NL 127 x 4096 6.35 -> 2.93; Q8_0 6.27 -> 3.20;
+    // Q4_K 4.11 -> 2.59.  The Llama-3-8B plans (4096-6144 rows: 9-16 waves) keep theirs.
+    if (m == 1 && (fmt == FMT_TQ2_0 || fused) && waves <= 8) {
+      const int per_block = (fmt == FMT_TQ2_0 || fmt == FMT_Q4_K) ? 16 : 8;
+      int64_t one_pass = (nblk * per_block + 63) / 64;
+      one_pass = one_pass < 16 ? one_pass : 16;
+      if (one_pass > waves) {
+        waves = one_pass;
+        wg_rows = waves * rpp;
+      }
     }
     // two or three columns only with two waves on most SIMDs: with fewer, the 8-wave plans below, two workgroups
     // a CU, stage and dot faster (TQ2_0 4097 x 2816, 3 columns: 4.16 against 4.32 us; 127 x 2816: 3.0 against 4.8).

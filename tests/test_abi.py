@@ -211,6 +211,16 @@ def test_auto_plan_tq2_one_column_stages_in_one_pass():
             assert _abi.auto_plan(1, 1, 6912, 2560, fused, mode) == (27, 4, 7, 16, 1)
 
 
+def test_auto_plan_fused_one_column_stages_in_one_pass():
+    # one f32 column over few rows a CU: 8 staging threads a block of q8_0 activations, 16 of q8_K ones, as many
+    # waves as one pass takes (at most 16), each with its full rows; the Llama-3-8B plans keep theirs
+    assert _abi.auto_plan(0, 1, 300, 4096, True) == (16, 2, 16, 64, 1)  # 128 blocks x 8 threads
+    assert _abi.auto_plan(2, 1, 127, 4096, True) == (16, 4, 16, 64, 1)
+    assert _abi.auto_plan(4, 1, 127, 4096, True) == (8, 2, 4, 32, 1)  # q4_k: 16 blocks x 16 threads
+    assert _abi.auto_plan(0, 1, 4097, 4096, True) == (17, 4, 9, 32, 1)
+    assert _abi.auto_plan(0, 1, 6144, 4096, True) == (24, 4, 12, 32, 1)
+
+
 def test_auto_plan_q4_0_columns_one_k_step():
     # 131 blocks a row (K 4192): the one-CU plan's 32 lanes x nb 4 would take two K steps, 64 lanes one; with q8 in,
     # 2-3 columns take the one-column plan's shape, fused launches keep the wider plan

@@ -21,7 +21,9 @@ CASES = [("q4_0", 37, 416, 3), ("q4_0", 4097, 4192, 1), ("q4_0", 64, 512, 4), ("
          ("tq2_0", 6913, 2816, 2), ("tq2_0", 5, 1280, 1), ("q8_0", 37, 416, 3), ("q8_0", 4097, 4192, 1),
          ("iq4_nl", 37, 416, 3), ("iq4_nl", 4097, 4192, 1), ("iq4_nl", 64, 512, 4), ("q4_k", 37, 768, 3),
          ("q4_k", 4097, 4352, 1), ("q4_k", 64, 1024, 4),
-         ("tq2_0", 2048, 2816, 3), ("tq2_0", 1000, 4096, 3)]  # 3 columns over few rows: 9 and 12 waves of one row  # fmt: skip
+         ("tq2_0", 2048, 2816, 3), ("tq2_0", 1000, 4096, 3),  # 3 columns over few rows: 9 and 12 waves of one row
+         ("q4_0", 300, 4096, 1), ("q8_0", 127, 4096, 1), ("iq4_nl", 127, 4096, 1), ("q4_k", 127, 4096, 1)]  # fmt: skip
+# (the last four: one f32 column over few rows a CU, staged in one pass by 16 or 4 waves)
 
 
 @pytest.mark.parametrize("fmt,n,k,m", CASES)
