@@ -307,3 +307,24 @@ def test_stream_read_probe_reads_every_byte(nbytes):
     pieces[: data.size] = data
     per_wave = np.bitwise_xor.reduce(pieces.reshape(grid, 4, 8, 64 * 4), axis=(1, 3)).reshape(-1)
     assert np.array_equal(words, per_wave)
+
+
+@pytest.mark.parametrize("fmt,n,k", [("tq2_0", 127, 65536), ("tq2_0", 1000, 32768), ("q4_0", 127, 32768),
+                                     ("q8_0", 127, 32768), ("iq4_nl", 127, 32768), ("q4_k", 127, 32768)])  # fmt: skip
+def test_few_rows_long_columns(fmt, n, k):
+    # one column over few rows a CU with rows of 128-256 blocks: the plans that stage in one pass of up to 16 waves
+    # (several K steps a row), q8 and f32 in, dp4a and (Q4_0, TQ2_0) bytes mode, against the oracle
+    print(f"few rows long columns {fmt} {n}x{k}", flush=True)
+    W, x = O.problem(fmt, n, k, 1, 77)
+    wq, ws = host.split(fmt, W, n, k)
+    wq_d, ws_d = dev(wq), dev(ws)
+    rq, rd, _ = O.quantize(fmt, x)
+    r, rs = O.gemv(fmt, wq, ws, rq, rd, n, k)
+    xq, xd, *_ = host.quantize(fmt, dev(x))
+    for mode in (2, 0) if fmt in ("q4_0", "tq2_0") else (2,):
+        y, s = host.gemv(fmt, wq_d, ws_d, xq, xd, n, k, None, 0, mode, 0, store_s=True)
+        yf, sf = host.gemv_f32(fmt, wq_d, ws_d, dev(x), n, k, None, 0, mode, 0, store_s=True)
+        torch.cuda.synchronize()
+        for yy, ss in ((y, s), (yf, sf)):
+            assert np.array_equal(ss.cpu().numpy().astype(np.int64), rs)
+            assert outputs_ok(fmt, yy.cpu().numpy(), ws, rd, rs, r)
